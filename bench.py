@@ -1,0 +1,291 @@
+#!/usr/bin/env python
+"""PISA 64K prefill on one MI355X: block selection + sparse attention forward.
+
+    python bench.py [--gpus 1] [--steps 5] [--warmup 2] [--config 2] [--no-cpu-baseline]
+
+One step = the hot path over one batch of synthetic input already resident in
+HBM: ``select_blocks`` (pyramid build, coarse LSE/second-order routing, grouped
+leaf scoring, final top-K) followed by ``sparse_attention_with_lse`` (O and LSE).
+Prints ONE JSON line.  ``value`` is the selection latency (ms, lower is better),
+the first number of the metric; the sparse-attention TFLOP/s and the roofline
+fractions sit beside it.  The ``roofline`` object describes the kernel with the
+largest share of the step, timed by HIP events recorded on its own stream
+(``nlogn_pisa_amd._lib.profile_begin/end``).  ``cpu_baseline`` times the NumPy
+oracle (the reference's Torch equations restated) on a bounded token sample of
+the same workload on this host's cores, extrapolated to the full sequence.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK = 8.0e12          # bytes/s, MI355X HBM3E
+MFMA_PEAK = {"bf16": 2.5e15, "fp16": 2.5e15, "fp32": 157.3e12}
+TILE = 256                 # requests per bucketed tile (csrc/pisa_capi.hip)
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--config", type=int, default=2)
+    ap.add_argument("--tokens", type=int, default=None, help="config 4 length")
+    ap.add_argument("--cpu-sample", type=int, default=384, help="oracle tokens timed on the CPU")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+# ---------------------------------------------------------------- work counts
+
+def selection_counts(P, w, q, k, positions):
+    """Exact scoreable request counts per level (from the per-level selections)."""
+    import torch
+    ids, trace = P.selection.select_blocks_traced(
+        q, k, w.method, w.block_size, w.topk, force_first=w.force_first,
+        force_recent=w.force_recent, branching=w.branching)
+    blocks = math.ceil(w.keys / w.block_size)
+    top, first = P.routing_geometry(blocks, w.topk, w.branching)
+    _, lengths = P.pooling.pyramid_layout(w.keys, w.block_size, w.branching, top)
+    lengths = lengths + [lengths[-1]] * (top + 1 - len(lengths))
+    pos = positions[..., None, None].expand(w.batch, w.tokens, w.key_heads, 1)
+    leaf = pos // w.block_size
+    counts, tiles = {}, 0
+    b = w.branching
+    for j, level in enumerate(range(top, -1, -1)):
+        if level == top:
+            cand = torch.arange(first, device=q.device).expand(w.batch, w.tokens, w.key_heads, first)
+        else:
+            sel = trace[..., j - 1, :].long()
+            cand = (sel[..., None] * b + torch.arange(b, device=q.device)).flatten(-2)
+            cand = torch.where(sel.repeat_interleave(b, -1) < 0, -1, cand)
+        cand = torch.where(cand >= lengths[level], -1, cand)
+        span = b ** level
+        valid = (cand >= 0) & (cand * (w.block_size * span) <= pos)
+        forced = valid & (cand == 0) if w.force_first else torch.zeros_like(valid)
+        for r in range(w.force_recent):
+            target = leaf - r
+            forced |= valid & (target >= 0) & (cand == torch.div(target.clamp(min=0), span,
+                                                                  rounding_mode="floor"))
+        scoreable = valid & ~forced
+        if w.method != "pisa1":
+            scoreable &= (valid.sum(-1, keepdim=True) > w.topk)
+        counts[level] = int(scoreable.sum())
+        if level == 0 and w.method != "pisa1":
+            heads = torch.arange(w.key_heads, device=q.device)[None, None, :, None]
+            batches = torch.arange(w.batch, device=q.device)[:, None, None, None]
+            group = ((batches * w.key_heads + heads) * blocks + cand)[scoreable]
+            per = torch.bincount(group, minlength=w.batch * w.key_heads * blocks)
+            tiles = int(((per + TILE - 1) // TILE).sum())
+    return ids, counts, tiles, top, first
+
+
+def attention_counts(w, ids, positions):
+    """(requests, tiles, visible (row, key) pairs per KV head) of the attention step."""
+    import torch
+    blocks = math.ceil(w.keys / w.block_size)
+    pos = positions[..., None, None]
+    vis = (ids >= 0) & (ids < blocks) & (ids * w.block_size <= pos)
+    start = ids * w.block_size
+    keys = torch.minimum(torch.minimum(torch.full_like(ids, w.block_size), w.keys - start),
+                         pos - start + 1).clamp(min=0)
+    pairs = int(torch.where(vis, keys, 0).sum())
+    heads = torch.arange(w.key_heads, device=ids.device)[None, None, :, None]
+    batches = torch.arange(w.batch, device=ids.device)[:, None, None, None]
+    group = ((batches * w.key_heads + heads) * blocks + ids)[vis]
+    per = torch.bincount(group, minlength=w.batch * w.key_heads * blocks)
+    tiles = int(((per + TILE - 1) // TILE).sum())
+    return int(vis.sum()), tiles, pairs
+
+
+# ---------------------------------------------------------------- CPU baseline
+
+def cpu_baseline(w, q, k, sample):
+    """Time the NumPy oracle on ``sample`` tokens (full pyramid) and extrapolate."""
+    import numpy as np
+    import oracle as O
+    dtype = {"torch.bfloat16": "bf16", "torch.float16": "fp16", "torch.float32": "fp32"}[str(w.dtype)]
+    qn = q.float().cpu().numpy()
+    kn = k.float().cpu().numpy()
+    positions = O.query_positions(w.batch, w.tokens, w.keys)
+    tokens = np.unique(np.linspace(0, w.tokens - 1, sample).astype(np.int64))
+    t0 = time.perf_counter()
+    levels = O.build_pyramid(kn, w.block_size, w.branching, None, dtype)
+    t1 = time.perf_counter()
+    O.pyramid_select(qn, kn, w.method, w.block_size, w.topk, positions, w.force_first,
+                     w.force_recent, levels, branching=w.branching, tokens=tokens)
+    t2 = time.perf_counter()
+    per_token = (t2 - t1) / len(tokens)
+    total_ms = 1e3 * ((t1 - t0) + per_token * w.tokens)
+    threads = os.cpu_count()
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max(int(x.get("num_threads", 1)) for x in threadpool_info()) or threads
+    except Exception:
+        pass
+    return {"value": round(total_ms, 1), "unit": "ms", "cores": int(threads), "kind": "port",
+            "sample": (f"oracle (NumPy restatement of the Torch path) selection on {len(tokens)} "
+                       f"evenly spaced of {w.tokens} query tokens with the full pyramid "
+                       f"({1e3 * (t1 - t0):.0f} ms pyramid + {1e3 * per_token:.2f} ms/token), "
+                       f"extrapolated to all tokens")}
+
+
+# ---------------------------------------------------------------- main
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on exactly one GPU (this build has no multi-GPU path); "
+              f"got --gpus {args.gpus}", file=sys.stderr)
+        return 2
+    import torch
+    import nlogn_pisa_amd as P
+    from nlogn_pisa_amd import _lib
+    from nlogn_pisa_amd.inputs import config, make_inputs
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+    _lib.library()
+    w = config(args.config, args.tokens)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    print(f"[bench] generating {w.name}", file=sys.stderr, flush=True)
+    q, k, v = make_inputs(w, dev)[:3]
+    positions = P.query_positions(q, k)
+    dname = {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[w.dtype]
+
+    def select():
+        return P.select_blocks(q, k, method=w.method, block_size=w.block_size, topk=w.topk,
+                               force_first=w.force_first, force_recent=w.force_recent,
+                               backend="auto", branching=w.branching)
+
+    def attend(ids):
+        return P.sparse_attention_with_lse(q, k, v, ids, block_size=w.block_size)
+
+    with torch.no_grad():
+        print("[bench] warmup", file=sys.stderr, flush=True)
+        for _ in range(args.warmup):
+            attend(select())
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        marks = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+        print("[bench] timed steps", file=sys.stderr, flush=True)
+        torch.cuda.synchronize()
+        wall0 = time.perf_counter()
+        for m in marks:
+            m[0].record(stream)
+            ids = select()
+            m[1].record(stream)
+            attend(ids)
+            m[2].record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - wall0
+        sel_ms = sum(m[0].elapsed_time(m[1]) for m in marks) / args.steps
+        att_ms = sum(m[1].elapsed_time(m[2]) for m in marks) / args.steps
+        step_ms = sel_ms + att_ms
+
+        print("[bench] kernel timing", file=sys.stderr, flush=True)
+        _lib.profile_begin()
+        for _ in range(2):
+            attend(select())
+        kernels = _lib.profile_end()
+        per_step = {name: total / 2 for name, (n, total) in kernels.items()}
+        launches = {name: n / 2 for name, (n, total) in kernels.items()}
+
+        print("[bench] work counts", file=sys.stderr, flush=True)
+        ids, counts, leaf_tiles, top, first = selection_counts(P, w, q, k, positions)
+        requests, attn_tiles, pairs = attention_counts(w, ids, positions)
+
+    e = q.element_size()
+    G = w.query_heads // w.key_heads
+    D = w.head_dim
+    items = w.batch * w.tokens * w.key_heads
+    width = first if top == 0 else w.branching * w.topk
+    r_leaf = counts.get(0, 0)
+    r_int = sum(v for lvl, v in counts.items() if lvl > 0)
+    # algorithmic bytes / flops per launch of each hot kernel
+    algo = {
+        "route": {"bound": "hbm",
+                  "bytes": w.batch * w.tokens * w.query_heads * D * e + r_int * w.branching * D * e
+                  + items * width * 5},
+        "leaf": {"bound": "hbm",
+                 "bytes": leaf_tiles * w.block_size * D * e + r_leaf * (G * D * e + 8),
+                 "flops": 2 * r_leaf * w.block_size * D * G},
+        "final": {"bound": "hbm", "bytes": items * (width * 9 + w.topk * 8)},
+        "attn_fwd": {"bound": "hbm",
+                     "bytes": attn_tiles * 2 * w.block_size * D * e
+                     + requests * G * (D * e + (D + 2) * 4),
+                     "flops": 4 * D * G * pairs},
+        "attn_combine": {"bound": "hbm",
+                         "bytes": requests * G * (D + 2) * 4 + items * G * (D * e + 4)},
+        "pool": {"bound": "hbm", "bytes": w.batch * w.keys * w.key_heads * D * e},
+    }
+    dominant = max(per_step, key=per_step.get)
+    dom_ms = per_step[dominant] / max(launches[dominant], 1)
+    info = algo.get(dominant, {"bound": "hbm", "bytes": 0})
+    achieved = info["bytes"] / (dom_ms * 1e-3)
+    roofline = {"kernel": dominant, "bound": "hbm", "achieved": round(achieved / 1e9, 1),
+                "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4),
+                "traffic": None, "avg_launch_ms": round(dom_ms, 4),
+                "algorithmic_bytes": int(info["bytes"])}
+
+    attn_flops = 4 * D * G * pairs
+    attn_kernel_ms = per_step.get("attn_fwd", 0) + per_step.get("attn_combine", 0)
+    leaf_ms = per_step.get("leaf", 0)
+    sel_kernels = ["pool", "route", "fill", "bucket_count", "bucket_scan", "bucket_scatter",
+                   "leaf", "final"]
+    sel_bytes = sum(algo[n]["bytes"] for n in ("pool", "route", "leaf", "final"))
+    result = {
+        "metric": "selection ms + sparse-attn TFLOP/s at 64K prefill; % HBM / % MFMA peak",
+        "value": round(sel_ms, 3),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 3),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dname,
+        "data": "synthetic (seeded q,k,v; k with per-64-token offsets and 1% needle blocks)",
+        "config": {"workload": w.name, "batch": w.batch, "tokens": w.tokens,
+                   "query_heads": w.query_heads, "kv_heads": w.key_heads, "head_dim": D,
+                   "block_size": w.block_size, "branching": w.branching, "topk": w.topk,
+                   "method": w.method, "forced": f"first + {w.force_recent} recent",
+                   "step": "select_blocks + sparse_attention forward (O, LSE)"},
+        "selection_ms": round(sel_ms, 3),
+        "sparse_attn_ms": round(att_ms, 3),
+        "sparse_attn_tflops": round(attn_flops / (att_ms * 1e-3) / 1e12, 2),
+        "sparse_attn_mfma_frac": round(attn_flops / (att_ms * 1e-3) / MFMA_PEAK[dname], 4),
+        "selection_hbm_frac": round(sel_bytes / (sel_ms * 1e-3) / HBM_PEAK, 4),
+        "leaf_hbm_frac": round(algo["leaf"]["bytes"] / (leaf_ms * 1e-3) / HBM_PEAK, 4)
+        if leaf_ms else None,
+        "kernel_ms_per_step": {n: round(t, 4) for n, t in sorted(per_step.items(),
+                                                                  key=lambda x: -x[1])},
+        "work": {"route_requests": r_int, "leaf_requests": r_leaf, "leaf_tiles": leaf_tiles,
+                 "attn_requests": requests, "attn_tiles": attn_tiles, "attn_pairs": pairs,
+                 "attn_flops": attn_flops, "top": top, "first_width": first},
+        "roofline": roofline,
+        "wall_s_timed": round(wall, 3),
+    }
+    del sel_kernels
+    if not args.no_cpu_baseline:
+        print("[bench] cpu baseline", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline(w, q, k, args.cpu_sample)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,737 @@
+// Sparse attention over selected blocks (kernel 5) and decode attention
+// (kernel 4, attention half), forward and backward, on MFMA tiles.
+//
+// Equations: sparse_attn_torch.py:6-35 - each (batch, token, kv head) row
+// attends the keys of its K selected blocks (slots), masked to the sequence
+// and, when causal, to keys <= its position; rows without a visible key
+// output 0.  LSE (natural log) is returned for the backward pass.
+//
+// Forward.  A request is one visible slot.  Requests are bucketed by
+// (batch, kv head, block) (pisa_group.hip) so a workgroup loads a K/V block
+// once for up to `tile` requests; its waves sweep 16-row MFMA units (row =
+// request x query head): S = Q K^T, row max/sum, P V.  Each request leaves a
+// partial (m, l, o = sum_j exp(s_j - m) v_j) per head; the combine kernel
+// merges a row's K partials in slot order: O = sum e^(m_s-M) o_s / L,
+// LSE = M + ln L.  With few queries per key (decode) the direct kernel runs one
+// request per wavefront and writes the same partials.
+//
+// Backward (P = exp(s*S - LSE), dS = P (dP - rowsum(dO O))).  Block-major
+// too: wave w of a workgroup owns keys [16w, 16w+16) of the tile's block and
+// accumulates their dK/dV over all of the tile's requests in registers
+// (written once per tile, reduced per block in tile order); dQ of each request
+// is split across the waves by head-dim tiles and written as a partial per
+// slot, summed per row in slot order.
+
+#include "pisa_device.h"
+#include "pisa_internal.h"
+
+namespace pisa {
+
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+template <typename I>
+__device__ __forceinline__ int64_t load_index(const void* p, int64_t i) {
+  return (int64_t) static_cast<const I*>(p)[i];
+}
+
+__device__ __forceinline__ int64_t slot_block(const AttnArgs& a, int64_t slot) {
+  return a.index_bits == 64 ? load_index<int64_t>(a.indices, slot)
+                            : load_index<int32_t>(a.indices, slot);
+}
+
+// A slot is a request iff its block exists and (causal) starts at or before the
+// row's position - exactly the rows bucketed by AttnSrc in pisa_group.hip.
+__device__ __forceinline__ bool slot_visible(const AttnArgs& a, int64_t blk, int64_t pos) {
+  return blk >= 0 && blk < a.M0 && (!a.causal || blk * a.C <= pos);
+}
+
+// Row bookkeeping of one request slot.
+struct RowInfo {
+  int64_t slot;
+  int b, t, h;
+  int64_t pos;
+};
+
+__device__ __forceinline__ RowInfo row_info(const AttnArgs& a, int64_t slot) {
+  RowInfo r;
+  r.slot = slot;
+  const int64_t item = slot / a.K;
+  r.h = (int)(item % a.Hkv);
+  const int64_t bt = item / a.Hkv;
+  r.t = (int)(bt % a.T);
+  r.b = (int)(bt / a.T);
+  r.pos = a.positions[(int64_t)r.b * a.pos_batch + r.t];
+  return r;
+}
+
+// ------------------------------------------------------------------ forward
+
+// Stage the K block row-major (ks[key][d]) and the V block transposed
+// (vt[d][key]); keys >= rows are zero.
+template <typename T>
+__device__ void stage_kv(const AttnArgs& a, int b, int h, int64_t blk, int rows, T* ks, int ldk,
+                         T* vt, int ldv, int Cp, int tid, int nthr) {
+  const int vec = 16 / (int)sizeof(T);
+  const T* kb = static_cast<const T*>(a.k) + (int64_t)b * a.k_batch + blk * a.C * a.k_token +
+                (int64_t)h * a.D;
+  const T* vb = static_cast<const T*>(a.v) + (int64_t)b * a.v_batch + blk * a.C * a.v_token +
+                (int64_t)h * a.Dv;
+  const int kv_vecs = a.D / vec;
+  for (int idx = tid; idx < Cp * kv_vecs; idx += nthr) {
+    const int r = idx / kv_vecs, c = (idx % kv_vecs) * vec;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (r < rows) v = *reinterpret_cast<const uint4*>(kb + (int64_t)r * a.k_token + c);
+    *reinterpret_cast<uint4*>(ks + r * ldk + c) = v;
+  }
+  const int v_vecs = a.Dv / vec;
+  for (int idx = tid; idx < Cp * v_vecs; idx += nthr) {
+    const int r = idx / v_vecs, c = (idx % v_vecs) * vec;
+    union {
+      uint4 u;
+      T e[16 / sizeof(T)];
+    } v;
+    v.u = make_uint4(0, 0, 0, 0);
+    if (r < rows) v.u = *reinterpret_cast<const uint4*>(vb + (int64_t)r * a.v_token + c);
+#pragma unroll
+    for (int e = 0; e < (int)(16 / sizeof(T)); ++e) vt[(c + e) * ldv + r] = v.e[e];
+  }
+}
+
+// One 16-row unit: rows unit*16 .. +15 of the request list (row = request x Gp + head).
+// P enters the P V product as a pair of 16-bit values hi + lo (lo = P - hi),
+// so the product keeps ~16 significant bits of P; fp32 needs no split.
+template <typename T>
+constexpr bool kSplit = sizeof(T) == 2;
+
+template <typename T, typename ReqFn>
+__device__ void fwd_unit(const AttnArgs& a, ReqFn req_slot, int nreq, int unit, int b, int h,
+                         int64_t blk, int rows, const T* ks, int ldk, const T* vt, int ldv, T* ps,
+                         int ldp, int Cp, int lane) {
+  T* ps_lo = ps + 16 * ldp;
+  using M = Mfma<T>;
+  const int col = lane & 15, grp = lane >> 4;
+  const int NT = Cp / 16;
+  const int Gp = a.Gp;
+  // A rows (lane row = col)
+  const int rho = unit * 16 + col;
+  const int rq = rho / Gp, gh = rho % Gp;
+  const T* qrow = nullptr;
+  if (rq < nreq && gh < a.G) {
+    const RowInfo ri = row_info(a, req_slot(rq));
+    qrow = static_cast<const T*>(a.q) + (int64_t)ri.b * a.q_batch + (int64_t)ri.t * a.q_token +
+           ((int64_t)h * a.G + gh) * a.D;
+  }
+  f4 acc[8];
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) acc[nt] = f4{0.f, 0.f, 0.f, 0.f};
+  for (int k0 = 0; k0 < a.D; k0 += M::KS) {
+    typename M::frag fa;
+    if (qrow) {
+      fa = M::load(qrow + k0 + M::E * grp);
+    } else {
+      float z[4] = {0.f, 0.f, 0.f, 0.f};
+      fa = M::make(z);
+    }
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt)
+      if (nt < NT) acc[nt] = M::mma(fa, M::load(ks + (nt * 16 + col) * ldk + k0 + M::E * grp), acc[nt]);
+  }
+  // C-layout rows 4*grp + i
+  float mrow[4], lrow[4];
+  int64_t slot_r[4];
+  int gh_r[4];
+  bool valid_r[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = unit * 16 + 4 * grp + i;
+    const int rq_i = r / Gp;
+    gh_r[i] = r % Gp;
+    valid_r[i] = rq_i < nreq && gh_r[i] < a.G;
+    int64_t pos = -1;
+    slot_r[i] = -1;
+    if (valid_r[i]) {
+      slot_r[i] = req_slot(rq_i);
+      pos = row_info(a, slot_r[i]).pos;
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      if (nt < NT) {
+        const int key = nt * 16 + col;
+        const bool ok = valid_r[i] && key < rows && (!a.causal || blk * a.C + key <= pos);
+        const float z = ok ? acc[nt][i] * a.scale : -INFINITY;
+        acc[nt][i] = z;
+        m = fmaxf(m, z);
+      }
+    }
+    m = row_max16(m);
+    const float safe = m == -INFINITY ? 0.f : m;
+    float l = 0.f;
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      if (nt < NT) {
+        const float p = __expf(acc[nt][i] - safe);
+        l += p;
+        const T hi = from_f<T>(p);
+        ps[(4 * grp + i) * ldp + nt * 16 + col] = hi;
+        if constexpr (kSplit<T>) ps_lo[(4 * grp + i) * ldp + nt * 16 + col] = from_f<T>(p - to_f(hi));
+      }
+    }
+    mrow[i] = m;
+    lrow[i] = row_sum16(l);
+  }
+  wave_lds_sync();
+  // O = P V over Cp keys
+  const int DT = a.Dv / 16;
+  for (int dt = 0; dt < DT; ++dt) {
+    f4 o = f4{0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < Cp; k0 += M::KS) {
+      const typename M::frag fb = M::load(vt + (dt * 16 + col) * ldv + k0 + M::E * grp);
+      o = M::mma(M::load(ps + col * ldp + k0 + M::E * grp), fb, o);
+      if constexpr (kSplit<T>) o = M::mma(M::load(ps_lo + col * ldp + k0 + M::E * grp), fb, o);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (valid_r[i]) {
+        const int64_t row = slot_r[i] * a.G + gh_r[i];
+        a.part_o[row * a.Dv + dt * 16 + col] = o[i];
+        if (dt == 0 && col == 0) {
+          a.part_ml[row * 2] = mrow[i];
+          a.part_ml[row * 2 + 1] = lrow[i];
+        }
+      }
+    }
+  }
+  wave_lds_sync();
+}
+
+struct TileReqs {
+  const int32_t* reqs;
+  __device__ __forceinline__ int64_t operator()(int i) const { return reqs[i]; }
+};
+
+template <typename T>
+__global__ void __launch_bounds__(256) attn_fwd_grouped_kernel(AttnArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int Cp = (a.C + 15) / 16 * 16;
+  const int ldk = a.D + 16 / (int)sizeof(T);
+  const int ldv = Cp + 16 / (int)sizeof(T);
+  const int ldp = Cp + 16 / (int)sizeof(T);
+  T* ks = reinterpret_cast<T*>(smem);
+  T* vt = ks + Cp * ldk;
+  T* pbase = vt + a.Dv * ldv;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  T* ps = pbase + wave * 32 * ldp;
+  const int ntiles = *a.num_tiles;
+  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int g = a.tile_group[tile];
+    const int64_t blk = g % a.M0;
+    const int bh = g / a.M0;
+    const int h = bh % a.Hkv, b = bh / a.Hkv;
+    const int start = (tile - a.tile_off[g]) * a.tile;
+    const int nreq = min(a.tile, a.counts[g] - start);
+    const int rows = (int)min((int64_t)a.C, (int64_t)a.N - blk * a.C);
+    __syncthreads();
+    stage_kv<T>(a, b, h, blk, rows, ks, ldk, vt, ldv, Cp, tid, blockDim.x);
+    __syncthreads();
+    const TileReqs reqs{a.tile_req + (int64_t)tile * a.tile};
+    const int units = (nreq * a.Gp + 15) / 16;
+    for (int u = wave; u < units; u += (int)(blockDim.x >> 6))
+      fwd_unit<T>(a, reqs, nreq, u, b, h, blk, rows, ks, ldk, vt, ldv, ps, ldp, Cp, lane);
+  }
+}
+
+struct OneReq {
+  int64_t slot;
+  __device__ __forceinline__ int64_t operator()(int) const { return slot; }
+};
+
+// One request (slot) per workgroup of one wave: decode and other short queries.
+template <typename T>
+__global__ void __launch_bounds__(64) attn_fwd_direct_kernel(AttnArgs a, int64_t slots) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int64_t slot = blockIdx.x;
+  if (slot >= slots) return;
+  const RowInfo ri = row_info(a, slot);
+  const int64_t blk = slot_block(a, slot);
+  if (!slot_visible(a, blk, ri.pos)) return;
+  const int Cp = (a.C + 15) / 16 * 16;
+  const int ldk = a.D + 16 / (int)sizeof(T);
+  const int ldv = Cp + 16 / (int)sizeof(T);
+  const int ldp = Cp + 16 / (int)sizeof(T);
+  T* ks = reinterpret_cast<T*>(smem);
+  T* vt = ks + Cp * ldk;
+  T* ps = vt + a.Dv * ldv;
+  const int rows = (int)min((int64_t)a.C, (int64_t)a.N - blk * a.C);
+  stage_kv<T>(a, ri.b, ri.h, blk, rows, ks, ldk, vt, ldv, Cp, threadIdx.x, blockDim.x);
+  __syncthreads();
+  const int units = (a.Gp + 15) / 16;
+  for (int u = 0; u < units; ++u)
+    fwd_unit<T>(a, OneReq{slot}, 1, u, ri.b, ri.h, blk, rows, ks, ldk, vt, ldv, ps, ldp, Cp,
+                threadIdx.x & 63);
+}
+
+// Merge the K partials of each (batch, token, query head) in slot order.
+// One wave per (batch, token, kv head); lanes over the value dims.
+template <typename T>
+__global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a, int64_t items) {
+  const int lane = threadIdx.x & 63;
+  const int64_t item = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (item >= items) return;
+  const RowInfo ri = row_info(a, item * a.K);
+  for (int gh = 0; gh < a.G; ++gh) {
+    float big = -INFINITY;
+    for (int s = 0; s < a.K; ++s) {
+      const int64_t slot = item * a.K + s;
+      if (!slot_visible(a, slot_block(a, slot), ri.pos)) continue;
+      big = fmaxf(big, a.part_ml[(slot * a.G + gh) * 2]);
+    }
+    const int64_t orow = (item * a.G + gh);  // == ((b*T + t)*Hq + h*G + gh)
+    T* out = static_cast<T*>(a.out) + orow * a.Dv;
+    float* out32 = a.out_f32 ? a.out_f32 + orow * a.Dv : nullptr;
+    if (big == -INFINITY) {
+      for (int d = lane; d < a.Dv; d += 64) {
+        out[d] = from_f<T>(0.f);
+        if (out32) out32[d] = 0.f;
+      }
+      if (lane == 0) a.lse_out[orow] = -INFINITY;
+      continue;
+    }
+    float total = 0.f;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};  // Dv <= 256
+    for (int s = 0; s < a.K; ++s) {
+      const int64_t slot = item * a.K + s;
+      if (!slot_visible(a, slot_block(a, slot), ri.pos)) continue;
+      const int64_t prow = slot * a.G + gh;
+      const float w = __expf(a.part_ml[prow * 2] - big);
+      total += w * a.part_ml[prow * 2 + 1];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d = lane + 64 * j;
+        if (d < a.Dv) acc[j] = fmaf(w, a.part_o[prow * a.Dv + d], acc[j]);
+      }
+    }
+    const float inv = 1.f / total;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d = lane + 64 * j;
+      if (d < a.Dv) {
+        out[d] = from_f<T>(acc[j] * inv);
+        if (out32) out32[d] = acc[j] * inv;
+      }
+    }
+    if (lane == 0) a.lse_out[orow] = big + __logf(total);
+  }
+}
+
+// ------------------------------------------------------------------ backward
+
+// delta[row] = sum_d dO[row, d] * O[row, d] (float32; O before its 16-bit
+// rounding when the forward kept it), one wave per row.
+template <typename T>
+__global__ void __launch_bounds__(256) attn_delta_kernel(AttnArgs a, int64_t rows) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* o = static_cast<const T*>(a.out) + row * a.Dv;
+  const float* o32 = a.out_f32 ? a.out_f32 + row * a.Dv : nullptr;
+  const T* d = static_cast<const T*>(a.dout) + row * a.Dv;
+  float s = 0.f;
+  for (int i = lane; i < a.Dv; i += 64) s = fmaf(o32 ? o32[i] : to_f(o[i]), to_f(d[i]), s);
+  s = wave_sum(s);
+  if (lane == 0) a.delta[row] = s;
+}
+
+// LDS carve of the backward kernel (byte offsets, 16-byte aligned regions).
+struct BwdLds {
+  size_t kt, qt, dot, dsa, pw, lse, delta, pos, slot, gh, total;
+  int ldkt, ldt, lds, ldp;
+};
+
+__host__ __device__ inline BwdLds bwd_layout(int C, int D, int Dv, int es) {
+  BwdLds L;
+  const int Cp = (C + 15) / 16 * 16;
+  const int pad = 16 / es;
+  const int NW = Cp / 16;
+  L.ldkt = Cp + pad;  // kt[d][key]
+  L.ldt = 16 + pad;   // qt[d][row], dot[d][row]
+  L.lds = Cp + pad;   // dsa[row][key]
+  L.ldp = 16 + pad;   // pw[wave][row][key]
+  size_t o = 0;
+  auto take = [&](size_t bytes) { size_t at = o; o = (o + bytes + 15) / 16 * 16; return at; };
+  L.kt = take((size_t)D * L.ldkt * es);
+  L.qt = take((size_t)D * L.ldt * es);
+  L.dot = take((size_t)Dv * L.ldt * es);
+  L.dsa = take((size_t)32 * L.lds * es);          // dS hi rows 0..15, lo rows 16..31
+  L.pw = take((size_t)NW * 32 * L.ldp * es);       // per wave: P hi, then P lo
+  L.lse = take(16 * 4);
+  L.delta = take(16 * 4);
+  L.pos = take(16 * 8);
+  L.slot = take(16 * 8);
+  L.gh = take(16 * 4);
+  L.total = o;
+  return L;
+}
+
+template <typename T, int HD>
+__global__ void __launch_bounds__(512) attn_bwd_grouped_kernel(AttnArgs a) {
+  using M = Mfma<T>;
+  constexpr int NF = HD / M::KS;  // fragments along the head dim
+  constexpr int DT = HD / 16;     // 16-wide output tiles along the head dim
+  constexpr int VEC = 16 / sizeof(T);
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const BwdLds L = bwd_layout(a.C, HD, HD, sizeof(T));
+  const int Cp = (a.C + 15) / 16 * 16;
+  const int NW = Cp / 16;
+  T* kt = reinterpret_cast<T*>(smem + L.kt);
+  T* qt = reinterpret_cast<T*>(smem + L.qt);
+  T* dot = reinterpret_cast<T*>(smem + L.dot);
+  T* dsa = reinterpret_cast<T*>(smem + L.dsa);
+  float* rlse = reinterpret_cast<float*>(smem + L.lse);
+  float* rdelta = reinterpret_cast<float*>(smem + L.delta);
+  int64_t* rpos = reinterpret_cast<int64_t*>(smem + L.pos);
+  int64_t* rslot = reinterpret_cast<int64_t*>(smem + L.slot);
+  int* rgh = reinterpret_cast<int*>(smem + L.gh);
+  const int ldkt = L.ldkt, ldt = L.ldt, lds = L.lds, ldp = L.ldp;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int col = lane & 15, grp = lane >> 4;
+  T* pw = reinterpret_cast<T*>(smem + L.pw) + wave * 32 * ldp;
+  T* pw_lo = pw + 16 * ldp;
+  T* dsa_lo = dsa + 16 * lds;
+  const int kbase = wave * 16;  // this wave's keys
+  const int ntiles = *a.num_tiles;
+  const int Hq = a.Hkv * a.G;
+
+  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int g = a.tile_group[tile];
+    const int64_t blk = g % a.M0;
+    const int bh = g / a.M0;
+    const int h = bh % a.Hkv, b = bh / a.Hkv;
+    const int start = (tile - a.tile_off[g]) * a.tile;
+    const int nreq = min(a.tile, a.counts[g] - start);
+    const int rows = (int)min((int64_t)a.C, (int64_t)a.N - blk * a.C);
+    const int32_t* reqs = a.tile_req + (int64_t)tile * a.tile;
+    const T* kb = static_cast<const T*>(a.k) + (int64_t)b * a.k_batch + blk * a.C * a.k_token +
+                  (int64_t)h * HD;
+    const T* vb = static_cast<const T*>(a.v) + (int64_t)b * a.v_batch + blk * a.C * a.v_token +
+                  (int64_t)h * HD;
+    __syncthreads();
+    // K transposed into LDS (B operand of dQ = dS K)
+    for (int idx = tid; idx < Cp * (HD / VEC); idx += blockDim.x) {
+      const int r = idx / (HD / VEC), c = (idx % (HD / VEC)) * VEC;
+      union {
+        uint4 u;
+        T e[VEC];
+      } v;
+      v.u = make_uint4(0, 0, 0, 0);
+      if (r < rows) v.u = *reinterpret_cast<const uint4*>(kb + (int64_t)r * a.k_token + c);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) kt[(c + e) * ldkt + r] = v.e[e];
+    }
+    // this wave's K and V rows as B fragments of S = Q K^T and dP = dO V^T
+    const int key_l = kbase + col;
+    typename M::frag kf[NF], vf[NF];
+    {
+      float z[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < NF; ++j) {
+        kf[j] = key_l < rows ? M::load(kb + (int64_t)key_l * a.k_token + j * M::KS + M::E * grp) : M::make(z);
+        vf[j] = key_l < rows ? M::load(vb + (int64_t)key_l * a.v_token + j * M::KS + M::E * grp) : M::make(z);
+      }
+    }
+    f4 dk[DT], dv[DT];
+#pragma unroll
+    for (int j = 0; j < DT; ++j) { dk[j] = f4{0.f, 0.f, 0.f, 0.f}; dv[j] = f4{0.f, 0.f, 0.f, 0.f}; }
+
+    const int units = (nreq * a.Gp + 15) / 16;
+    for (int u = 0; u < units; ++u) {
+      __syncthreads();  // the previous unit is done with the staged rows
+      if (tid < 16) {
+        const int rho = u * 16 + tid;
+        const int rq = rho / a.Gp, gh = rho % a.Gp;
+        rslot[tid] = -1;
+        rgh[tid] = gh;
+        rlse[tid] = 0.f;
+        rdelta[tid] = 0.f;
+        rpos[tid] = -1;
+        if (rq < nreq && gh < a.G) {
+          const RowInfo ri = row_info(a, reqs[rq]);
+          const int64_t orow = ((int64_t)ri.b * a.T + ri.t) * Hq + (int64_t)h * a.G + gh;
+          rslot[tid] = ri.slot;
+          rpos[tid] = ri.pos;
+          rlse[tid] = a.lse[orow];
+          rdelta[tid] = a.delta[orow];
+        }
+      }
+      __syncthreads();
+      // Q and dO rows, transposed (B operands of dK and dV)
+      for (int idx = tid; idx < 2 * 16 * (HD / VEC); idx += blockDim.x) {
+        const int which = idx / (16 * (HD / VEC));
+        const int rem = idx % (16 * (HD / VEC));
+        const int r = rem / (HD / VEC), c = (rem % (HD / VEC)) * VEC;
+        union {
+          uint4 u;
+          T e[VEC];
+        } v;
+        v.u = make_uint4(0, 0, 0, 0);
+        if (rslot[r] >= 0) {
+          const RowInfo ri = row_info(a, rslot[r]);
+          const int64_t orow = ((int64_t)ri.b * a.T + ri.t) * Hq + (int64_t)h * a.G + rgh[r];
+          const T* src = which == 0 ? static_cast<const T*>(a.q) + (int64_t)ri.b * a.q_batch +
+                                          (int64_t)ri.t * a.q_token + ((int64_t)h * a.G + rgh[r]) * HD
+                                    : static_cast<const T*>(a.dout) + orow * HD;
+          v.u = *reinterpret_cast<const uint4*>(src + c);
+        }
+        T* tr = which == 0 ? qt : dot;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) tr[(c + e) * ldt + r] = v.e[e];
+      }
+      __syncthreads();
+
+      // S and dP for this wave's 16 keys; A rows (lane row = col) read from global
+      const T* qrow = nullptr;
+      const T* orow_p = nullptr;
+      if (rslot[col] >= 0) {
+        const RowInfo ri = row_info(a, rslot[col]);
+        qrow = static_cast<const T*>(a.q) + (int64_t)ri.b * a.q_batch + (int64_t)ri.t * a.q_token +
+               ((int64_t)h * a.G + rgh[col]) * HD;
+        orow_p = static_cast<const T*>(a.dout) +
+                 (((int64_t)ri.b * a.T + ri.t) * Hq + (int64_t)h * a.G + rgh[col]) * HD;
+      }
+      f4 s = f4{0.f, 0.f, 0.f, 0.f}, dp = f4{0.f, 0.f, 0.f, 0.f};
+      {
+        float z[4] = {0.f, 0.f, 0.f, 0.f};
+        const typename M::frag zero = M::make(z);
+#pragma unroll
+        for (int j = 0; j < NF; ++j) {
+          const typename M::frag fq = qrow ? M::load(qrow + j * M::KS + M::E * grp) : zero;
+          const typename M::frag fo = orow_p ? M::load(orow_p + j * M::KS + M::E * grp) : zero;
+          s = M::mma(fq, kf[j], s);
+          dp = M::mma(fo, vf[j], dp);
+        }
+      }
+      const int key = kbase + col;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * grp + i;
+        const bool ok = rslot[r] >= 0 && key < rows && (!a.causal || blk * a.C + key <= rpos[r]);
+        const float p = ok ? __expf(s[i] * a.scale - rlse[r]) : 0.f;
+        const float ds = p * (dp[i] - rdelta[r]);
+        const T p_hi = from_f<T>(p);
+        const T ds_hi = from_f<T>(ds);
+        pw[r * ldp + col] = p_hi;
+        dsa[r * lds + kbase + col] = ds_hi;
+        if constexpr (kSplit<T>) {
+          pw_lo[r * ldp + col] = from_f<T>(p - to_f(p_hi));
+          dsa_lo[r * lds + kbase + col] = from_f<T>(ds - to_f(ds_hi));
+        }
+      }
+      wave_lds_sync();
+      // dV += P^T dO ; dK += dS^T Q   (rows = this wave's keys, k = the 16 query rows)
+#pragma unroll
+      for (int k0 = 0; k0 < 16; k0 += M::KS) {
+        const typename M::frag pa = M::gather(pw + (k0 + M::E * grp) * ldp + col, ldp);
+        const typename M::frag da = M::gather(dsa + (k0 + M::E * grp) * lds + kbase + col, lds);
+        typename M::frag pa_lo = pa, da_lo = da;
+        if constexpr (kSplit<T>) {
+          pa_lo = M::gather(pw_lo + (k0 + M::E * grp) * ldp + col, ldp);
+          da_lo = M::gather(dsa_lo + (k0 + M::E * grp) * lds + kbase + col, lds);
+        }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const typename M::frag fo = M::load(dot + (dt * 16 + col) * ldt + k0 + M::E * grp);
+          const typename M::frag fq = M::load(qt + (dt * 16 + col) * ldt + k0 + M::E * grp);
+          dv[dt] = M::mma(pa, fo, dv[dt]);
+          dk[dt] = M::mma(da, fq, dk[dt]);
+          if constexpr (kSplit<T>) {
+            dv[dt] = M::mma(pa_lo, fo, dv[dt]);
+            dk[dt] = M::mma(da_lo, fq, dk[dt]);
+          }
+        }
+      }
+      __syncthreads();  // dS of every key is in dsa
+      // dQ = scale * dS K on head-dim tiles wave, wave + NW, ...
+      for (int dt = wave; dt < DT; dt += NW) {
+        f4 q = f4{0.f, 0.f, 0.f, 0.f};
+        for (int k0 = 0; k0 < Cp; k0 += M::KS) {
+          const typename M::frag fk = M::load(kt + (dt * 16 + col) * ldkt + k0 + M::E * grp);
+          q = M::mma(M::load(dsa + col * lds + k0 + M::E * grp), fk, q);
+          if constexpr (kSplit<T>) q = M::mma(M::load(dsa_lo + col * lds + k0 + M::E * grp), fk, q);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 4 * grp + i;
+          if (rslot[r] >= 0)
+            a.part_dq[(rslot[r] * a.G + rgh[r]) * HD + dt * 16 + col] = q[i] * a.scale;
+        }
+      }
+    }
+    // the tile's dK/dV partial for this wave's keys (C-layout rows 4*grp + i)
+    float* part = a.part_dkv + (int64_t)tile * Cp * (2 * HD);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key_r = kbase + 4 * grp + i;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        part[(int64_t)key_r * (2 * HD) + dt * 16 + col] = dk[dt][i] * a.scale;
+        part[(int64_t)key_r * (2 * HD) + HD + dt * 16 + col] = dv[dt][i];
+      }
+    }
+  }
+}
+
+// dK/dV of every key: the sum of its block's tile partials in tile order
+// (zero for blocks no row selected).  One workgroup per (batch, head, block).
+template <typename T>
+__global__ void __launch_bounds__(256) attn_dkv_reduce_kernel(AttnArgs a, int64_t groups) {
+  const int64_t g = blockIdx.x;
+  if (g >= groups) return;
+  const int Cp = (a.C + 15) / 16 * 16;
+  const int64_t blk = g % a.M0;
+  const int64_t bh = g / a.M0;
+  const int h = (int)(bh % a.Hkv), b = (int)(bh / a.Hkv);
+  const int rows = (int)min((int64_t)a.C, (int64_t)a.N - blk * a.C);
+  const int first = a.tile_off[g];
+  const int n = (a.counts[g] + a.tile - 1) / a.tile;
+  const int width = a.D + a.Dv;
+  for (int idx = threadIdx.x; idx < rows * width; idx += blockDim.x) {
+    const int r = idx / width, c = idx % width;
+    float s = 0.f;
+    for (int j = 0; j < n; ++j) s += a.part_dkv[((int64_t)(first + j) * Cp + r) * width + c];
+    const int64_t tok = blk * a.C + r;
+    if (c < a.D)
+      static_cast<T*>(a.dk)[(int64_t)b * a.dk_batch + tok * a.dk_token + (int64_t)h * a.D + c] = from_f<T>(s);
+    else
+      static_cast<T*>(a.dv)[(int64_t)b * a.dv_batch + tok * a.dv_token + (int64_t)h * a.Dv + (c - a.D)] =
+          from_f<T>(s);
+  }
+}
+
+// dQ of each (batch, token, query head): its visible slots' partials in slot order.
+template <typename T>
+__global__ void __launch_bounds__(256) attn_dq_combine_kernel(AttnArgs a, int64_t items) {
+  const int lane = threadIdx.x & 63;
+  const int64_t item = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (item >= items) return;
+  const RowInfo ri = row_info(a, item * a.K);
+  for (int gh = 0; gh < a.G; ++gh) {
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < a.K; ++s) {
+      const int64_t slot = item * a.K + s;
+      if (!slot_visible(a, slot_block(a, slot), ri.pos)) continue;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d = lane + 64 * j;
+        if (d < a.D) acc[j] += a.part_dq[(slot * a.G + gh) * a.D + d];
+      }
+    }
+    T* out = static_cast<T*>(a.dq) + (item * a.G + gh) * a.D;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d = lane + 64 * j;
+      if (d < a.D) out[d] = from_f<T>(acc[j]);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ launchers
+
+static size_t fwd_lds(const AttnArgs& a, int es, int waves) {
+  const int Cp = (a.C + 15) / 16 * 16;
+  const int pad = 16 / es;
+  return (size_t)es * ((size_t)Cp * (a.D + pad) + (size_t)a.Dv * (Cp + pad) + (size_t)waves * 32 * (Cp + pad));
+}
+
+static size_t bwd_lds(const AttnArgs& a, int es) { return bwd_layout(a.C, a.D, a.Dv, es).total; }
+
+int attn_check(const AttnArgs& a, int dtype, bool backward) {
+  const int es = dtype_size(dtype);
+  if (!es) return fail(PISA_ERR_INVALID, "unknown dtype %d", dtype);
+  if (a.D % 16 || a.Dv % 16 || a.D > 256 || a.Dv > 256)
+    return fail(PISA_ERR_UNSUPPORTED, "attention needs head dims that are multiples of 16, <= 256");
+  if (a.C > 128) return fail(PISA_ERR_UNSUPPORTED, "attention supports block_size <= 128");
+  const size_t limit = (size_t)device_lds_limit();
+  if (fwd_lds(a, es, 4) > limit) return fail(PISA_ERR_UNSUPPORTED, "forward tiles exceed LDS");
+  if (backward) {
+    if (a.D != a.Dv || (a.D != 16 && a.D != 32 && a.D != 64 && a.D != 128))
+      return fail(PISA_ERR_UNSUPPORTED, "attention backward needs head_dim == value_dim in {16,32,64,128}");
+    if (bwd_lds(a, es) > limit) return fail(PISA_ERR_UNSUPPORTED, "backward tiles exceed LDS");
+  }
+  return PISA_OK;
+}
+
+static int grid_size() {
+  const int cus = device_cus();
+  return cus * 8;
+}
+
+template <typename T>
+static int attn_fwd_t(const AttnArgs& a, bool grouped, int64_t slots, int64_t items, hipStream_t stream) {
+  const int es = sizeof(T);
+  if (grouped) {
+    const size_t lds = fwd_lds(a, es, 4);
+    allow_lds((const void*)attn_fwd_grouped_kernel<T>, lds);
+    PISA_TIMED("attn_fwd", stream, hipLaunchKernelGGL(attn_fwd_grouped_kernel<T>, dim3(grid_size()), dim3(256), lds, stream, a));
+  } else if (slots > 0) {
+    const size_t lds = fwd_lds(a, es, 1);
+    allow_lds((const void*)attn_fwd_direct_kernel<T>, lds);
+    PISA_TIMED("attn_fwd_direct", stream, hipLaunchKernelGGL(attn_fwd_direct_kernel<T>, dim3(slots), dim3(64), lds, stream, a, slots));
+  }
+  if (items > 0)
+    PISA_TIMED("attn_combine", stream, hipLaunchKernelGGL(attn_combine_kernel<T>, dim3((items + 3) / 4), dim3(256), 0, stream, a, items));
+  return check_launch("attention forward");
+}
+
+int launch_attn_fwd(int dtype, const AttnArgs& a, bool grouped, int64_t slots, int64_t items,
+                    hipStream_t stream) {
+  switch (dtype) {
+    case PISA_F32: return attn_fwd_t<float>(a, grouped, slots, items, stream);
+    case PISA_F16: return attn_fwd_t<f16_t>(a, grouped, slots, items, stream);
+    case PISA_BF16: return attn_fwd_t<bf16_t>(a, grouped, slots, items, stream);
+    default: return fail(PISA_ERR_INVALID, "unknown dtype %d", dtype);
+  }
+}
+
+template <typename T, int HD>
+static void launch_bwd_kernel(const AttnArgs& a, hipStream_t stream) {
+  const int Cp = (a.C + 15) / 16 * 16;
+  const size_t lds = bwd_lds(a, sizeof(T));
+  allow_lds((const void*)attn_bwd_grouped_kernel<T, HD>, lds);
+  PISA_TIMED("attn_bwd", stream, hipLaunchKernelGGL((attn_bwd_grouped_kernel<T, HD>), dim3(grid_size()), dim3(64 * (Cp / 16)),
+                     lds, stream, a));
+}
+
+template <typename T>
+static int attn_bwd_t(const AttnArgs& a, int64_t groups, int64_t items, hipStream_t stream) {
+  const int64_t rows = items * a.G;
+  if (rows > 0)
+    PISA_TIMED("attn_delta", stream, hipLaunchKernelGGL(attn_delta_kernel<T>, dim3((rows + 3) / 4), dim3(256), 0, stream, a, rows));
+  switch (a.D) {
+    case 16: launch_bwd_kernel<T, 16>(a, stream); break;
+    case 32: launch_bwd_kernel<T, 32>(a, stream); break;
+    case 64: launch_bwd_kernel<T, 64>(a, stream); break;
+    case 128: launch_bwd_kernel<T, 128>(a, stream); break;
+    default: return fail(PISA_ERR_UNSUPPORTED, "attention backward head_dim %d", a.D);
+  }
+  if (groups > 0)
+    PISA_TIMED("attn_dkv_reduce", stream, hipLaunchKernelGGL(attn_dkv_reduce_kernel<T>, dim3(groups), dim3(256), 0, stream, a, groups));
+  if (items > 0)
+    PISA_TIMED("attn_dq_combine", stream, hipLaunchKernelGGL(attn_dq_combine_kernel<T>, dim3((items + 3) / 4), dim3(256), 0, stream, a, items));
+  return check_launch("attention backward");
+}
+
+int launch_attn_bwd(int dtype, const AttnArgs& a, int64_t groups, int64_t items, hipStream_t stream) {
+  switch (dtype) {
+    case PISA_F32: return attn_bwd_t<float>(a, groups, items, stream);
+    case PISA_F16: return attn_bwd_t<f16_t>(a, groups, items, stream);
+    case PISA_BF16: return attn_bwd_t<bf16_t>(a, groups, items, stream);
+    default: return fail(PISA_ERR_INVALID, "unknown dtype %d", dtype);
+  }
+}
+
+}  // namespace pisa

@@ -1,0 +1,501 @@
+// C ABI entry points of libpisa_hip.so: argument checks, workspace carving and
+// the launch sequence of each operator.  The kernels live in pisa_pool.hip,
+// pisa_route.hip, pisa_group.hip, pisa_leaf.hip and pisa_attn.hip.
+
+#include "pisa_device.h"
+#include "pisa_internal.h"
+
+using namespace pisa;
+
+namespace {
+
+constexpr int kLeafTile = 256;  // requests per leaf tile (one key-block load each)
+constexpr int kAttnTile = 256;  // requests per attention tile
+
+bool pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+int padded_group(int g) { return g <= 16 ? next_pow2(g) : (g + 15) / 16 * 16; }
+
+int check_qk(const pisa_qk_desc* qk) {
+  if (!qk) return fail(PISA_ERR_INVALID, "null descriptor");
+  if (qk->batch < 1 || qk->query_tokens < 1 || qk->query_heads < 1 || qk->key_tokens < 1 ||
+      qk->key_heads < 1 || qk->head_dim < 1)
+    return fail(PISA_ERR_INVALID, "nonempty tensors are required");
+  if (qk->query_heads % qk->key_heads)
+    return fail(PISA_ERR_INVALID, "a whole number of query heads per KV head is required");
+  if (!dtype_size(qk->dtype)) return fail(PISA_ERR_INVALID, "unknown dtype %d", qk->dtype);
+  const int vec = 16 / dtype_size(qk->dtype);
+  if (qk->q_stride_batch % vec || qk->q_stride_token % vec || qk->k_stride_batch % vec ||
+      qk->k_stride_token % vec)
+    return fail(PISA_ERR_UNSUPPORTED, "q/k batch and token strides must be multiples of 16 bytes");
+  return PISA_OK;
+}
+
+struct SelectPlan {
+  bool grouped;
+  int64_t items;
+  int W;
+  int64_t slots;
+  int64_t groups;
+  int M0;
+  int G;
+};
+
+int plan_select(const pisa_qk_desc* qk, const pisa_select_params* p, SelectPlan& pl) {
+  int rc = check_qk(qk);
+  if (rc) return rc;
+  if (!p) return fail(PISA_ERR_INVALID, "null parameters");
+  if (p->method < PISA_METHOD_PISA1 || p->method > PISA_METHOD_LSE)
+    return fail(PISA_ERR_INVALID, "method must be pisa1, pisa2 or pisa");
+  if (!pow2(p->block_size) || p->block_size < 16 || p->block_size > 128)
+    return fail(PISA_ERR_UNSUPPORTED, "GPU routing requires a power-of-two block_size in [16, 128]");
+  if (!pow2(p->branching) || p->branching < 2 || p->branching > 16)
+    return fail(PISA_ERR_UNSUPPORTED, "branching must be a power of two in [2, 16]");
+  if (p->topk < 1 || p->topk > 64) return fail(PISA_ERR_UNSUPPORTED, "topk must be in [1, 64]");
+  if (p->force_recent < 1) return fail(PISA_ERR_INVALID, "causal pyramid routing requires force_recent >= 1");
+  if (p->first_width < 1 || p->first_width > 512 || p->branching * p->topk > 512)
+    return fail(PISA_ERR_UNSUPPORTED, "network width above 512");
+  const int G = qk->query_heads / qk->key_heads;
+  if (G > 16) return fail(PISA_ERR_UNSUPPORTED, "routing supports up to 16 query heads per KV head");
+  const int D = qk->head_dim;
+  if (D != 16 && D != 32 && D != 64 && D != 128)
+    return fail(PISA_ERR_UNSUPPORTED, "routing supports head_dim 16, 32, 64 or 128");
+  pl.G = G;
+  pl.M0 = (qk->key_tokens + p->block_size - 1) / p->block_size;
+  pl.items = (int64_t)qk->batch * qk->query_tokens * qk->key_heads;
+  pl.W = p->top == 0 ? p->first_width : p->branching * p->topk;
+  pl.grouped = p->schedule == PISA_SCHEDULE_GROUPED && p->method != PISA_METHOD_PISA1;
+  pl.slots = pl.items * pl.W;
+  pl.groups = (int64_t)qk->batch * qk->key_heads * pl.M0;
+  return PISA_OK;
+}
+
+struct SelectBuffers {
+  int32_t* cand;
+  uint8_t* scoreable;
+  float* scores;
+  Buckets buckets;
+};
+
+void carve_select(const SelectPlan& pl, Carve& c, SelectBuffers& sb) {
+  sb.cand = c.take<int32_t>(pl.slots);
+  sb.scoreable = c.take<uint8_t>(pl.slots);
+  sb.scores = c.take<float>(pl.slots);
+  carve_buckets(c, sb.buckets, pl.slots, pl.groups, kLeafTile);
+}
+
+LeafArgs leaf_args(const pisa_qk_desc* qk, int method, int block_size, int W, int M0, int G,
+                   const void* q, const void* src, int64_t src_batch, int64_t src_row, int src_rows,
+                   int C, const Buckets& b, float* scores) {
+  LeafArgs a;
+  a.q = q;
+  a.q_batch = qk->q_stride_batch;
+  a.q_token = qk->q_stride_token;
+  a.src = src;
+  a.src_batch = src_batch;
+  a.src_row = src_row;
+  a.T = qk->query_tokens;
+  a.Hkv = qk->key_heads;
+  a.G = G;
+  a.Gp = padded_group(G);
+  a.D = qk->head_dim;
+  a.src_rows = src_rows;
+  a.C = C;
+  a.W = W;
+  a.M0 = M0;
+  a.method = method;
+  a.scale = (float)(1.0 / sqrt((double)qk->head_dim));
+  a.tile_group = b.tile_group;
+  a.tile_req = b.tile_req;
+  a.tile_off = b.tile_off;
+  a.counts = b.counts;
+  a.num_tiles = b.num_tiles;
+  a.tile = b.tile;
+  a.scores = scores;
+  (void)block_size;
+  return a;
+}
+
+}  // namespace
+
+extern "C" size_t pisa_select_workspace_size(const pisa_qk_desc* qk, const pisa_select_params* p) {
+  SelectPlan pl;
+  if (plan_select(qk, p, pl)) return 0;
+  if (!pl.grouped) return 0;
+  Carve c{nullptr, 0, 0};
+  SelectBuffers sb;
+  carve_select(pl, c, sb);
+  return align_up(c.used, 256);
+}
+
+extern "C" int pisa_select(const pisa_qk_desc* qk, const pisa_select_params* p, const void* q,
+                           const void* k, const pisa_pyramid_desc* pyramid,
+                           const int64_t* positions, int64_t positions_stride_batch, int64_t* out,
+                           int32_t* trace, void* workspace, size_t workspace_bytes, void* stream) {
+  SelectPlan pl;
+  int rc = plan_select(qk, p, pl);
+  if (rc) return rc;
+  if (!q || !k || !pyramid || !pyramid->storage || !positions || !out)
+    return fail(PISA_ERR_INVALID, "null tensor argument");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(pyramid->storage))
+    return fail(PISA_ERR_UNSUPPORTED, "q, k and the pyramid must be 16-byte aligned");
+  if (pyramid->levels < p->top + 1 || pyramid->levels > PISA_MAX_LEVELS)
+    return fail(PISA_ERR_INVALID, "the pyramid has %d levels, routing needs %d", pyramid->levels,
+                p->top + 1);
+  if (pyramid->lengths[0] != pl.M0)
+    return fail(PISA_ERR_INVALID, "pyramid leaf level has %d blocks, expected %d",
+                pyramid->lengths[0], pl.M0);
+  hipStream_t st = (hipStream_t)stream;
+  SelectBuffers sb{};
+  if (pl.grouped) {
+    Carve c{static_cast<char*>(workspace), 0, workspace_bytes};
+    carve_select(pl, c, sb);
+    if (!workspace || !c.fits())
+      return fail(PISA_ERR_WORKSPACE, "select needs %zu workspace bytes", c.used);
+  }
+  RouteArgs a;
+  a.q = q;
+  a.q_batch = qk->q_stride_batch;
+  a.q_token = qk->q_stride_token;
+  a.summary = pyramid->storage;
+  a.sum_batch = pyramid->stride_batch;
+  a.key = k;
+  a.key_batch = qk->k_stride_batch;
+  a.key_token = qk->k_stride_token;
+  a.positions = positions;
+  a.pos_batch = positions_stride_batch;
+  a.T = qk->query_tokens;
+  a.Hkv = qk->key_heads;
+  a.G = pl.G;
+  a.D = qk->head_dim;
+  a.N = qk->key_tokens;
+  a.C = p->block_size;
+  a.branching = p->branching;
+  a.topk = p->topk;
+  a.top = p->top;
+  a.first_width = p->first_width;
+  a.method = p->method;
+  a.force_first = p->force_first ? 1 : 0;
+  a.force_recent = p->force_recent;
+  a.fused = pl.grouped ? 0 : 1;
+  a.scale = (float)(1.0 / sqrt((double)qk->head_dim));
+  for (int l = 0; l < PISA_MAX_LEVELS; ++l) {
+    a.offsets[l] = l < pyramid->levels ? pyramid->offsets[l] : 0;
+    a.lengths[l] = l < pyramid->levels ? pyramid->lengths[l] : 0;
+  }
+  a.cand = sb.cand;
+  a.scoreable = sb.scoreable;
+  a.out = out;
+  a.trace = trace;
+  // One wave per item for prefill; the fused leaf of a few long rows (decode)
+  // spreads its support rows over eight waves.
+  int threads = 64;
+  if (!pl.grouped && p->method != PISA_METHOD_PISA1) threads = pl.items < 8192 ? 512 : 256;
+  rc = launch_route(qk->dtype, a, pl.items, threads, st);
+  if (rc || !pl.grouped) return rc;
+
+  LeafRequests req{sb.cand, sb.scoreable, pl.W, qk->key_heads, qk->query_tokens, pl.M0};
+  rc = bucket_leaf(req, pl.slots, sb.buckets, st);
+  if (rc) return rc;
+  LeafArgs la = leaf_args(qk, p->method, p->block_size, pl.W, pl.M0, pl.G, q, k,
+                          qk->k_stride_batch, qk->k_stride_token, qk->key_tokens, p->block_size,
+                          sb.buckets, sb.scores);
+  rc = launch_leaf(qk->dtype, la, st);
+  if (rc) return rc;
+  FinalArgs f;
+  f.cand = sb.cand;
+  f.scoreable = sb.scoreable;
+  f.scores = sb.scores;
+  f.positions = positions;
+  f.pos_batch = positions_stride_batch;
+  f.items = pl.items;
+  f.T = qk->query_tokens;
+  f.Hkv = qk->key_heads;
+  f.W = pl.W;
+  f.K = p->topk;
+  f.C = p->block_size;
+  f.M0 = pl.M0;
+  f.force_first = a.force_first;
+  f.force_recent = p->force_recent;
+  f.top = p->top;
+  f.out = out;
+  f.trace = trace;
+  return launch_final(f, st);
+}
+
+namespace {
+
+void carve_leaf(const pisa_qk_desc* qk, int block_size, int width, Carve& c, uint8_t** mask,
+                Buckets& b) {
+  const int M0 = (qk->key_tokens + block_size - 1) / block_size;
+  const int64_t slots = (int64_t)qk->batch * qk->query_tokens * qk->key_heads * width;
+  const int64_t groups = (int64_t)qk->batch * qk->key_heads * M0;
+  *mask = c.take<uint8_t>(slots);
+  carve_buckets(c, b, slots, groups, kLeafTile);
+}
+
+}  // namespace
+
+extern "C" size_t pisa_leaf_workspace_size(const pisa_qk_desc* qk, int32_t block_size,
+                                           int32_t width) {
+  if (check_qk(qk) || block_size < 1 || width < 1) return 0;
+  Carve c{nullptr, 0, 0};
+  uint8_t* mask;
+  Buckets b;
+  carve_leaf(qk, block_size, width, c, &mask, b);
+  return align_up(c.used, 256);
+}
+
+extern "C" int pisa_leaf_scores(const pisa_qk_desc* qk, const pisa_select_params* p, const void* q,
+                                const void* k, const void* leaf_means,
+                                int64_t leaf_means_stride_batch, const int32_t* candidates,
+                                int32_t width, const int64_t* positions,
+                                int64_t positions_stride_batch, float* scores, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  int rc = check_qk(qk);
+  if (rc) return rc;
+  if (!p || !q || !k || !candidates || !positions || !scores)
+    return fail(PISA_ERR_INVALID, "null argument");
+  if (width < 1 || width > 512) return fail(PISA_ERR_UNSUPPORTED, "candidate width must be in [1, 512]");
+  if (p->method == PISA_METHOD_PISA1 && !leaf_means)
+    return fail(PISA_ERR_INVALID, "pisa1 leaf scoring needs the leaf means");
+  if (p->block_size < 1 || p->block_size > 128)
+    return fail(PISA_ERR_UNSUPPORTED, "leaf scoring supports block_size <= 128");
+  if (qk->head_dim % 16 || qk->head_dim > 256)
+    return fail(PISA_ERR_UNSUPPORTED, "leaf scoring needs head_dim % 16 == 0 and <= 256");
+  const int G = qk->query_heads / qk->key_heads;
+  const int M0 = (qk->key_tokens + p->block_size - 1) / p->block_size;
+  const int64_t items = (int64_t)qk->batch * qk->query_tokens * qk->key_heads;
+  const int64_t slots = items * width;
+  const int64_t groups = (int64_t)qk->batch * qk->key_heads * M0;
+  Carve c{static_cast<char*>(workspace), 0, workspace_bytes};
+  uint8_t* mask;
+  Buckets b;
+  carve_leaf(qk, p->block_size, width, c, &mask, b);
+  (void)groups;
+  if (!workspace || !c.fits()) return fail(PISA_ERR_WORKSPACE, "leaf scoring needs %zu bytes", c.used);
+  hipStream_t st = (hipStream_t)stream;
+  fill_f32(scores, slots, -INFINITY, st);
+  MaskArgs m;
+  m.cand = candidates;
+  m.positions = positions;
+  m.pos_batch = positions_stride_batch;
+  m.items = items;
+  m.T = qk->query_tokens;
+  m.Hkv = qk->key_heads;
+  m.W = width;
+  m.K = p->topk;
+  m.C = p->block_size;
+  m.M0 = M0;
+  m.force_first = p->force_first ? 1 : 0;
+  m.force_recent = p->force_recent;
+  m.method = p->method;
+  m.scoreable = mask;
+  rc = launch_scoreable(m, st);
+  if (rc) return rc;
+  LeafRequests req{candidates, mask, width, qk->key_heads, qk->query_tokens, M0};
+  rc = bucket_leaf(req, slots, b, st);
+  if (rc) return rc;
+  const bool pisa1 = p->method == PISA_METHOD_PISA1;
+  const int64_t row = (int64_t)qk->key_heads * qk->head_dim;
+  LeafArgs la = leaf_args(qk, p->method, p->block_size, width, M0, G, q, pisa1 ? leaf_means : k,
+                          pisa1 ? leaf_means_stride_batch : qk->k_stride_batch,
+                          pisa1 ? row : qk->k_stride_token, pisa1 ? M0 : qk->key_tokens,
+                          pisa1 ? 1 : p->block_size, b, scores);
+  return launch_leaf(qk->dtype, la, st);
+}
+
+// ------------------------------------------------------------------ attention
+
+namespace {
+
+struct AttnPlan {
+  int64_t slots, items, groups;
+  int M0, G, Cp;
+  bool grouped;
+};
+
+int plan_attn(const pisa_attn_desc* d, AttnPlan& pl) {
+  if (!d) return fail(PISA_ERR_INVALID, "null descriptor");
+  if (d->batch < 1 || d->query_tokens < 1 || d->query_heads < 1 || d->key_tokens < 1 ||
+      d->key_heads < 1 || d->head_dim < 1 || d->value_dim < 1)
+    return fail(PISA_ERR_INVALID, "nonempty tensors are required");
+  if (d->query_heads % d->key_heads)
+    return fail(PISA_ERR_INVALID, "a whole number of query heads per KV head is required");
+  if (d->topk < 0) return fail(PISA_ERR_INVALID, "negative topk");
+  if (d->block_size < 1) return fail(PISA_ERR_INVALID, "block_size must be positive");
+  if (d->index_bits != 32 && d->index_bits != 64) return fail(PISA_ERR_INVALID, "indices must be int32 or int64");
+  const int es = dtype_size(d->dtype);
+  if (!es) return fail(PISA_ERR_INVALID, "unknown dtype %d", d->dtype);
+  const int vec = 16 / es;
+  if (d->q_stride_batch % vec || d->q_stride_token % vec || d->k_stride_batch % vec ||
+      d->k_stride_token % vec || d->v_stride_batch % vec || d->v_stride_token % vec)
+    return fail(PISA_ERR_UNSUPPORTED, "batch and token strides must be multiples of 16 bytes");
+  pl.G = d->query_heads / d->key_heads;
+  pl.M0 = (d->key_tokens + d->block_size - 1) / d->block_size;
+  pl.items = (int64_t)d->batch * d->query_tokens * d->key_heads;
+  pl.slots = pl.items * d->topk;
+  pl.groups = (int64_t)d->batch * d->key_heads * pl.M0;
+  pl.Cp = (d->block_size + 15) / 16 * 16;
+  pl.grouped = pl.slots >= 4 * pl.groups;
+  return PISA_OK;
+}
+
+AttnArgs attn_args(const pisa_attn_desc* d, const AttnPlan& pl, const void* q, const void* k,
+                   const void* v, const void* indices, const int64_t* positions,
+                   int64_t pos_batch) {
+  AttnArgs a{};
+  a.q = q;
+  a.q_batch = d->q_stride_batch;
+  a.q_token = d->q_stride_token;
+  a.k = k;
+  a.k_batch = d->k_stride_batch;
+  a.k_token = d->k_stride_token;
+  a.v = v;
+  a.v_batch = d->v_stride_batch;
+  a.v_token = d->v_stride_token;
+  a.indices = indices;
+  a.index_bits = d->index_bits;
+  a.positions = positions;
+  a.pos_batch = pos_batch;
+  a.T = d->query_tokens;
+  a.Hkv = d->key_heads;
+  a.G = pl.G;
+  a.Gp = padded_group(pl.G);
+  a.D = d->head_dim;
+  a.Dv = d->value_dim;
+  a.N = d->key_tokens;
+  a.K = d->topk;
+  a.C = d->block_size;
+  a.M0 = pl.M0;
+  a.causal = d->causal ? 1 : 0;
+  a.scale = d->scale;
+  return a;
+}
+
+void carve_attn(const pisa_attn_desc* d, const AttnPlan& pl, bool backward, Carve& c, AttnArgs& a,
+                Buckets& b) {
+  if (!backward) {
+    a.part_o = c.take<float>(pl.slots * pl.G * d->value_dim);
+    a.part_ml = c.take<float>(pl.slots * pl.G * 2);
+    if (pl.grouped) carve_buckets(c, b, pl.slots, pl.groups, kAttnTile);
+  } else {
+    a.delta = c.take<float>(pl.items * pl.G);
+    a.part_dq = c.take<float>(pl.slots * pl.G * d->head_dim);
+    carve_buckets(c, b, pl.slots, pl.groups, kAttnTile);
+    a.part_dkv = c.take<float>(b.max_tiles * pl.Cp * (d->head_dim + d->value_dim));
+  }
+}
+
+AttnRequests attn_requests(const pisa_attn_desc* d, const AttnPlan& pl, const void* indices,
+                           const int64_t* positions, int64_t pos_batch) {
+  AttnRequests r;
+  r.indices = indices;
+  r.index_bits = d->index_bits;
+  r.positions = positions;
+  r.pos_stride_batch = pos_batch;
+  r.topk = d->topk;
+  r.heads = d->key_heads;
+  r.tokens = d->query_tokens;
+  r.blocks = pl.M0;
+  r.block_size = d->block_size;
+  r.causal = d->causal ? 1 : 0;
+  return r;
+}
+
+void bind_buckets(AttnArgs& a, const Buckets& b) {
+  a.tile_group = b.tile_group;
+  a.tile_req = b.tile_req;
+  a.tile_off = b.tile_off;
+  a.counts = b.counts;
+  a.num_tiles = b.num_tiles;
+  a.tile = b.tile;
+}
+
+}  // namespace
+
+extern "C" size_t pisa_attention_workspace_size(const pisa_attn_desc* d, int32_t backward) {
+  AttnPlan pl;
+  if (plan_attn(d, pl)) return 0;
+  Carve c{nullptr, 0, 0};
+  AttnArgs a{};
+  Buckets b{};
+  carve_attn(d, pl, backward != 0, c, a, b);
+  return align_up(c.used, 256);
+}
+
+extern "C" int pisa_sparse_attention_fwd(const pisa_attn_desc* d, const void* q, const void* k,
+                                         const void* v, const void* indices,
+                                         const int64_t* positions, int64_t positions_stride_batch,
+                                         void* out, float* lse, float* out_f32, void* workspace,
+                                         size_t workspace_bytes, void* stream) {
+  AttnPlan pl;
+  int rc = plan_attn(d, pl);
+  if (rc) return rc;
+  if (!q || !k || !v || !positions || !out || !lse || (d->topk && !indices))
+    return fail(PISA_ERR_INVALID, "null tensor argument");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
+    return fail(PISA_ERR_UNSUPPORTED, "q, k, v and out must be 16-byte aligned");
+  AttnArgs a = attn_args(d, pl, q, k, v, indices, positions, positions_stride_batch);
+  rc = attn_check(a, d->dtype, false);
+  if (rc) return rc;
+  Carve c{static_cast<char*>(workspace), 0, workspace_bytes};
+  Buckets b{};
+  carve_attn(d, pl, false, c, a, b);
+  if ((c.used && !workspace) || !c.fits())
+    return fail(PISA_ERR_WORKSPACE, "attention forward needs %zu workspace bytes", c.used);
+  a.out = out;
+  a.out_f32 = out_f32;
+  a.lse_out = lse;
+  hipStream_t st = (hipStream_t)stream;
+  if (pl.grouped) {
+    rc = bucket_attn(attn_requests(d, pl, indices, positions, positions_stride_batch), pl.slots, b, st);
+    if (rc) return rc;
+    bind_buckets(a, b);
+  }
+  return launch_attn_fwd(d->dtype, a, pl.grouped, pl.slots, pl.items, st);
+}
+
+extern "C" int pisa_sparse_attention_bwd(const pisa_attn_desc* d, const void* q, const void* k,
+                                         const void* v, const void* indices,
+                                         const int64_t* positions, int64_t positions_stride_batch,
+                                         const void* out, const float* out_f32, const float* lse,
+                                         const void* grad_out, void* grad_q, void* grad_k,
+                                         void* grad_v, void* workspace, size_t workspace_bytes,
+                                         void* stream) {
+  AttnPlan pl;
+  int rc = plan_attn(d, pl);
+  if (rc) return rc;
+  if (!q || !k || !v || !positions || !out || !lse || !grad_out || !grad_q || !grad_k || !grad_v ||
+      (d->topk && !indices))
+    return fail(PISA_ERR_INVALID, "null tensor argument");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(grad_out))
+    return fail(PISA_ERR_UNSUPPORTED, "q, k, v and grad_out must be 16-byte aligned");
+  AttnArgs a = attn_args(d, pl, q, k, v, indices, positions, positions_stride_batch);
+  rc = attn_check(a, d->dtype, true);
+  if (rc) return rc;
+  Carve c{static_cast<char*>(workspace), 0, workspace_bytes};
+  Buckets b{};
+  carve_attn(d, pl, true, c, a, b);
+  if (!workspace || !c.fits())
+    return fail(PISA_ERR_WORKSPACE, "attention backward needs %zu workspace bytes", c.used);
+  a.out = const_cast<void*>(out);
+  a.out_f32 = const_cast<float*>(out_f32);
+  a.lse = lse;
+  a.dout = grad_out;
+  a.dq = grad_q;
+  a.dk = grad_k;
+  a.dv = grad_v;
+  // gradients are written contiguous [B, N, Hkv, D]
+  a.dk_token = (int64_t)d->key_heads * d->head_dim;
+  a.dk_batch = (int64_t)d->key_tokens * a.dk_token;
+  a.dv_token = (int64_t)d->key_heads * d->value_dim;
+  a.dv_batch = (int64_t)d->key_tokens * a.dv_token;
+  hipStream_t st = (hipStream_t)stream;
+  rc = bucket_attn(attn_requests(d, pl, indices, positions, positions_stride_batch), pl.slots, b, st);
+  if (rc) return rc;
+  bind_buckets(a, b);
+  return launch_attn_bwd(d->dtype, a, pl.groups, pl.items, st);
+}

@@ -1,0 +1,267 @@
+// Device-side building blocks shared by the PISA kernels (gfx950, wave64).
+//
+// * element types: fp32, fp16 (_Float16) and bf16 (raw bits) with float conversions;
+// * 16-lane DPP row reductions (a wave64 is four DPP rows of 16 lanes);
+// * MFMA 16x16 fragments for the three element types;
+// * the descending bitonic comparison network of the reference's selection
+//   (top_k_pyramid_torch.py:84-110), distributed over the lanes of one wave.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pisa {
+
+struct __attribute__((aligned(2))) bf16_t {
+  uint16_t bits;
+};
+typedef _Float16 f16_t;
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef short s4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+
+constexpr float kForced = 1.0e9f;    // sentinel of required blocks
+constexpr float kInvalid = -1.0e9f;  // sentinel of invalid / future blocks
+
+// ------------------------------------------------------------------ conversions
+
+__device__ __forceinline__ float to_f(float x) { return x; }
+__device__ __forceinline__ float to_f(f16_t x) { return (float)x; }
+__device__ __forceinline__ float to_f(bf16_t x) { return __uint_as_float(((uint32_t)x.bits) << 16); }
+
+template <typename T>
+__device__ __forceinline__ T from_f(float x);
+template <>
+__device__ __forceinline__ float from_f<float>(float x) { return x; }
+template <>
+__device__ __forceinline__ f16_t from_f<f16_t>(float x) { return (f16_t)x; }
+template <>
+__device__ __forceinline__ bf16_t from_f<bf16_t>(float x) {
+  uint32_t u = __float_as_uint(x);
+  bf16_t r;
+  if ((u & 0x7fffffffu) > 0x7f800000u) {
+    r.bits = (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
+  } else {
+    u += 0x7fffu + ((u >> 16) & 1u);        // round to nearest even
+    r.bits = (uint16_t)(u >> 16);
+  }
+  return r;
+}
+
+// Load N consecutive elements (16-byte, 8-byte or 4-byte aligned runs) as floats.
+template <int N>
+__device__ __forceinline__ void load_f(const float* p, float* out) {
+  if constexpr (N % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < N; i += 4) {
+      float4 v = *reinterpret_cast<const float4*>(p + i);
+      out[i] = v.x; out[i + 1] = v.y; out[i + 2] = v.z; out[i + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) out[i] = p[i];
+  }
+}
+
+__device__ __forceinline__ void unpack_bf16x2(uint32_t w, float& lo, float& hi) {
+  lo = __uint_as_float(w << 16);
+  hi = __uint_as_float(w & 0xffff0000u);
+}
+
+template <int N>
+__device__ __forceinline__ void load_f(const bf16_t* p, float* out) {
+  if constexpr (N % 8 == 0) {
+#pragma unroll
+    for (int i = 0; i < N; i += 8) {
+      uint4 v = *reinterpret_cast<const uint4*>(p + i);
+      unpack_bf16x2(v.x, out[i], out[i + 1]);
+      unpack_bf16x2(v.y, out[i + 2], out[i + 3]);
+      unpack_bf16x2(v.z, out[i + 4], out[i + 5]);
+      unpack_bf16x2(v.w, out[i + 6], out[i + 7]);
+    }
+  } else if constexpr (N % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < N; i += 4) {
+      uint2 v = *reinterpret_cast<const uint2*>(p + i);
+      unpack_bf16x2(v.x, out[i], out[i + 1]);
+      unpack_bf16x2(v.y, out[i + 2], out[i + 3]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) out[i] = to_f(p[i]);
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void load_f(const f16_t* p, float* out) {
+  if constexpr (N % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < N; i += 4) {
+      h4 v = *reinterpret_cast<const h4*>(p + i);
+      out[i] = (float)v[0]; out[i + 1] = (float)v[1];
+      out[i + 2] = (float)v[2]; out[i + 3] = (float)v[3];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) out[i] = (float)p[i];
+  }
+}
+
+// ------------------------------------------------------------------ lane reductions
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// All-reduce over each DPP row of 16 lanes with row rotations 8, 4, 2, 1.  Every
+// lane of the row ends with the identical (commutatively combined) value.
+__device__ __forceinline__ float row_sum16(float v) {
+  v += dpp_f<0x128>(v);
+  v += dpp_f<0x124>(v);
+  v += dpp_f<0x122>(v);
+  v += dpp_f<0x121>(v);
+  return v;
+}
+
+__device__ __forceinline__ float row_max16(float v) {
+  v = fmaxf(v, dpp_f<0x128>(v));
+  v = fmaxf(v, dpp_f<0x124>(v));
+  v = fmaxf(v, dpp_f<0x122>(v));
+  v = fmaxf(v, dpp_f<0x121>(v));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row_sum16(v);
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
+// ------------------------------------------------------------------ MFMA fragments
+//
+// For all three element types (E elements per lane, KS = 4*E per instruction):
+//   A fragment:  lane l holds A[row = l & 15][k = E*(l >> 4) + e],  e < E
+//   B fragment:  lane l holds B[k = E*(l >> 4) + e][col = l & 15]
+//   C/D:         lane l holds D[row = 4*(l >> 4) + i][col = l & 15], i < 4
+
+template <typename T>
+struct Mfma;
+
+template <>
+struct Mfma<bf16_t> {
+  static constexpr int E = 4;
+  static constexpr int KS = 16;
+  typedef s4 frag;
+  static __device__ __forceinline__ f4 mma(frag a, frag b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+  }
+  // E contiguous elements
+  static __device__ __forceinline__ frag load(const bf16_t* p) {
+    return *reinterpret_cast<const frag*>(p);
+  }
+  // E elements with a stride
+  static __device__ __forceinline__ frag gather(const bf16_t* p, int stride) {
+    frag f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) f[e] = (short)p[e * stride].bits;
+    return f;
+  }
+  static __device__ __forceinline__ frag make(const float* x) {
+    frag f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) f[e] = (short)from_f<bf16_t>(x[e]).bits;
+    return f;
+  }
+};
+
+template <>
+struct Mfma<f16_t> {
+  static constexpr int E = 4;
+  static constexpr int KS = 16;
+  typedef h4 frag;
+  static __device__ __forceinline__ f4 mma(frag a, frag b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ frag load(const f16_t* p) {
+    return *reinterpret_cast<const frag*>(p);
+  }
+  static __device__ __forceinline__ frag gather(const f16_t* p, int stride) {
+    frag f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) f[e] = p[e * stride];
+    return f;
+  }
+  static __device__ __forceinline__ frag make(const float* x) {
+    frag f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) f[e] = (f16_t)x[e];
+    return f;
+  }
+};
+
+template <>
+struct Mfma<float> {
+  static constexpr int E = 1;
+  static constexpr int KS = 4;
+  typedef float frag;
+  static __device__ __forceinline__ f4 mma(frag a, frag b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ frag load(const float* p) { return *p; }
+  static __device__ __forceinline__ frag gather(const float* p, int) { return *p; }
+  static __device__ __forceinline__ frag make(const float* x) { return x[0]; }
+};
+
+// ------------------------------------------------------------------ comparison network
+//
+// Element e of a network of width `width` (power of two, <= 64*J) lives in lane
+// e % 64, register e / 64.  The network is the reference's: for each stage
+// group = 2^x (all-descending when group == width) and distance group/2 .. 1,
+// the pair (e, e ^ distance) exchanges iff (left > right) != descending, so
+// equal scores exchange in descending groups and stay in ascending ones.
+template <int J>
+__device__ __forceinline__ void bitonic_desc(float (&s)[J], int (&id)[J], int width, int lane) {
+  for (int group = 2; group <= width; group <<= 1) {
+    for (int dist = group >> 1; dist > 0; dist >>= 1) {
+      if (dist >= 64) {
+        const int jd = dist >> 6;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+          if ((j & jd) == 0 && (j | jd) < J) {
+            const int j2 = j | jd;
+            const int e = j * 64 + lane;
+            const bool desc = (group == width) || ((e & group) != 0);
+            const float l = s[j], r = s[j2];
+            if ((l > r) != desc) {
+              s[j] = r; s[j2] = l;
+              const int t = id[j]; id[j] = id[j2]; id[j2] = t;
+            }
+          }
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+          const float ps = __shfl_xor(s[j], dist);
+          const int pid = __shfl_xor(id[j], dist);
+          const int e = j * 64 + lane;
+          const bool left = (e & dist) == 0;
+          const bool desc = (group == width) || ((e & group) != 0);
+          const float ls = left ? s[j] : ps;
+          const float rs = left ? ps : s[j];
+          if ((ls > rs) != desc) { s[j] = ps; id[j] = pid; }
+        }
+      }
+    }
+  }
+}
+
+__host__ __device__ __forceinline__ int next_pow2(int x) {
+  int p = 1;
+  while (p < x) p <<= 1;
+  return p;
+}
+
+}  // namespace pisa

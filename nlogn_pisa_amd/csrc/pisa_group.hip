@@ -1,0 +1,206 @@
+// Block-major request bucketing, built entirely on the device.
+//
+// A request is one (batch, token, kv head, slot) that needs one key block:
+// a scoreable leaf candidate (group_requests, grouping_triton.py:44-103) or a
+// visible selected block of sparse attention.  Requests are bucketed by
+// group = (batch * Hkv + head) * blocks + block and cut into tiles of at most
+// `tile` requests of one group, so a consumer loads each key block once per
+// tile.  Three launches, no host read of a count (the tile array is sized for
+// the worst case, ceil(slots / tile) + groups, as the reference does):
+//   count   - per-workgroup LDS histogram, one global atomic per non-empty bin;
+//   scan    - tiles per group, exclusive prefix sum, total tile count;
+//   scatter - LDS ranks plus one reserved global range per bin and workgroup.
+// Request order inside a group is unspecified; every consumer computes each
+// request independently of its tile-mates.
+
+#include "pisa_device.h"
+#include "pisa_internal.h"
+
+#include <algorithm>
+
+namespace pisa {
+
+constexpr int kLdsGroups = 16384;  // 64 KB of int32 bins
+constexpr int kBucketThreads = 256;
+constexpr int64_t kBucketChunk = 32768;
+
+struct LeafSrc {
+  LeafRequests r;
+  __device__ __forceinline__ bool get(int64_t slot, int& group) const {
+    if (!r.scoreable[slot]) return false;
+    const int blk = r.cand[slot];
+    const int64_t item = slot / r.width;
+    const int h = (int)(item % r.heads);
+    const int64_t b = item / ((int64_t)r.heads * r.tokens);
+    group = (int)((b * r.heads + h) * r.blocks + blk);
+    return true;
+  }
+};
+
+template <typename I>
+struct AttnSrc {
+  AttnRequests r;
+  __device__ __forceinline__ bool get(int64_t slot, int& group) const {
+    const int64_t blk = (int64_t) static_cast<const I*>(r.indices)[slot];
+    if (blk < 0 || blk >= r.blocks) return false;
+    const int64_t item = slot / r.topk;
+    const int h = (int)(item % r.heads);
+    const int64_t bt = item / r.heads;
+    const int t = (int)(bt % r.tokens);
+    const int64_t b = bt / r.tokens;
+    if (r.causal && blk * r.block_size > r.positions[b * r.pos_stride_batch + t]) return false;
+    group = (int)((b * r.heads + h) * r.blocks + blk);
+    return true;
+  }
+};
+
+__global__ void fill_f32_kernel(float* p, int64_t n, float v) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = v;
+}
+
+__global__ void fill_i32_kernel(int32_t* p, int64_t n, int32_t v) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = v;
+}
+
+template <typename Src>
+__global__ void __launch_bounds__(kBucketThreads) bucket_count_kernel(Src src, int64_t slots,
+                                                                      int groups, int32_t* counts) {
+  extern __shared__ int hist[];
+  const bool lds = groups <= kLdsGroups;
+  const int64_t begin = (int64_t)blockIdx.x * kBucketChunk;
+  const int64_t end = min(slots, begin + kBucketChunk);
+  if (lds) {
+    for (int g = threadIdx.x; g < groups; g += blockDim.x) hist[g] = 0;
+    __syncthreads();
+  }
+  for (int64_t s = begin + threadIdx.x; s < end; s += blockDim.x) {
+    int g;
+    if (src.get(s, g)) {
+      if (lds) atomicAdd(&hist[g], 1);
+      else atomicAdd(&counts[g], 1);
+    }
+  }
+  if (lds) {
+    __syncthreads();
+    for (int g = threadIdx.x; g < groups; g += blockDim.x)
+      if (hist[g]) atomicAdd(&counts[g], hist[g]);
+  }
+}
+
+__global__ void __launch_bounds__(1024) bucket_scan_kernel(const int32_t* counts, int64_t groups,
+                                                           int tile, int32_t* tile_off,
+                                                           int32_t* num_tiles) {
+  __shared__ int64_t part[1024];
+  const int tid = threadIdx.x;
+  const int64_t per = (groups + 1023) / 1024;
+  const int64_t begin = tid * per;
+  const int64_t end = min(groups, begin + per);
+  int64_t sum = 0;
+  for (int64_t g = begin; g < end; ++g) sum += (counts[g] + tile - 1) / tile;
+  part[tid] = sum;
+  __syncthreads();
+  for (int off = 1; off < 1024; off <<= 1) {
+    const int64_t v = tid >= off ? part[tid - off] : 0;
+    __syncthreads();
+    part[tid] += v;
+    __syncthreads();
+  }
+  int64_t run = part[tid] - sum;
+  for (int64_t g = begin; g < end; ++g) {
+    tile_off[g] = (int32_t)run;
+    run += (counts[g] + tile - 1) / tile;
+  }
+  if (tid == 1023) *num_tiles = (int32_t)part[1023];
+}
+
+template <typename Src>
+__global__ void __launch_bounds__(kBucketThreads) bucket_scatter_kernel(
+    Src src, int64_t slots, int groups, const int32_t* __restrict__ tile_off, int32_t* cursors,
+    int tile, int32_t* __restrict__ tile_group, int32_t* __restrict__ tile_req) {
+  extern __shared__ int hist[];
+  const bool lds = groups <= kLdsGroups;
+  const int64_t begin = (int64_t)blockIdx.x * kBucketChunk;
+  const int64_t end = min(slots, begin + kBucketChunk);
+  if (lds) {
+    for (int g = threadIdx.x; g < groups; g += blockDim.x) hist[g] = 0;
+    __syncthreads();
+    for (int64_t s = begin + threadIdx.x; s < end; s += blockDim.x) {
+      int g;
+      if (src.get(s, g)) atomicAdd(&hist[g], 1);
+    }
+    __syncthreads();
+    for (int g = threadIdx.x; g < groups; g += blockDim.x) {
+      const int c = hist[g];
+      if (c) hist[g] = atomicAdd(&cursors[g], c);
+    }
+    __syncthreads();
+  }
+  for (int64_t s = begin + threadIdx.x; s < end; s += blockDim.x) {
+    int g;
+    if (!src.get(s, g)) continue;
+    const int rank = lds ? atomicAdd(&hist[g], 1) : atomicAdd(&cursors[g], 1);
+    const int t = tile_off[g] + rank / tile;
+    const int within = rank % tile;
+    tile_req[(int64_t)t * tile + within] = (int32_t)s;
+    if (within == 0) tile_group[t] = g;
+  }
+}
+
+void carve_buckets(Carve& c, Buckets& b, int64_t slots, int64_t groups, int tile) {
+  b.groups = groups;
+  b.tile = tile;
+  b.max_tiles = (slots + tile - 1) / tile + groups;
+  b.counts = c.take<int32_t>(groups);
+  b.cursors = c.take<int32_t>(groups);
+  b.tile_off = c.take<int32_t>(groups);
+  b.num_tiles = c.take<int32_t>(1);
+  b.tile_group = c.take<int32_t>(b.max_tiles);
+  b.tile_req = c.take<int32_t>(b.max_tiles * tile);
+}
+
+static void fill_i32(int32_t* p, int64_t n, int32_t v, hipStream_t stream) {
+  if (n <= 0) return;
+  const int64_t blocks = std::min<int64_t>((n + 255) / 256, 4096);
+  PISA_TIMED("fill", stream, hipLaunchKernelGGL(fill_i32_kernel, dim3(blocks), dim3(256), 0, stream, p, n, v));
+}
+
+void fill_f32(float* p, int64_t n, float v, hipStream_t stream) {
+  if (n <= 0) return;
+  const int64_t blocks = std::min<int64_t>((n + 255) / 256, 4096);
+  PISA_TIMED("fill", stream, hipLaunchKernelGGL(fill_f32_kernel, dim3(blocks), dim3(256), 0, stream, p, n, v));
+}
+
+template <typename Src>
+static int run_buckets(const Src& src, int64_t slots, Buckets& b, hipStream_t stream) {
+  if (slots >= (int64_t)INT32_MAX || b.groups >= (int64_t)INT32_MAX)
+    return fail(PISA_ERR_UNSUPPORTED, "too many requests to bucket (%lld slots)", (long long)slots);
+  fill_i32(b.counts, b.groups, 0, stream);
+  fill_i32(b.cursors, b.groups, 0, stream);
+  fill_i32(b.num_tiles, 1, 0, stream);
+  if (slots == 0) return check_launch("bucket fill");
+  const int64_t grid = (slots + kBucketChunk - 1) / kBucketChunk;
+  const size_t lds = b.groups <= kLdsGroups ? (size_t)b.groups * sizeof(int) : 0;
+  PISA_TIMED("bucket_count", stream, hipLaunchKernelGGL((bucket_count_kernel<Src>), dim3(grid), dim3(kBucketThreads), lds, stream,
+                     src, slots, (int)b.groups, b.counts));
+  PISA_TIMED("bucket_scan", stream, hipLaunchKernelGGL(bucket_scan_kernel, dim3(1), dim3(1024), 0, stream, b.counts, b.groups,
+                     b.tile, b.tile_off, b.num_tiles));
+  PISA_TIMED("bucket_scatter", stream, hipLaunchKernelGGL((bucket_scatter_kernel<Src>), dim3(grid), dim3(kBucketThreads), lds, stream,
+                     src, slots, (int)b.groups, b.tile_off, b.cursors, b.tile, b.tile_group,
+                     b.tile_req));
+  return check_launch("bucket");
+}
+
+int bucket_leaf(const LeafRequests& src, int64_t slots, Buckets& b, hipStream_t stream) {
+  return run_buckets(LeafSrc{src}, slots, b, stream);
+}
+
+int bucket_attn(const AttnRequests& src, int64_t slots, Buckets& b, hipStream_t stream) {
+  if (src.index_bits == 64) return run_buckets(AttnSrc<int64_t>{src}, slots, b, stream);
+  return run_buckets(AttnSrc<int32_t>{src}, slots, b, stream);
+}
+
+}  // namespace pisa

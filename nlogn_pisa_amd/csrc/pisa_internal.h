@@ -1,0 +1,203 @@
+// Host-side helpers shared by the translation units of libpisa_hip.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/pisa_hip.h"
+
+namespace pisa {
+
+// Records a printf-style message as this thread's last error and returns `code`.
+int fail(int code, const char* fmt, ...);
+// Turns a pending launch error into PISA_ERR_LAUNCH.
+int check_launch(const char* what);
+
+inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+// Brackets one kernel launch with timing events while profiling is enabled
+// (pisa_profile.hip).
+class ProfScope {
+ public:
+  ProfScope(const char* name, hipStream_t stream);
+  ~ProfScope();
+
+ private:
+  const char* name_;
+  hipStream_t stream_;
+  hipEvent_t start_{}, stop_{};
+  bool armed_ = false;
+};
+
+#define PISA_TIMED(NAME, STREAM, ...)        \
+  do {                                       \
+    ::pisa::ProfScope pisa_scope_(NAME, STREAM); \
+    __VA_ARGS__;                             \
+  } while (0)
+
+// Bump allocator over a caller-provided workspace.
+struct Carve {
+  char* base;
+  size_t used;
+  size_t cap;
+  template <typename T>
+  T* take(size_t count) {
+    used = align_up(used, 256);
+    T* p = reinterpret_cast<T*>(base ? base + used : nullptr);
+    used += count * sizeof(T);
+    return p;
+  }
+  bool fits() const { return used <= cap; }
+};
+
+// Request bucketing by (batch, kv head, block).  Sizes of its buffers.
+struct Buckets {
+  int32_t* counts;      // [groups]
+  int32_t* cursors;     // [groups]
+  int32_t* tile_off;    // [groups]
+  int32_t* tile_group;  // [max_tiles]
+  int32_t* tile_req;    // [max_tiles * tile]
+  int32_t* num_tiles;   // [1]
+  int64_t groups;
+  int64_t max_tiles;
+  int tile;
+};
+
+void carve_buckets(Carve& c, Buckets& b, int64_t slots, int64_t groups, int tile);
+
+// Sources of bucketed requests.
+struct LeafRequests {
+  const int32_t* cand;      // [B,T,Hkv,W]
+  const uint8_t* scoreable; // [B,T,Hkv,W]
+  int32_t width, heads, tokens, blocks;
+};
+
+struct AttnRequests {
+  const void* indices;      // [B,T,Hkv,K] int32 or int64
+  int32_t index_bits;
+  const int64_t* positions;
+  int64_t pos_stride_batch;
+  int32_t topk, heads, tokens, blocks, block_size, causal;
+};
+
+int bucket_leaf(const LeafRequests& src, int64_t slots, Buckets& b, hipStream_t stream);
+int bucket_attn(const AttnRequests& src, int64_t slots, Buckets& b, hipStream_t stream);
+
+int dtype_size(int dtype);
+// Compute units of the current device (cached per device).
+int device_cus();
+// Largest dynamic LDS allocation of one workgroup on the current device.
+int device_lds_limit();
+// Lets `kernel` take `bytes` of dynamic LDS (above the 64 KB default).
+void allow_lds(const void* kernel, size_t bytes);
+
+// ------------------------------------------------------------------ kernel arguments
+
+struct RouteArgs {
+  const void* q;
+  int64_t q_batch, q_token;
+  const void* summary;
+  int64_t sum_batch;
+  const void* key;
+  int64_t key_batch, key_token;
+  const int64_t* positions;
+  int64_t pos_batch;
+  int T, Hkv, G, D, N;
+  int C, branching, topk, top, first_width, method, force_first, force_recent;
+  int fused;
+  float scale;
+  int offsets[PISA_MAX_LEVELS];
+  int lengths[PISA_MAX_LEVELS];
+  int32_t* cand;
+  uint8_t* scoreable;
+  int64_t* out;
+  int32_t* trace;
+};
+
+struct FinalArgs {
+  const int32_t* cand;
+  const uint8_t* scoreable;
+  const float* scores;
+  const int64_t* positions;
+  int64_t pos_batch;
+  int64_t items;
+  int T, Hkv, W, K, C, M0, force_first, force_recent, top;
+  int64_t* out;
+  int32_t* trace;
+};
+
+struct MaskArgs {
+  const int32_t* cand;
+  const int64_t* positions;
+  int64_t pos_batch;
+  int64_t items;
+  int T, Hkv, W, K, C, M0, force_first, force_recent, method;
+  uint8_t* scoreable;
+};
+
+struct LeafArgs {
+  const void* q;
+  int64_t q_batch, q_token;
+  const void* src;           // raw keys, or leaf means for PISA1
+  int64_t src_batch, src_row;
+  int T, Hkv, G, Gp, D, src_rows, C, W, M0, method;
+  float scale;
+  const int32_t* tile_group;
+  const int32_t* tile_req;
+  const int32_t* tile_off;
+  const int32_t* counts;
+  const int32_t* num_tiles;
+  int tile;
+  float* scores;
+};
+
+struct AttnArgs {
+  const void* q;
+  int64_t q_batch, q_token;
+  const void* k;
+  int64_t k_batch, k_token;
+  const void* v;
+  int64_t v_batch, v_token;
+  const void* indices;
+  int index_bits;
+  const int64_t* positions;
+  int64_t pos_batch;
+  int T, Hkv, G, Gp, D, Dv, N, K, C, M0, causal;
+  float scale;
+  // request tiles (pisa_group.hip)
+  const int32_t* tile_group;
+  const int32_t* tile_req;
+  const int32_t* tile_off;
+  const int32_t* counts;
+  const int32_t* num_tiles;
+  int tile;
+  // forward
+  float* part_o;   // [slots * G, Dv]
+  float* part_ml;  // [slots * G, 2]
+  void* out;       // O [B,T,Hq,Dv] (written by the forward, read by the backward)
+  float* out_f32;  // optional float32 O (forward output, backward input)
+  float* lse_out;  // [B,T,Hq]
+  // backward
+  const float* lse;
+  const void* dout;
+  float* delta;     // [B,T,Hq]
+  float* part_dq;   // [slots * G, D]
+  float* part_dkv;  // [tiles, Cp, D + Dv]
+  void* dq;
+  void* dk;
+  void* dv;
+  int64_t dk_batch, dk_token, dv_batch, dv_token;
+};
+
+int launch_route(int dtype, const RouteArgs& a, int64_t items, int threads, hipStream_t stream);
+int launch_final(const FinalArgs& a, hipStream_t stream);
+int launch_scoreable(const MaskArgs& a, hipStream_t stream);
+int launch_leaf(int dtype, const LeafArgs& a, hipStream_t stream);
+int attn_check(const AttnArgs& a, int dtype, bool backward);
+int launch_attn_fwd(int dtype, const AttnArgs& a, bool grouped, int64_t slots, int64_t items,
+                    hipStream_t stream);
+int launch_attn_bwd(int dtype, const AttnArgs& a, int64_t groups, int64_t items, hipStream_t stream);
+void fill_f32(float* p, int64_t n, float v, hipStream_t stream);
+
+}  // namespace pisa

@@ -1,0 +1,248 @@
+// Key pyramid: valid-count mean pooling (kernel 1) and the host-side geometry.
+//
+// Level 0 is the mean of each C-token block of K, the tail block dividing by
+// its real count (mean_pooling_torch.py:7-14); level l+1 is the mean of b
+// level-l nodes (mean_pooling.py:45-52, b = 2 there).  Sums are exact: bf16 and
+// fp16 inputs are summed in float64, then divided, rounded once to float32
+// and once to the storage dtype, so the result does not depend on the order in
+// which lanes combine (the reference's float32 sums do, in their last bit).
+//
+// One workgroup owns one output row (a block of one batch) across all heads:
+// lane c handles VEC consecutive elements of the Hkv*D row, so a wavefront reads
+// 64*16 contiguous bytes per input row (coalesced, HBM-bound).
+
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "pisa_device.h"
+#include "pisa_internal.h"
+
+namespace pisa {
+
+static thread_local char g_error[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list args;
+  va_start(args, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, args);
+  va_end(args);
+  return code;
+}
+
+int check_launch(const char* what) {
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(PISA_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(err));
+  return PISA_OK;
+}
+
+int dtype_size(int dtype) {
+  switch (dtype) {
+    case PISA_F32: return 4;
+    case PISA_F16: return 2;
+    case PISA_BF16: return 2;
+    default: return 0;
+  }
+}
+
+int device_cus() {
+  static thread_local int cached_device = -1;
+  static thread_local int cached_cus = 256;
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) return cached_cus;
+  if (device != cached_device) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && cus > 0)
+      cached_cus = cus;
+    cached_device = device;
+  }
+  return cached_cus;
+}
+
+int device_lds_limit() {
+  static thread_local int cached_device = -1;
+  static thread_local int cached_lds = 65536;
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) return cached_lds;
+  if (device != cached_device) {
+    int lds = 0;
+    if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device) == hipSuccess &&
+        lds > 0)
+      cached_lds = lds;
+    cached_device = device;
+  }
+  return cached_lds;
+}
+
+void allow_lds(const void* kernel, size_t bytes) {
+  if (bytes > 65536)
+    (void)hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+}
+
+template <typename T, int VEC>
+__global__ void __launch_bounds__(256) pool_kernel(const T* __restrict__ src, int64_t src_batch,
+                                                   int64_t src_row, int rows, T* __restrict__ dst,
+                                                   int64_t dst_batch, int64_t dst_row, int size,
+                                                   int row_elems) {
+  const int out_row = blockIdx.x;
+  const int b = blockIdx.y;
+  const int first = out_row * size;
+  const int count = min(size, rows - first);
+  const T* base = src + b * src_batch + (int64_t)first * src_row;
+  T* out = dst + b * dst_batch + (int64_t)out_row * dst_row;
+  const int chunks = row_elems / VEC;
+  for (int c = threadIdx.x; c < chunks; c += blockDim.x) {
+    double acc[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] = 0.0;
+    const T* p = base + c * VEC;
+    int r = 0;
+    for (; r + 4 <= count; r += 4) {
+      float v0[VEC], v1[VEC], v2[VEC], v3[VEC];
+      load_f<VEC>(p + (int64_t)(r + 0) * src_row, v0);
+      load_f<VEC>(p + (int64_t)(r + 1) * src_row, v1);
+      load_f<VEC>(p + (int64_t)(r + 2) * src_row, v2);
+      load_f<VEC>(p + (int64_t)(r + 3) * src_row, v3);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        acc[e] += (double)v0[e];
+        acc[e] += (double)v1[e];
+        acc[e] += (double)v2[e];
+        acc[e] += (double)v3[e];
+      }
+    }
+    for (; r < count; ++r) {
+      float v[VEC];
+      load_f<VEC>(p + (int64_t)r * src_row, v);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc[e] += (double)v[e];
+    }
+    const double inv = (double)count;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) out[c * VEC + e] = from_f<T>((float)(acc[e] / inv));
+  }
+}
+
+template <typename T>
+static int launch_pool(const void* src, int64_t src_batch, int64_t src_row, int batch, int rows,
+                       int row_elems, int size, void* dst, int64_t dst_batch, int64_t dst_row,
+                       hipStream_t stream) {
+  const int out_rows = (rows + size - 1) / size;
+  if (out_rows == 0 || batch == 0) return PISA_OK;
+  const int vec = (16 / (int)sizeof(T));
+  dim3 grid(out_rows, batch);
+  const T* s = static_cast<const T*>(src);
+  T* d = static_cast<T*>(dst);
+  const bool aligned = (row_elems % vec == 0) && (src_row % vec == 0) && (src_batch % vec == 0) &&
+                       (dst_row % vec == 0) && (dst_batch % vec == 0) &&
+                       ((uintptr_t)src % 16 == 0) && ((uintptr_t)dst % 16 == 0);
+  if (aligned) {
+    const int threads = min(256, max(64, (row_elems / vec + 63) / 64 * 64));
+    PISA_TIMED("pool", stream, hipLaunchKernelGGL((pool_kernel<T, 16 / sizeof(T)>), grid, dim3(threads), 0, stream, s,
+                       src_batch, src_row, rows, d, dst_batch, dst_row, size, row_elems));
+  } else {
+    const int threads = min(256, max(64, (row_elems + 63) / 64 * 64));
+    PISA_TIMED("pool", stream, hipLaunchKernelGGL((pool_kernel<T, 1>), grid, dim3(threads), 0, stream, s, src_batch, src_row,
+                       rows, d, dst_batch, dst_row, size, row_elems));
+  }
+  return check_launch("mean_pool");
+}
+
+static int pool_dispatch(int dtype, const void* src, int64_t src_batch, int64_t src_row, int batch,
+                         int rows, int row_elems, int size, void* dst, int64_t dst_batch,
+                         int64_t dst_row, hipStream_t stream) {
+  switch (dtype) {
+    case PISA_F32:
+      return launch_pool<float>(src, src_batch, src_row, batch, rows, row_elems, size, dst,
+                                dst_batch, dst_row, stream);
+    case PISA_F16:
+      return launch_pool<f16_t>(src, src_batch, src_row, batch, rows, row_elems, size, dst,
+                                dst_batch, dst_row, stream);
+    case PISA_BF16:
+      return launch_pool<bf16_t>(src, src_batch, src_row, batch, rows, row_elems, size, dst,
+                                 dst_batch, dst_row, stream);
+    default:
+      return fail(PISA_ERR_INVALID, "unknown dtype %d", dtype);
+  }
+}
+
+}  // namespace pisa
+
+using namespace pisa;
+
+extern "C" const char* pisa_last_error(void) { return g_error; }
+
+extern "C" int pisa_abi_version(void) { return PISA_ABI_VERSION; }
+
+extern "C" int pisa_routing_geometry(int32_t blocks, int32_t topk, int32_t branching, int32_t* top,
+                                     int32_t* first_width) {
+  if (blocks < 1 || topk < 1 || branching < 2)
+    return fail(PISA_ERR_INVALID, "routing geometry needs blocks, topk >= 1 and branching >= 2");
+  int t = 0;
+  int64_t b = blocks;
+  while (b > topk) {
+    const int64_t parent = (b + branching - 1) / branching;
+    if (parent < topk || parent == b) break;
+    b = parent;
+    ++t;
+  }
+  int64_t w = b > topk ? b : topk;
+  int64_t p = 1;
+  while (p < w) p <<= 1;
+  *top = t;
+  *first_width = (int32_t)(p > 16 ? p : 16);
+  return PISA_OK;
+}
+
+extern "C" int pisa_pyramid_layout(int32_t keys, int32_t block_size, int32_t branching,
+                                   int32_t max_level, int32_t* levels, int32_t* offsets,
+                                   int32_t* lengths) {
+  if (keys < 1 || block_size < 1 || branching < 2)
+    return fail(PISA_ERR_INVALID, "pyramid layout needs keys, block_size >= 1, branching >= 2");
+  int n = 0;
+  int size = (keys + block_size - 1) / block_size;
+  int offset = 0;
+  while (true) {
+    if (n >= PISA_MAX_LEVELS) return fail(PISA_ERR_UNSUPPORTED, "more than %d levels", PISA_MAX_LEVELS);
+    offsets[n] = offset;
+    lengths[n] = size;
+    offset += size;
+    ++n;
+    if (size <= 1 || (max_level >= 0 && n > max_level)) break;
+    size = (size + branching - 1) / branching;
+  }
+  *levels = n;
+  return PISA_OK;
+}
+
+extern "C" int pisa_mean_pool(const void* src, int64_t src_stride_batch, int64_t src_stride_row,
+                              int32_t batch, int32_t rows, int32_t heads, int32_t dim, int32_t size,
+                              void* dst, int64_t dst_stride_batch, int64_t dst_stride_row,
+                              int32_t dtype, void* stream) {
+  if (size < 1) return fail(PISA_ERR_INVALID, "pool size must be positive");
+  if (batch < 0 || rows < 0 || heads < 1 || dim < 1) return fail(PISA_ERR_INVALID, "bad pool shape");
+  return pool_dispatch(dtype, src, src_stride_batch, src_stride_row, batch, rows, heads * dim, size,
+                       dst, dst_stride_batch, dst_stride_row, (hipStream_t)stream);
+}
+
+extern "C" int pisa_build_pyramid(const void* keys, int64_t k_stride_batch, int64_t k_stride_token,
+                                  int32_t batch, int32_t key_tokens, int32_t heads, int32_t dim,
+                                  int32_t block_size, int32_t branching, int32_t max_level,
+                                  void* storage, int64_t storage_stride_batch, int32_t dtype,
+                                  void* stream) {
+  int32_t levels, offsets[PISA_MAX_LEVELS], lengths[PISA_MAX_LEVELS];
+  int rc = pisa_pyramid_layout(key_tokens, block_size, branching, max_level, &levels, offsets,
+                               lengths);
+  if (rc) return rc;
+  const int row = heads * dim;
+  const int es = dtype_size(dtype);
+  if (!es) return fail(PISA_ERR_INVALID, "unknown dtype %d", dtype);
+  char* base = static_cast<char*>(storage);
+  rc = pool_dispatch(dtype, keys, k_stride_batch, k_stride_token, batch, key_tokens, row,
+                     block_size, base, storage_stride_batch, row, (hipStream_t)stream);
+  for (int l = 1; l < levels && rc == PISA_OK; ++l) {
+    rc = pool_dispatch(dtype, base + (int64_t)offsets[l - 1] * row * es, storage_stride_batch, row,
+                       batch, lengths[l - 1], row, branching, base + (int64_t)offsets[l] * row * es,
+                       storage_stride_batch, row, (hipStream_t)stream);
+  }
+  return rc;
+}

@@ -1,0 +1,178 @@
+"""GPU parity of pooling and block selection against the CPU oracle and the
+reference's golden vectors.
+
+Bar: pooled summaries bit-exact; selected ids bit-exact including slot order,
+except rows whose first diverging level swaps ids with oracle scores closer
+than 1e-4 x the row's largest real score (``tests/parity.py``).
+"""
+
+import os
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from parity import adjudicate, structured_qkv, to_gpu
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+METHODS = ("pisa", "pisa1", "pisa2")
+
+
+@pytest.fixture(scope="module")
+def P():
+    import nlogn_pisa_amd
+    nlogn_pisa_amd._lib.library()   # the HIP library must load: no fallback
+    return nlogn_pisa_amd
+
+
+@pytest.mark.parametrize("dtype", ["fp32", "bf16", "fp16"])
+@pytest.mark.parametrize("size", [2, 4, 16, 64])
+def test_mean_pool_bit_exact(P, dtype, size):
+    print(f"mean_pool dtype={dtype} size={size}", flush=True)
+    _, k = structured_qkv(1, 2, 1000, 4, 3, 64, dtype, value=False)
+    out = P.mean_pool(to_gpu(k, dtype), size).float().cpu().numpy()
+    np.testing.assert_array_equal(out, O.mean_pool(k, size, dtype))
+
+
+@pytest.mark.parametrize("branching", [2, 4, 8])
+def test_build_pyramid_bit_exact(P, branching):
+    print(f"build_pyramid b={branching}", flush=True)
+    _, k = structured_qkv(2, 1, 4000, 4, 2, 128, "bf16", value=False)
+    levels = P.build_pyramid(to_gpu(k, "bf16"), 64, branching=branching)
+    ref = O.build_pyramid(k, 64, branching, None, "bf16")
+    assert len(levels) == len(ref)
+    for mine, want in zip(levels, ref):
+        np.testing.assert_array_equal(mine.float().cpu().numpy(), want)
+
+
+def _run_select(P, q, k, dtype, method, block, topk, ff, fr, offset, schedule, branching=2):
+    qg, kg = to_gpu(q, dtype), to_gpu(k, dtype)
+    ids, trace = P.selection.select_blocks_traced(
+        qg, kg, method, block, topk, query_offset=offset, force_first=ff, force_recent=fr,
+        routing_schedule=schedule, branching=branching)
+    return ids.cpu().numpy(), trace.cpu().numpy()
+
+
+def _check_against(q, k, dtype, method, block, topk, ff, fr, offset, branching, ids, trace,
+                   expected=None, tokens=None):
+    """Compare GPU ids with ``expected`` (default: the oracle) and adjudicate mismatches."""
+    batch, tq = q.shape[:2]
+    pos = O.query_positions(batch, tq, k.shape[1], offset)
+    levels = O.build_pyramid(k, block, branching, None, dtype)
+    if expected is None:
+        expected = O.pyramid_select(q, k, method, block, topk, pos, ff, fr, levels,
+                                    branching=branching, tokens=tokens)
+    if tokens is not None:
+        ids, trace = ids[:, tokens], trace[:, tokens]
+    if np.array_equal(ids, expected):
+        return 0
+    toks = np.arange(tq) if tokens is None else np.asarray(tokens)
+    _, otrace = O.pyramid_select(q, k, method, block, topk, pos, ff, fr, levels,
+                                 branching=branching, tokens=toks, trace=True)
+    heads = ids.shape[2]
+    rows, mism, exempt, failures = adjudicate(
+        ids.reshape(-1, heads, ids.shape[-1]), trace.reshape(-1, heads, *trace.shape[-2:]),
+        expected.reshape(-1, heads, ids.shape[-1]), otrace)
+    assert not failures, f"{len(failures)} non-exempt mismatches of {rows} rows, e.g. {failures[:5]}"
+    return exempt
+
+
+def _golden_cases():
+    sel = np.load(os.path.join(GOLDEN, "select_b2.npz"))
+    for c in range(int(sel["count"])):
+        si, isbf, mi, topk, ff, fr, block, off = (int(x) for x in sel[f"s{c}_meta"])
+        dt = "bf16" if isbf else "fp32"
+        yield dict(q=sel[f"in{si}{dt}_q"], k=sel[f"in{si}{dt}_k"], dtype=dt, method=METHODS[mi],
+                   topk=topk, ff=bool(ff), fr=fr, block=block, offset=None if off < 0 else off,
+                   out=sel[f"s{c}_out"].astype(np.int64), case=c)
+
+
+@pytest.mark.parametrize("schedule", ["auto", "grouped", "fused"])
+def test_select_matches_reference_goldens(P, schedule):
+    """The reference's own Torch-path ids (branching 2, depth >= 2), slot order included."""
+    exempt = 0
+    for g in _golden_cases():
+        print(f"golden case {g['case']} {schedule}", flush=True)
+        ids, trace = _run_select(P, g["q"], g["k"], g["dtype"], g["method"], g["block"],
+                                 g["topk"], g["ff"], g["fr"], g["offset"], schedule)
+        exempt += _check_against(g["q"], g["k"], g["dtype"], g["method"], g["block"], g["topk"],
+                                 g["ff"], g["fr"], g["offset"], 2, ids, trace, expected=g["out"])
+    print("tie-exempt rows:", exempt)
+
+
+CONFIGS = [
+    # name, B, T(N), Hq, Hkv, D, C, b, K, method, ff, fr, dtype, needles, tq
+    ("cfg0", 1, 4096, 4, 4, 64, 64, 4, 8, "pisa", True, 1, "fp32", 0.0, None),
+    ("cfg0-pisa1", 1, 4096, 4, 4, 64, 64, 4, 8, "pisa1", True, 1, "fp32", 0.0, None),
+    ("cfg1-slice", 1, 4096, 16, 4, 128, 64, 4, 16, "pisa", True, 1, "bf16", 0.0, None),
+    ("cfg2-slice", 1, 8192, 8, 2, 128, 64, 4, 32, "pisa2", True, 2, "bf16", 0.01, None),
+    ("cfg4-slice", 1, 16384, 16, 2, 128, 128, 8, 16, "pisa", True, 1, "bf16", 0.0, None),
+    ("refbench", 1, 8192, 32, 2, 64, 64, 2, 8, "pisa", True, 2, "bf16", 0.0, None),
+    ("fp16-b2", 2, 2048, 8, 2, 64, 32, 2, 8, "pisa2", False, 1, "fp16", 0.0, None),
+    ("suffix", 1, 4096, 8, 2, 64, 64, 4, 8, "pisa", True, 2, "bf16", 0.0, 100),
+]
+
+
+@pytest.mark.parametrize("cfg", CONFIGS, ids=[c[0] for c in CONFIGS])
+def test_select_matches_oracle(P, cfg):
+    name, batch, length, qh, kh, dim, block, b, topk, method, ff, fr, dtype, needles, tq = cfg
+    print(f"select {name}", flush=True)
+    q, k = structured_qkv(zlib.crc32(name.encode()) % 1000, batch, length, qh, kh, dim, dtype, needles=needles,
+                          value=False, tq=tq)
+    offset = None
+    tokens = np.unique(np.linspace(0, q.shape[1] - 1, 256).astype(np.int64))
+    for schedule in ("auto", "fused") if method != "pisa1" else ("auto",):
+        ids, trace = _run_select(P, q, k, dtype, method, block, topk, ff, fr, offset, schedule, b)
+        _check_against(q, k, dtype, method, block, topk, ff, fr, offset, b, ids, trace,
+                       tokens=tokens)
+
+
+@pytest.mark.parametrize("method", ["pisa", "pisa2"])
+def test_decode_fused_selection(P, method):
+    """Tq = 1 against a long cache (the reference's fused decode route)."""
+    print(f"decode {method}", flush=True)
+    q, k = structured_qkv(7, 4, 32768, 32, 8, 128, "bf16", needles=0.01, value=False, tq=1)
+    ids, trace = _run_select(P, q, k, "bf16", method, 64, 32, True, 1, None, "auto", 4)
+    _check_against(q, k, "bf16", method, 64, 32, True, 1, None, 4, ids, trace)
+    assert (ids[..., :2] >= 0).all()
+
+
+def test_select_is_deterministic(P):
+    q, k = structured_qkv(8, 1, 16384, 16, 4, 128, "bf16", value=False)
+    qg, kg = to_gpu(q, "bf16"), to_gpu(k, "bf16")
+    a = P.select_blocks(qg, kg, "pisa", 64, 16, force_recent=1, branching=4)
+    b = P.select_blocks(qg, kg, "pisa", 64, 16, force_recent=1, branching=4)
+    assert torch.equal(a, b)
+    assert a.dtype == torch.int64 and tuple(a.shape) == (1, 16384, 4, 16)
+
+
+@pytest.mark.parametrize("method", METHODS)
+def test_leaf_scores_match_oracle(P, method):
+    print(f"leaf_scores {method}", flush=True)
+    q, k = structured_qkv(9, 2, 2048, 8, 2, 64, "bf16", value=False)
+    rng = np.random.default_rng(0)
+    cand = rng.integers(-1, 34, size=(2, 2048, 2, 40)).astype(np.int32)
+    pos = O.query_positions(2, 2048, 2048)
+    qg, kg = to_gpu(q, "bf16"), to_gpu(k, "bf16")
+    out = P.leaf_scores(qg, kg, torch.from_numpy(cand).cuda(), 64, method,
+                        torch.from_numpy(pos).cuda(), 8, True, 1).cpu().numpy()
+    ref = O.leaf_scores(q, k, cand, 64, method, pos, 8, True, 1,
+                        leaf_means=O.mean_pool(k, 64, "bf16"))
+    assert np.array_equal(np.isneginf(out), np.isneginf(ref))
+    fin = np.isfinite(ref)
+    np.testing.assert_allclose(out[fin], ref[fin], rtol=2e-5, atol=2e-5)
+
+
+def test_packed_documents(P):
+    """cu_seqlens: document-local ids, equal to selecting each document alone."""
+    q, k = structured_qkv(10, 1, 3000, 8, 2, 64, "bf16", value=False)
+    qg, kg = to_gpu(q, "bf16"), to_gpu(k, "bf16")
+    cu = torch.tensor([0, 1000, 1700, 3000], dtype=torch.int32, device="cuda")
+    out = P.select_blocks(qg, kg, "pisa", 64, 8, cu_seqlens=cu, force_recent=1)
+    for s, e in ((0, 1000), (1000, 1700), (1700, 3000)):
+        alone = P.select_blocks(qg[:, s:e], kg[:, s:e], "pisa", 64, 8, force_recent=1)
+        assert torch.equal(out[:, s:e], alone)
