@@ -41,7 +41,21 @@ def parse():
     ap.add_argument("--tokens", type=int, default=None, help="config 4 length")
     ap.add_argument("--cpu-sample", type=int, default=384, help="oracle tokens timed on the CPU")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only run a plain 1 GiB device copy (calibrates rocprofv3 FETCH/WRITE_SIZE)")
     return ap.parse_args()
+
+
+def copy_probe():
+    """A plain copy of exactly 1 GiB, three times, for counter calibration."""
+    import torch
+    src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes": src.numel() * 4, "launches": 3}), flush=True)
+    return 0
 
 
 # ---------------------------------------------------------------- work counts
@@ -146,6 +160,8 @@ def main():
         print(f"bench.py runs on exactly one GPU (this build has no multi-GPU path); "
               f"got --gpus {args.gpus}", file=sys.stderr)
         return 2
+    if args.copy_probe:
+        return copy_probe()
     import torch
     import nlogn_pisa_amd as P
     from nlogn_pisa_amd import _lib

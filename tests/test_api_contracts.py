@@ -1,0 +1,112 @@
+"""Host-side contracts of the operator API (no GPU needed): the reference's
+ValueError messages (``top_k_pyramid.py:47-59``, ``validation.py``,
+``sparse_attn.py:28-34``, ``mean_pooling.py:22-25``), auto-schedule and
+geometry helpers, and deterministic synthetic inputs."""
+
+import pytest
+import torch
+
+import nlogn_pisa_amd as P
+import oracle as O
+from nlogn_pisa_amd.inputs import config, make_inputs
+
+
+def qk(tq=128, n=128, qh=4, kh=2, d=64, dtype=torch.float32):
+    return torch.zeros(1, tq, qh, d, dtype=dtype), torch.zeros(1, n, kh, d, dtype=dtype)
+
+
+@pytest.mark.parametrize("kwargs,message", [
+    (dict(method="nope"), "method must be bsa, pisa1, pisa2 or pisa"),
+    (dict(backend="cuda"), "backend must be torch, triton or auto"),
+    (dict(leaf_tile=3), "leaf_tile must be 1, 2 or 4"),
+    (dict(routing_schedule="x"), "routing_schedule must be auto, grouped or fused"),
+    (dict(topk=0), "positive block_size/topk and nonnegative force_recent required"),
+    (dict(force_recent=0), "causal pyramid routing requires force_recent >= 1"),
+])
+def test_select_blocks_reference_errors(kwargs, message):
+    q, k = qk()
+    with pytest.raises(ValueError, match=message):
+        P.select_blocks(q, k, **kwargs)
+
+
+def test_validate_qkv_reference_errors():
+    q, k = qk()
+    with pytest.raises(ValueError, match=r"q and k must have shape \[batch, tokens, heads, head_dim\]"):
+        P.validate_qkv(q[0], k)
+    with pytest.raises(ValueError, match="q and k must share batch size and head dimension"):
+        P.validate_qkv(q, k[..., :32])
+    with pytest.raises(ValueError, match="whole number of query heads per KV head"):
+        P.validate_qkv(torch.zeros(1, 8, 3, 64), k)
+    with pytest.raises(ValueError, match="q and k must share a floating dtype and device"):
+        P.validate_qkv(q, k.double())
+    with pytest.raises(ValueError, match="v must share k's batch, length, heads, dtype and device"):
+        P.validate_qkv(q, k, k[:, :5])
+
+
+def test_query_positions_contract():
+    q, k = qk(tq=4, n=10)
+    assert P.query_positions(q, k).tolist() == [[6, 7, 8, 9]]
+    assert P.query_positions(q, k, 2).tolist() == [[2, 3, 4, 5]]
+    with pytest.raises(ValueError, match="queries must refer to positions within their key sequence"):
+        P.query_positions(q, k, 7)
+    with pytest.raises(ValueError, match="one offset per batch element"):
+        P.query_positions(q, k, torch.tensor([1, 2]))
+    assert (P.query_positions(q, k).numpy() == O.query_positions(1, 4, 10)).all()
+
+
+def test_packed_query_contracts():
+    q, k = qk(tq=10, n=10)
+    cu = torch.tensor([0, 4, 10])
+    assert P.packed_queries(q, k, cu) == [(0, 4, 0, 4, 0), (4, 10, 4, 10, 0)]
+    qd = torch.zeros(1, 2, 4, 64)
+    assert P.packed_queries(qd, k, cu) == [(0, 1, 0, 4, 3), (1, 2, 4, 10, 5)]
+    with pytest.raises(ValueError, match="cu_seqlens must start at zero and end at the key length"):
+        P.sequence_slices(torch.tensor([0, 4]), 10)
+    with pytest.raises(ValueError, match="packed sequences must be nonempty and strictly ordered"):
+        P.sequence_slices(torch.tensor([0, 4, 4, 10]), 10)
+    with pytest.raises(ValueError, match="packed inputs require batch size one"):
+        P.packed_queries(torch.zeros(2, 10, 4, 64), torch.zeros(2, 10, 2, 64), cu)
+
+
+def test_sparse_attention_reference_errors():
+    q, k = qk()
+    v = torch.zeros_like(k)
+    idx = torch.zeros(1, 128, 2, 4, dtype=torch.long)
+    with pytest.raises(ValueError, match=r"indices must have shape \[B,Tq,Hkv,K\]"):
+        P.sparse_attention(q, k, v, idx[:, :5])
+    with pytest.raises(ValueError, match="indices must be integers on the query device"):
+        P.sparse_attention(q, k, v, idx.float())
+    with pytest.raises(ValueError, match="invalid block_size or attention backend"):
+        P.sparse_attention(q, k, v, idx, backend="xla")
+
+
+def test_cpu_tensors_are_rejected_not_computed():
+    """The product has no CPU path: a CPU tensor is an error, never a fallback."""
+    q, k = qk()
+    with pytest.raises(ValueError, match="runs on a ROCm GPU"):
+        P.select_blocks(q, k, force_recent=1)
+    with pytest.raises(ValueError, match="runs on a ROCm GPU"):
+        P.sparse_attention(q, k, torch.zeros_like(k), torch.zeros(1, 128, 2, 4, dtype=torch.long))
+    with pytest.raises(ValueError, match="runs on a ROCm GPU"):
+        P.mean_pool(k, 64)
+    with pytest.raises(ValueError, match="pool size must be positive"):
+        P.mean_pool(k, 0)
+
+
+def test_routing_geometry_mirror():
+    for b in (2, 4, 8):
+        for blocks in range(1, 3000, 7):
+            assert P.routing_geometry(blocks, 16, b) == O.routing_geometry(blocks, 16, b)
+
+
+def test_synthetic_inputs_are_deterministic():
+    w = config(0)
+    a = make_inputs(w, "cpu")
+    b = make_inputs(w, "cpu")
+    assert all(torch.equal(x, y) for x, y in zip(a, b))
+    q, k, v = a
+    assert q.shape == (1, 4096, 4, 64) and k.shape == (1, 4096, 4, 64) and q.dtype == torch.float32
+    # keys carry the per-64-token offsets: block means differ much more than noise alone
+    means = k.reshape(1, 64, 64, 4, 64).mean(2)
+    assert means.std() > 0.35
+    assert config(2).needles == 0.01 and config(3).per_sequence_seed
