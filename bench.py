@@ -60,6 +60,17 @@ def copy_probe():
 
 # ---------------------------------------------------------------- work counts
 
+def tile_count(w, valid, ids):
+    """Tiles of <= TILE requests per (batch, kv head, block) group."""
+    import torch
+    blocks = math.ceil(w.keys / w.block_size)
+    dev = ids.device
+    b = torch.arange(w.batch, device=dev)[:, None, None, None]
+    h = torch.arange(w.key_heads, device=dev)[None, None, :, None]
+    group = ((b * w.key_heads + h) * blocks + ids)[valid]
+    per = torch.bincount(group, minlength=w.batch * w.key_heads * blocks)
+    return int(((per + TILE - 1) // TILE).sum())
+
 def selection_counts(P, w, q, k, positions):
     """Exact scoreable request counts per level (from the per-level selections)."""
     import torch
@@ -94,11 +105,7 @@ def selection_counts(P, w, q, k, positions):
             scoreable &= (valid.sum(-1, keepdim=True) > w.topk)
         counts[level] = int(scoreable.sum())
         if level == 0 and w.method != "pisa1":
-            heads = torch.arange(w.key_heads, device=q.device)[None, None, :, None]
-            batches = torch.arange(w.batch, device=q.device)[:, None, None, None]
-            group = ((batches * w.key_heads + heads) * blocks + cand)[scoreable]
-            per = torch.bincount(group, minlength=w.batch * w.key_heads * blocks)
-            tiles = int(((per + TILE - 1) // TILE).sum())
+            tiles = tile_count(w, scoreable, cand)
     return ids, counts, tiles, top, first
 
 
@@ -112,12 +119,7 @@ def attention_counts(w, ids, positions):
     keys = torch.minimum(torch.minimum(torch.full_like(ids, w.block_size), w.keys - start),
                          pos - start + 1).clamp(min=0)
     pairs = int(torch.where(vis, keys, 0).sum())
-    heads = torch.arange(w.key_heads, device=ids.device)[None, None, :, None]
-    batches = torch.arange(w.batch, device=ids.device)[:, None, None, None]
-    group = ((batches * w.key_heads + heads) * blocks + ids)[vis]
-    per = torch.bincount(group, minlength=w.batch * w.key_heads * blocks)
-    tiles = int(((per + TILE - 1) // TILE).sum())
-    return int(vis.sum()), tiles, pairs
+    return int(vis.sum()), tile_count(w, vis, ids), pairs
 
 
 # ---------------------------------------------------------------- CPU baseline
@@ -222,6 +224,7 @@ def main():
         requests, attn_tiles, pairs = attention_counts(w, ids, positions)
 
     e = q.element_size()
+    pe = 4 if e == 4 else 2    # partial rows: fp16 for 16-bit inputs, fp32 for fp32
     G = w.query_heads // w.key_heads
     D = w.head_dim
     items = w.batch * w.tokens * w.key_heads
@@ -239,10 +242,10 @@ def main():
         "final": {"bound": "hbm", "bytes": items * (width * 9 + w.topk * 8)},
         "attn_fwd": {"bound": "hbm",
                      "bytes": attn_tiles * 2 * w.block_size * D * e
-                     + requests * G * (D * e + (D + 2) * 4),
+                     + requests * G * (D * e + D * pe + 4),
                      "flops": 4 * D * G * pairs},
         "attn_combine": {"bound": "hbm",
-                         "bytes": requests * G * (D + 2) * 4 + items * G * (D * e + 4)},
+                         "bytes": requests * G * (D * pe + 4) + items * G * (D * e + 4)},
         "pool": {"bound": "hbm", "bytes": w.batch * w.keys * w.key_heads * D * e},
     }
     dominant = max(per_step, key=per_step.get)

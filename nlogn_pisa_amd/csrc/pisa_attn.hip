@@ -107,11 +107,42 @@ __device__ void stage_kv(const AttnArgs& a, int b, int h, int64_t blk, int rows,
 template <typename T>
 constexpr bool kSplit = sizeof(T) == 2;
 
+// Partial rows are stored normalized (o / l) in fp16 for 16-bit inputs (their
+// magnitude is bounded by max|v|) and in fp32 for fp32 inputs; each partial
+// also keeps its own log-sum-exp m + ln l in fp32.
+template <typename T>
+struct PartialT {
+  typedef f16_t type;
+};
+template <>
+struct PartialT<float> {
+  typedef float type;
+};
+
+// Per-wave LDS of the forward unit: P (hi and lo rows) then the output rows.
+template <typename T>
+struct FwdWaveLds {
+  int ldp, ldo;
+  size_t p_bytes, bytes;
+  __host__ __device__ FwdWaveLds(int Cp, int Dv) {
+    typedef typename PartialT<T>::type PT;
+    ldp = Cp + 16 / (int)sizeof(T);
+    ldo = Dv + 16 / (int)sizeof(PT);
+    p_bytes = ((size_t)32 * ldp * sizeof(T) + 15) / 16 * 16;
+    bytes = p_bytes + ((size_t)16 * ldo * sizeof(PT) + 15) / 16 * 16;
+  }
+};
+
 template <typename T, typename ReqFn>
 __device__ void fwd_unit(const AttnArgs& a, ReqFn req_slot, int nreq, int unit, int b, int h,
-                         int64_t blk, int rows, const T* ks, int ldk, const T* vt, int ldv, T* ps,
-                         int ldp, int Cp, int lane) {
+                         int64_t blk, int rows, const T* ks, int ldk, const T* vt, int ldv,
+                         char* wave_lds, int Cp, int lane) {
+  typedef typename PartialT<T>::type PT;
+  const FwdWaveLds<T> W(Cp, a.Dv);
+  const int ldp = W.ldp, ldo = W.ldo;
+  T* ps = reinterpret_cast<T*>(wave_lds);
   T* ps_lo = ps + 16 * ldp;
+  PT* os = reinterpret_cast<PT*>(wave_lds + W.p_bytes);
   using M = Mfma<T>;
   const int col = lane & 15, grp = lane >> 4;
   const int NT = Cp / 16;
@@ -185,7 +216,10 @@ __device__ void fwd_unit(const AttnArgs& a, ReqFn req_slot, int nreq, int unit, 
     lrow[i] = row_sum16(l);
   }
   wave_lds_sync();
-  // O = P V over Cp keys
+  // O = P V over Cp keys, normalized by l, staged in LDS as the partial's type
+  float inv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) inv[i] = lrow[i] > 0.f ? 1.f / lrow[i] : 0.f;
   const int DT = a.Dv / 16;
   for (int dt = 0; dt < DT; ++dt) {
     f4 o = f4{0.f, 0.f, 0.f, 0.f};
@@ -195,15 +229,22 @@ __device__ void fwd_unit(const AttnArgs& a, ReqFn req_slot, int nreq, int unit, 
       if constexpr (kSplit<T>) o = M::mma(M::load(ps_lo + col * ldp + k0 + M::E * grp), fb, o);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (valid_r[i]) {
-        const int64_t row = slot_r[i] * a.G + gh_r[i];
-        a.part_o[row * a.Dv + dt * 16 + col] = o[i];
-        if (dt == 0 && col == 0) {
-          a.part_ml[row * 2] = mrow[i];
-          a.part_ml[row * 2 + 1] = lrow[i];
-        }
-      }
+    for (int i = 0; i < 4; ++i) os[(4 * grp + i) * ldo + dt * 16 + col] = (PT)(o[i] * inv[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (valid_r[i] && col == 0) a.part_lse[slot_r[i] * a.G + gh_r[i]] = mrow[i] + __logf(lrow[i]);
+  wave_lds_sync();
+  // 16-byte stores of whole partial rows (row = request x head)
+  constexpr int V = 16 / sizeof(PT);
+  const int chunks = a.Dv / V;
+  for (int idx = lane; idx < 16 * chunks; idx += 64) {
+    const int r = idx / chunks, c = idx % chunks;
+    const int rho_r = unit * 16 + r;
+    const int rq_r = rho_r / Gp, g_r = rho_r % Gp;
+    if (rq_r < nreq && g_r < a.G) {
+      PT* dst = static_cast<PT*>(a.part_o) + (req_slot(rq_r) * a.G + g_r) * a.Dv + c * V;
+      *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(os + r * ldo + c * V);
     }
   }
   wave_lds_sync();
@@ -220,12 +261,11 @@ __global__ void __launch_bounds__(256) attn_fwd_grouped_kernel(AttnArgs a) {
   const int Cp = (a.C + 15) / 16 * 16;
   const int ldk = a.D + 16 / (int)sizeof(T);
   const int ldv = Cp + 16 / (int)sizeof(T);
-  const int ldp = Cp + 16 / (int)sizeof(T);
   T* ks = reinterpret_cast<T*>(smem);
   T* vt = ks + Cp * ldk;
-  T* pbase = vt + a.Dv * ldv;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  T* ps = pbase + wave * 32 * ldp;
+  char* wave_lds = smem + (size_t)(Cp * ldk + a.Dv * ldv) * sizeof(T) +
+                   wave * FwdWaveLds<T>(Cp, a.Dv).bytes;
   const int ntiles = *a.num_tiles;
   for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
     const int g = a.tile_group[tile];
@@ -241,7 +281,7 @@ __global__ void __launch_bounds__(256) attn_fwd_grouped_kernel(AttnArgs a) {
     const TileReqs reqs{a.tile_req + (int64_t)tile * a.tile};
     const int units = (nreq * a.Gp + 15) / 16;
     for (int u = wave; u < units; u += (int)(blockDim.x >> 6))
-      fwd_unit<T>(a, reqs, nreq, u, b, h, blk, rows, ks, ldk, vt, ldv, ps, ldp, Cp, lane);
+      fwd_unit<T>(a, reqs, nreq, u, b, h, blk, rows, ks, ldk, vt, ldv, wave_lds, Cp, lane);
   }
 }
 
@@ -262,69 +302,76 @@ __global__ void __launch_bounds__(64) attn_fwd_direct_kernel(AttnArgs a, int64_t
   const int Cp = (a.C + 15) / 16 * 16;
   const int ldk = a.D + 16 / (int)sizeof(T);
   const int ldv = Cp + 16 / (int)sizeof(T);
-  const int ldp = Cp + 16 / (int)sizeof(T);
   T* ks = reinterpret_cast<T*>(smem);
   T* vt = ks + Cp * ldk;
-  T* ps = vt + a.Dv * ldv;
+  char* wave_lds = smem + (size_t)(Cp * ldk + a.Dv * ldv) * sizeof(T);
   const int rows = (int)min((int64_t)a.C, (int64_t)a.N - blk * a.C);
   stage_kv<T>(a, ri.b, ri.h, blk, rows, ks, ldk, vt, ldv, Cp, threadIdx.x, blockDim.x);
   __syncthreads();
   const int units = (a.Gp + 15) / 16;
   for (int u = 0; u < units; ++u)
-    fwd_unit<T>(a, OneReq{slot}, 1, u, ri.b, ri.h, blk, rows, ks, ldk, vt, ldv, ps, ldp, Cp,
+    fwd_unit<T>(a, OneReq{slot}, 1, u, ri.b, ri.h, blk, rows, ks, ldk, vt, ldv, wave_lds, Cp,
                 threadIdx.x & 63);
 }
 
-// Merge the K partials of each (batch, token, query head) in slot order.
-// One wave per (batch, token, kv head); lanes over the value dims.
+// Merge the K partials of each (batch, token, query head) in slot order:
+// M = max lse_s, w_s = e^(lse_s - M), O = sum w_s o_s / sum w_s, LSE = M + ln sum w_s.
+// One wave per (batch, token, kv head); a lane owns one 16-byte chunk of one
+// head's row, so each slot's [G, Dv] partial block is one coalesced read.
 template <typename T>
 __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a, int64_t items) {
+  typedef typename PartialT<T>::type PT;
+  constexpr int V = 16 / sizeof(PT);
   const int lane = threadIdx.x & 63;
   const int64_t item = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (item >= items) return;
   const RowInfo ri = row_info(a, item * a.K);
-  for (int gh = 0; gh < a.G; ++gh) {
+  const int chunks = a.Dv / V;
+  const int work = a.G * chunks;
+  for (int base = 0; base < work; base += 64) {
+    const int idx = min(base + lane, work - 1);
+    const bool writer = base + lane < work;
+    const int g = idx / chunks, c = idx % chunks;
     float big = -INFINITY;
+#pragma unroll 8
     for (int s = 0; s < a.K; ++s) {
       const int64_t slot = item * a.K + s;
-      if (!slot_visible(a, slot_block(a, slot), ri.pos)) continue;
-      big = fmaxf(big, a.part_ml[(slot * a.G + gh) * 2]);
+      if (slot_visible(a, slot_block(a, slot), ri.pos))
+        big = fmaxf(big, a.part_lse[slot * a.G + g]);
     }
-    const int64_t orow = (item * a.G + gh);  // == ((b*T + t)*Hq + h*G + gh)
-    T* out = static_cast<T*>(a.out) + orow * a.Dv;
-    float* out32 = a.out_f32 ? a.out_f32 + orow * a.Dv : nullptr;
-    if (big == -INFINITY) {
-      for (int d = lane; d < a.Dv; d += 64) {
-        out[d] = from_f<T>(0.f);
-        if (out32) out32[d] = 0.f;
-      }
-      if (lane == 0) a.lse_out[orow] = -INFINITY;
-      continue;
-    }
+    float acc[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) acc[v] = 0.f;
     float total = 0.f;
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};  // Dv <= 256
-    for (int s = 0; s < a.K; ++s) {
-      const int64_t slot = item * a.K + s;
-      if (!slot_visible(a, slot_block(a, slot), ri.pos)) continue;
-      const int64_t prow = slot * a.G + gh;
-      const float w = __expf(a.part_ml[prow * 2] - big);
-      total += w * a.part_ml[prow * 2 + 1];
+    if (big != -INFINITY) {
+#pragma unroll 4
+      for (int s = 0; s < a.K; ++s) {
+        const int64_t slot = item * a.K + s;
+        if (!slot_visible(a, slot_block(a, slot), ri.pos)) continue;
+        const float w = __expf(a.part_lse[slot * a.G + g] - big);
+        total += w;
+        union {
+          uint4 u;
+          PT e[V];
+        } x;
+        x.u = *reinterpret_cast<const uint4*>(static_cast<const PT*>(a.part_o) +
+                                              (slot * a.G + g) * a.Dv + c * V);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int d = lane + 64 * j;
-        if (d < a.Dv) acc[j] = fmaf(w, a.part_o[prow * a.Dv + d], acc[j]);
+        for (int v = 0; v < V; ++v) acc[v] = fmaf(w, (float)x.e[v], acc[v]);
       }
     }
-    const float inv = 1.f / total;
+    if (!writer) continue;
+    const float inv = total > 0.f ? 1.f / total : 0.f;
+    const int64_t orow = item * a.G + g;  // == ((b*T + t)*Hq + h*G + g)
+    T* out = static_cast<T*>(a.out) + orow * a.Dv + c * V;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int d = lane + 64 * j;
-      if (d < a.Dv) {
-        out[d] = from_f<T>(acc[j] * inv);
-        if (out32) out32[d] = acc[j] * inv;
-      }
+    for (int v = 0; v < V; ++v) out[v] = from_f<T>(acc[v] * inv);
+    if (a.out_f32) {
+      float* out32 = a.out_f32 + orow * a.Dv + c * V;
+#pragma unroll
+      for (int v = 0; v < V; ++v) out32[v] = acc[v] * inv;
     }
-    if (lane == 0) a.lse_out[orow] = big + __logf(total);
+    if (c == 0) a.lse_out[orow] = big == -INFINITY ? -INFINITY : big + __logf(total);
   }
 }
 
@@ -644,7 +691,9 @@ __global__ void __launch_bounds__(256) attn_dq_combine_kernel(AttnArgs a, int64_
 static size_t fwd_lds(const AttnArgs& a, int es, int waves) {
   const int Cp = (a.C + 15) / 16 * 16;
   const int pad = 16 / es;
-  return (size_t)es * ((size_t)Cp * (a.D + pad) + (size_t)a.Dv * (Cp + pad) + (size_t)waves * 32 * (Cp + pad));
+  const size_t kv = (size_t)es * ((size_t)Cp * (a.D + pad) + (size_t)a.Dv * (Cp + pad));
+  const size_t wave = es == 4 ? FwdWaveLds<float>(Cp, a.Dv).bytes : FwdWaveLds<bf16_t>(Cp, a.Dv).bytes;
+  return kv + (size_t)waves * wave;
 }
 
 static size_t bwd_lds(const AttnArgs& a, int es) { return bwd_layout(a.C, a.D, a.Dv, es).total; }

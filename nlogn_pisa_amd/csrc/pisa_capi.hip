@@ -378,8 +378,9 @@ AttnArgs attn_args(const pisa_attn_desc* d, const AttnPlan& pl, const void* q, c
 void carve_attn(const pisa_attn_desc* d, const AttnPlan& pl, bool backward, Carve& c, AttnArgs& a,
                 Buckets& b) {
   if (!backward) {
-    a.part_o = c.take<float>(pl.slots * pl.G * d->value_dim);
-    a.part_ml = c.take<float>(pl.slots * pl.G * 2);
+    const size_t part_elem = d->dtype == PISA_F32 ? 4 : 2;
+    a.part_o = c.take<char>(pl.slots * pl.G * d->value_dim * part_elem);
+    a.part_lse = c.take<float>(pl.slots * pl.G);
     if (pl.grouped) carve_buckets(c, b, pl.slots, pl.groups, kAttnTile);
   } else {
     a.delta = c.take<float>(pl.items * pl.G);

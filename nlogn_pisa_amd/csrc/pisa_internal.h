@@ -173,8 +173,8 @@ struct AttnArgs {
   const int32_t* num_tiles;
   int tile;
   // forward
-  float* part_o;   // [slots * G, Dv]
-  float* part_ml;  // [slots * G, 2]
+  void* part_o;     // [slots * G, Dv] normalized partial rows (fp16, or fp32 for fp32 inputs)
+  float* part_lse;  // [slots * G] log-sum-exp of each partial
   void* out;       // O [B,T,Hq,Dv] (written by the forward, read by the backward)
   float* out_f32;  // optional float32 O (forward output, backward input)
   float* lse_out;  // [B,T,Hq]
