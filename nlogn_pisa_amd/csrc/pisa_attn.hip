@@ -314,6 +314,316 @@ __global__ void __launch_bounds__(64) attn_fwd_direct_kernel(AttnArgs a, int64_t
                 threadIdx.x & 63);
 }
 
+// ------------------------------------------------------------------ forward, transposed tiles
+//
+// The path for D == Dv in {16, 32, 64, 128}.  S^T = K Q^T leaves in lane
+// (grp = l >> 4, col = l & 15) the scores of row `col` against keys
+// 16 mt + 4 grp + i (i < 4); P^T in that layout is already the B operand of
+// O^T = V^T P^T, so P never leaves registers.  The reduction index of S^T is
+// permuted so that lane group grp covers dimensions [grp D/4, (grp+1) D/4) of
+// the row, and the A rows of each O^T tile are permuted (row r of dv tile dt
+// is value (r >> 2) D/4 + 4 dt + (r & 3)) so that lane group grp ends with
+// values [grp D/4, (grp+1) D/4) of its row: a lane loads one contiguous
+// quarter of a query row and stores one contiguous quarter of a partial row.
+// Per-request bookkeeping (query row offset, position, slot) is computed once
+// per tile into LDS, and each wave loads the next unit's query rows while it
+// computes the current one.
+
+template <typename T, int HD, int NTM = 8>
+struct FwdShape {
+  static constexpr int E = sizeof(T) == 4 ? 1 : ((HD / 4) % 8 == 0 ? 8 : 4);
+  typedef MfmaOp<T, E> Op;
+  typedef typename Op::frag frag;
+  static constexpr int QL = HD / 4;                 // row elements per lane group
+  static constexpr int DS = QL / E;                 // reduction steps of S^T
+  static constexpr int NDT = HD / 16;               // dv tiles of O^T
+  static constexpr int KQ = E == 8 ? 32 : 16;       // key padding granularity
+  static constexpr int MAXK = NTM * 4 / E;          // P V steps at NTM key tiles
+  static constexpr int PAD = 16 / (int)sizeof(T);   // 16-byte LDS row padding
+};
+
+// LDS of one tile: K block [Cq][HD + PAD], V^T [HD][Cq + PAD], then per request
+// the query row offset (int64), position (int64) and slot (int32).
+struct TileLds {
+  int Cq, ldk, ldv;
+  size_t k_off, v_off, q_off, pos_off, slot_off, bytes;
+};
+
+template <typename T, int HD>
+__host__ __device__ inline TileLds tile_lds(int C, int tile) {
+  typedef FwdShape<T, HD> S;
+  TileLds L;
+  L.Cq = (C + S::KQ - 1) / S::KQ * S::KQ;
+  L.ldk = HD + S::PAD;
+  L.ldv = L.Cq + S::PAD;
+  size_t off = 0;
+  L.k_off = off;
+  off += (size_t)L.Cq * L.ldk * sizeof(T);
+  L.v_off = off;
+  off += (size_t)HD * L.ldv * sizeof(T);
+  off = (off + 15) / 16 * 16;
+  L.q_off = off;
+  off += (size_t)tile * 8;
+  L.pos_off = off;
+  off += (size_t)tile * 8;
+  L.slot_off = off;
+  off += (size_t)tile * 4;
+  L.bytes = (off + 15) / 16 * 16;
+  return L;
+}
+
+// Stage the K block row-major and the V block transposed, zero from `rows` up
+// to Cq keys.  16-bit V^T is written two keys per 32-bit word with consecutive
+// lanes on consecutive key pairs.
+template <typename T, int HD>
+__device__ void stage_tile(const AttnArgs& a, int b, int h, int64_t blk, int rows, T* ks, T* vt,
+                           const TileLds& L, int tid, int nthr) {
+  constexpr int vec = 16 / (int)sizeof(T);
+  constexpr int vpr = HD / vec;
+  const T* kb = static_cast<const T*>(a.k) + (int64_t)b * a.k_batch + blk * a.C * a.k_token +
+                (int64_t)h * HD;
+  const T* vb = static_cast<const T*>(a.v) + (int64_t)b * a.v_batch + blk * a.C * a.v_token +
+                (int64_t)h * HD;
+  for (int idx = tid; idx < L.Cq * vpr; idx += nthr) {
+    const int r = idx / vpr, c = (idx % vpr) * vec;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (r < rows) v = *reinterpret_cast<const uint4*>(kb + (int64_t)r * a.k_token + c);
+    *reinterpret_cast<uint4*>(ks + r * L.ldk + c) = v;
+  }
+  if constexpr (sizeof(T) == 2) {
+    const int pairs = L.Cq / 2;
+    for (int idx = tid; idx < pairs * vpr; idx += nthr) {
+      const int r = (idx % pairs) * 2, c = (idx / pairs) * vec;
+      union {
+        uint4 u;
+        uint16_t e[8];
+      } v0, v1;
+      v0.u = make_uint4(0, 0, 0, 0);
+      v1.u = make_uint4(0, 0, 0, 0);
+      if (r < rows) v0.u = *reinterpret_cast<const uint4*>(vb + (int64_t)r * a.v_token + c);
+      if (r + 1 < rows) v1.u = *reinterpret_cast<const uint4*>(vb + (int64_t)(r + 1) * a.v_token + c);
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        *reinterpret_cast<uint32_t*>(vt + (c + e) * L.ldv + r) = (uint32_t)v0.e[e] | ((uint32_t)v1.e[e] << 16);
+    }
+  } else {
+    for (int idx = tid; idx < L.Cq * vpr; idx += nthr) {
+      const int r = idx % L.Cq, c = (idx / L.Cq) * vec;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (r < rows) v = *reinterpret_cast<const float4*>(vb + (int64_t)r * a.v_token + c);
+      float* vf = reinterpret_cast<float*>(vt);
+      vf[(c + 0) * L.ldv + r] = v.x;
+      vf[(c + 1) * L.ldv + r] = v.y;
+      vf[(c + 2) * L.ldv + r] = v.z;
+      vf[(c + 3) * L.ldv + r] = v.w;
+    }
+  }
+}
+
+// A fragment of V^T for P V step kk: row `vrow` (a permuted dv), the keys whose
+// probabilities lane group grp holds in that step.
+template <typename T, int E>
+__device__ __forceinline__ typename MfmaOp<T, E>::frag load_vt(const T* vrow, int kk, int grp) {
+  typename MfmaOp<T, E>::frag f;
+  if constexpr (E == 8) {
+    const uint2 lo = *reinterpret_cast<const uint2*>(vrow + kk * 32 + 4 * grp);
+    const uint2 hi = *reinterpret_cast<const uint2*>(vrow + kk * 32 + 16 + 4 * grp);
+    const uint4 u = make_uint4(lo.x, lo.y, hi.x, hi.y);
+    __builtin_memcpy(&f, &u, 16);
+  } else if constexpr (E == 4) {
+    f = *reinterpret_cast<const typename MfmaOp<T, E>::frag*>(vrow + kk * 16 + 4 * grp);
+  } else {
+    f = vrow[(kk >> 2) * 16 + 4 * grp + (kk & 3)];
+  }
+  return f;
+}
+
+// The 16-row units of a tile (row = request x Gp + head), units wave, wave +
+// nwaves, ...: partial rows o / l (PartialT) and their log-sum-exp.  NTM bounds
+// the key tiles (Cq <= 16 NTM).
+template <typename T, int HD, int NTM>
+__device__ void fwd_tile_units(const AttnArgs& a, const TileLds& L, const T* ks, const T* vt,
+                               const int64_t* mq, const int64_t* mpos, const int32_t* mslot,
+                               int nreq, int64_t blk, int rows, int wave, int nwaves, int lane) {
+  typedef FwdShape<T, HD, NTM> S;
+  typedef typename S::Op Op;
+  typedef typename S::frag frag;
+  typedef typename PartialT<T>::type PT;
+  constexpr int E = S::E, QL = S::QL, DS = S::DS, NDT = S::NDT;
+  const int col = lane & 15, grp = lane >> 4;
+  const int NT = L.Cq / 16;     // key tiles, <= NTM
+  const int NK = NT * 4 / E;    // P V steps
+  const int Gp = a.Gp;
+  const int units = (nreq * Gp + 15) / 16;
+  const T* q = static_cast<const T*>(a.q);
+
+  frag qf[DS];
+  {
+    const int rho = wave * 16 + col, rq = rho / Gp, gh = rho % Gp;
+    if (wave < units && rq < nreq && gh < a.G)
+      load_frags(q + mq[rq] + (int64_t)gh * HD + QL * grp, qf);
+    else
+      zero_frags(qf);
+  }
+  for (int u = wave; u < units; u += nwaves) {
+    // next unit's query rows
+    frag qn[DS];
+    {
+      const int un = u + nwaves;
+      const int rho = un * 16 + col, rq = rho / Gp, gh = rho % Gp;
+      if (un < units && rq < nreq && gh < a.G)
+        load_frags(q + mq[rq] + (int64_t)gh * HD + QL * grp, qn);
+      else
+        zero_frags(qn);
+    }
+    // S^T = K Q^T
+    f4 s[NTM];
+#pragma unroll
+    for (int mt = 0; mt < NTM; ++mt) {
+      s[mt] = f4{0.f, 0.f, 0.f, 0.f};
+      if (mt < NT) {
+        frag kf[DS];
+        load_frags(ks + (mt * 16 + col) * L.ldk + QL * grp, kf);
+#pragma unroll
+        for (int d = 0; d < DS; ++d) s[mt] = Op::mma(kf[d], qf[d], s[mt]);
+      }
+    }
+    // softmax statistics of row `col` (lane groups hold disjoint keys)
+    const int rho = u * 16 + col, rq = rho / Gp, gh = rho % Gp;
+    const bool valid = rq < nreq && gh < a.G;
+    const int64_t pos = valid ? mpos[rq] : -1;
+    float m = -INFINITY;
+#pragma unroll
+    for (int mt = 0; mt < NTM; ++mt) {
+      if (mt < NT) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = mt * 16 + 4 * grp + i;
+          const bool ok = valid && key < rows && (!a.causal || blk * a.C + key <= pos);
+          const float z = ok ? s[mt][i] * a.scale : -INFINITY;
+          s[mt][i] = z;
+          m = fmaxf(m, z);
+        }
+      }
+    }
+    m = fmaxf(m, __shfl_xor(m, 16));
+    m = fmaxf(m, __shfl_xor(m, 32));
+    const float safe = m == -INFINITY ? 0.f : m;
+    float l = 0.f;
+#pragma unroll
+    for (int mt = 0; mt < NTM; ++mt) {
+      if (mt < NT) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float p = __expf(s[mt][i] - safe);
+          s[mt][i] = p;
+          l += p;
+        }
+      }
+    }
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    // O^T = V^T P^T, P entering as hi + lo for 16-bit types
+    f4 o[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) o[dt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < S::MAXK; ++kk) {
+      if (kk < NK) {
+        frag ph, pl;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const int lam = kk * E + e;
+          const float x = s[lam >> 2][lam & 3];
+          const float r = Op::set(ph, e, x);
+          if constexpr (kSplit<T>) Op::set(pl, e, x - r);
+        }
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+          const T* vrow = vt + (QL * (col >> 2) + 4 * dt + (col & 3)) * L.ldv;
+          const frag vf = load_vt<T, E>(vrow, kk, grp);
+          o[dt] = Op::mma(vf, ph, o[dt]);
+          if constexpr (kSplit<T>) o[dt] = Op::mma(vf, pl, o[dt]);
+        }
+      }
+    }
+    if (valid) {
+      const float inv = l > 0.f ? 1.f / l : 0.f;
+      PT vals[QL];
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) vals[4 * dt + i] = (PT)(o[dt][i] * inv);
+      const int64_t prow = (int64_t)mslot[rq] * a.G + gh;
+      store_vals(static_cast<PT*>(a.part_o) + prow * HD + QL * grp, vals);
+      if (grp == 0) a.part_lse[prow] = m + __logf(l);
+    }
+#pragma unroll
+    for (int d = 0; d < DS; ++d) qf[d] = qn[d];
+  }
+}
+
+template <typename T, int HD, int NTM>
+__global__ void __launch_bounds__(256, 2) attn_fwd_tile_kernel(AttnArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const TileLds L = tile_lds<T, HD>(a.C, a.tile);
+  T* ks = reinterpret_cast<T*>(smem + L.k_off);
+  T* vt = reinterpret_cast<T*>(smem + L.v_off);
+  int64_t* mq = reinterpret_cast<int64_t*>(smem + L.q_off);
+  int64_t* mpos = reinterpret_cast<int64_t*>(smem + L.pos_off);
+  int32_t* mslot = reinterpret_cast<int32_t*>(smem + L.slot_off);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ntiles = *a.num_tiles;
+  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int g = a.tile_group[tile];
+    const int64_t blk = g % a.M0;
+    const int bh = g / a.M0;
+    const int h = bh % a.Hkv, b = bh / a.Hkv;
+    const int start = (tile - a.tile_off[g]) * a.tile;
+    const int nreq = min(a.tile, a.counts[g] - start);
+    const int rows = (int)min((int64_t)a.C, (int64_t)a.N - blk * a.C);
+    const int32_t* reqs = a.tile_req + (int64_t)tile * a.tile;
+    __syncthreads();
+    for (int i = tid; i < nreq; i += blockDim.x) {
+      const int32_t slot = reqs[i];
+      const RowInfo ri = row_info(a, slot);
+      mq[i] = (int64_t)ri.b * a.q_batch + (int64_t)ri.t * a.q_token + (int64_t)h * a.G * HD;
+      mpos[i] = ri.pos;
+      mslot[i] = slot;
+    }
+    stage_tile<T, HD>(a, b, h, blk, rows, ks, vt, L, tid, blockDim.x);
+    __syncthreads();
+    fwd_tile_units<T, HD, NTM>(a, L, ks, vt, mq, mpos, mslot, nreq, blk, rows, wave,
+                               (int)(blockDim.x >> 6), lane);
+  }
+}
+
+// One request (slot) per workgroup of one wave (decode and other short queries).
+template <typename T, int HD, int NTM>
+__global__ void __launch_bounds__(64, 2) attn_fwd_tile_direct_kernel(AttnArgs a, int64_t slots) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int64_t slot = blockIdx.x;
+  if (slot >= slots) return;
+  const RowInfo ri = row_info(a, slot);
+  const int64_t blk = slot_block(a, slot);
+  if (!slot_visible(a, blk, ri.pos)) return;
+  const TileLds L = tile_lds<T, HD>(a.C, 1);
+  T* ks = reinterpret_cast<T*>(smem + L.k_off);
+  T* vt = reinterpret_cast<T*>(smem + L.v_off);
+  int64_t* mq = reinterpret_cast<int64_t*>(smem + L.q_off);
+  int64_t* mpos = reinterpret_cast<int64_t*>(smem + L.pos_off);
+  int32_t* mslot = reinterpret_cast<int32_t*>(smem + L.slot_off);
+  if (threadIdx.x == 0) {
+    mq[0] = (int64_t)ri.b * a.q_batch + (int64_t)ri.t * a.q_token + (int64_t)ri.h * a.G * HD;
+    mpos[0] = ri.pos;
+    mslot[0] = (int32_t)slot;
+  }
+  const int rows = (int)min((int64_t)a.C, (int64_t)a.N - blk * a.C);
+  stage_tile<T, HD>(a, ri.b, ri.h, blk, rows, ks, vt, L, threadIdx.x, blockDim.x);
+  __syncthreads();
+  fwd_tile_units<T, HD, NTM>(a, L, ks, vt, mq, mpos, mslot, 1, blk, rows, 0, 1, threadIdx.x & 63);
+}
+
 // Merge the K partials of each (batch, token, query head) in slot order:
 // M = max lse_s, w_s = e^(lse_s - M), O = sum w_s o_s / sum w_s, LSE = M + ln sum w_s.
 // One wave per (batch, token, kv head); a lane owns one 16-byte chunk of one
@@ -719,10 +1029,47 @@ static int grid_size() {
   return cus * 8;
 }
 
+template <typename T, int HD, int NTM>
+static void launch_fwd_tile_n(const AttnArgs& a, bool grouped, int64_t slots, hipStream_t stream) {
+  if (grouped) {
+    const size_t lds = tile_lds<T, HD>(a.C, a.tile).bytes;
+    allow_lds((const void*)attn_fwd_tile_kernel<T, HD, NTM>, lds);
+    PISA_TIMED("attn_fwd", stream, hipLaunchKernelGGL((attn_fwd_tile_kernel<T, HD, NTM>), dim3(grid_size()), dim3(256), lds, stream, a));
+  } else if (slots > 0) {
+    const size_t lds = tile_lds<T, HD>(a.C, 1).bytes;
+    allow_lds((const void*)attn_fwd_tile_direct_kernel<T, HD, NTM>, lds);
+    PISA_TIMED("attn_fwd_direct", stream, hipLaunchKernelGGL((attn_fwd_tile_direct_kernel<T, HD, NTM>), dim3(slots), dim3(64), lds, stream, a, slots));
+  }
+}
+
+template <typename T, int HD>
+static void launch_fwd_tile(const AttnArgs& a, bool grouped, int64_t slots, hipStream_t stream) {
+  const int nt = tile_lds<T, HD>(a.C, 1).Cq / 16;
+  if (nt <= 2) launch_fwd_tile_n<T, HD, 2>(a, grouped, slots, stream);
+  else if (nt <= 4) launch_fwd_tile_n<T, HD, 4>(a, grouped, slots, stream);
+  else launch_fwd_tile_n<T, HD, 8>(a, grouped, slots, stream);
+}
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// The transposed-tile kernels serve D == Dv in {16, 32, 64, 128} with 16-byte
+// aligned q, k and v; other shapes take the general kernels.
+static bool tile_path(const AttnArgs& a) {
+  return a.D == a.Dv && (a.D == 16 || a.D == 32 || a.D == 64 || a.D == 128) && aligned16(a.q) &&
+         aligned16(a.k) && aligned16(a.v);
+}
+
 template <typename T>
 static int attn_fwd_t(const AttnArgs& a, bool grouped, int64_t slots, int64_t items, hipStream_t stream) {
   const int es = sizeof(T);
-  if (grouped) {
+  if (tile_path(a)) {
+    switch (a.D) {
+      case 16: launch_fwd_tile<T, 16>(a, grouped, slots, stream); break;
+      case 32: launch_fwd_tile<T, 32>(a, grouped, slots, stream); break;
+      case 64: launch_fwd_tile<T, 64>(a, grouped, slots, stream); break;
+      default: launch_fwd_tile<T, 128>(a, grouped, slots, stream); break;
+    }
+  } else if (grouped) {
     const size_t lds = fwd_lds(a, es, 4);
     allow_lds((const void*)attn_fwd_grouped_kernel<T>, lds);
     PISA_TIMED("attn_fwd", stream, hipLaunchKernelGGL(attn_fwd_grouped_kernel<T>, dim3(grid_size()), dim3(256), lds, stream, a));

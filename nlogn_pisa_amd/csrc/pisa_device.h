@@ -215,6 +215,135 @@ struct Mfma<float> {
   static __device__ __forceinline__ frag make(const float* x) { return x[0]; }
 };
 
+// ------------------------------------------------------------------ tile MFMA shapes
+//
+// MfmaOp<T, E>: an MFMA whose A/B fragments hold E elements per lane, with the
+// same lane layout as above (A: row l & 15, reduction index E*(l >> 4) + e).
+//   bf16/fp16, E = 8: v_mfma_f32_16x16x32_{bf16,f16}   (gfx950)
+//   bf16/fp16, E = 4: v_mfma_f32_16x16x16{bf16_1k,f16}
+//   fp32,      E = 1: v_mfma_f32_16x16x4f32
+// set(f, e, x) stores x rounded to the element type and returns the rounded value.
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+template <typename T, int E>
+struct MfmaOp;
+
+template <>
+struct MfmaOp<bf16_t, 8> {
+  typedef bf16x8 frag;
+  static __device__ __forceinline__ f4 mma(frag a, frag b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float set(frag& f, int e, float x) {
+    const __bf16 h = (__bf16)x;
+    f[e] = h;
+    return (float)h;
+  }
+};
+
+template <>
+struct MfmaOp<f16_t, 8> {
+  typedef f16x8 frag;
+  static __device__ __forceinline__ f4 mma(frag a, frag b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float set(frag& f, int e, float x) {
+    const _Float16 h = (_Float16)x;
+    f[e] = h;
+    return (float)h;
+  }
+};
+
+template <>
+struct MfmaOp<bf16_t, 4> {
+  typedef s4 frag;
+  static __device__ __forceinline__ f4 mma(frag a, frag b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float set(frag& f, int e, float x) {
+    const bf16_t h = from_f<bf16_t>(x);
+    f[e] = (short)h.bits;
+    return to_f(h);
+  }
+};
+
+template <>
+struct MfmaOp<f16_t, 4> {
+  typedef h4 frag;
+  static __device__ __forceinline__ f4 mma(frag a, frag b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float set(frag& f, int e, float x) {
+    const _Float16 h = (_Float16)x;
+    f[e] = h;
+    return (float)h;
+  }
+};
+
+template <>
+struct MfmaOp<float, 1> {
+  typedef float frag;
+  static __device__ __forceinline__ f4 mma(frag a, frag b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float set(frag& f, int, float x) {
+    f = x;
+    return x;
+  }
+};
+
+// Copy N fragments from memory with the widest accesses the total size allows
+// (the address must be aligned to that width).
+template <typename F, int N>
+__device__ __forceinline__ void load_frags(const void* p, F (&f)[N]) {
+  constexpr int B = N * (int)sizeof(F);
+  if constexpr (B % 16 == 0) {
+    uint4 t[B / 16];
+#pragma unroll
+    for (int i = 0; i < B / 16; ++i) t[i] = static_cast<const uint4*>(p)[i];
+    __builtin_memcpy(f, t, B);
+  } else if constexpr (B % 8 == 0) {
+    uint2 t[B / 8];
+#pragma unroll
+    for (int i = 0; i < B / 8; ++i) t[i] = static_cast<const uint2*>(p)[i];
+    __builtin_memcpy(f, t, B);
+  } else {
+    uint32_t t[B / 4];
+#pragma unroll
+    for (int i = 0; i < B / 4; ++i) t[i] = static_cast<const uint32_t*>(p)[i];
+    __builtin_memcpy(f, t, B);
+  }
+}
+
+template <typename F, int N>
+__device__ __forceinline__ void zero_frags(F (&f)[N]) {
+  __builtin_memset(f, 0, sizeof(f));
+}
+
+// Store N values with the widest accesses the total size allows.
+template <typename V, int N>
+__device__ __forceinline__ void store_vals(void* p, const V (&v)[N]) {
+  constexpr int B = N * (int)sizeof(V);
+  if constexpr (B % 16 == 0) {
+    uint4 t[B / 16];
+    __builtin_memcpy(t, v, B);
+#pragma unroll
+    for (int i = 0; i < B / 16; ++i) static_cast<uint4*>(p)[i] = t[i];
+  } else if constexpr (B % 8 == 0) {
+    uint2 t[B / 8];
+    __builtin_memcpy(t, v, B);
+#pragma unroll
+    for (int i = 0; i < B / 8; ++i) static_cast<uint2*>(p)[i] = t[i];
+  } else {
+    uint32_t t[B / 4];
+    __builtin_memcpy(t, v, B);
+#pragma unroll
+    for (int i = 0; i < B / 4; ++i) static_cast<uint32_t*>(p)[i] = t[i];
+  }
+}
+
 // ------------------------------------------------------------------ comparison network
 //
 // Element e of a network of width `width` (power of two, <= 64*J) lives in lane

@@ -59,6 +59,10 @@ CASES = [
     ("bf16-decode", 3, 1, 4096, 32, 8, 128, 64, 16, "bf16", True, None),
     ("bf16-suffix", 1, 40, 900, 8, 2, 64, 64, 5, "bf16", True, 777),
     ("bf16-g16", 1, 256, 256, 16, 1, 64, 64, 4, "bf16", True, None),
+    ("bf16-d32", 1, 256, 256, 8, 2, 32, 32, 4, "bf16", True, None),
+    ("fp32-d16", 1, 128, 256, 4, 1, 16, 16, 6, "fp32", True, None),
+    ("fp16-d16-c48", 2, 200, 200, 4, 2, 16, 48, 3, "fp16", True, None),
+    ("bf16-c128", 1, 512, 640, 8, 2, 128, 128, 3, "bf16", True, None),
 ]
 
 
@@ -120,6 +124,23 @@ def test_selected_blocks_end_to_end(P):
     ref_o, ref_lse = O.sparse_attention(q, k, v, ids.cpu().numpy(), 64)
     assert excess_error(out.float().cpu().numpy(), ref_o, "bf16") <= 2e-2
     assert np.abs(lse.cpu().numpy() - ref_lse).max() <= 2e-2
+
+
+@pytest.mark.parametrize("dv", [64, 32])
+def test_forward_value_dim_differs(P, dv):
+    """Dv != D (the general forward kernels): O [B,Tq,Hq,Dv] and LSE."""
+    case = CASES[2]
+    name, batch, tq, n, qh, kh, dim, block, topk, dtype, causal, offset = case
+    print(f"attention forward {name} dv={dv}", flush=True)
+    q, k, v, idx = _inputs(case)
+    v = np.ascontiguousarray(v[..., :dv])
+    out, lse = P.sparse_attention_with_lse(to_gpu(q, dtype), to_gpu(k, dtype), to_gpu(v, dtype),
+                                           torch.from_numpy(idx).cuda(), block)
+    ref_o, ref_lse = O.sparse_attention(q, k, v, idx, block)
+    assert out.shape[-1] == dv
+    assert excess_error(out.float().cpu().numpy(), ref_o, dtype) <= TOL[dtype]
+    fin = np.isfinite(ref_lse)
+    assert np.abs(lse.cpu().numpy()[fin] - ref_lse[fin]).max() <= TOL[dtype]
 
 
 def test_int32_indices_and_determinism(P):
