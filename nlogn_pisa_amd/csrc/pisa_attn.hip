@@ -329,19 +329,6 @@ __global__ void __launch_bounds__(64) attn_fwd_direct_kernel(AttnArgs a, int64_t
 // per tile into LDS, and each wave loads the next unit's query rows while it
 // computes the current one.
 
-template <typename T, int HD, int NTM = 8>
-struct FwdShape {
-  static constexpr int E = sizeof(T) == 4 ? 1 : ((HD / 4) % 8 == 0 ? 8 : 4);
-  typedef MfmaOp<T, E> Op;
-  typedef typename Op::frag frag;
-  static constexpr int QL = HD / 4;                 // row elements per lane group
-  static constexpr int DS = QL / E;                 // reduction steps of S^T
-  static constexpr int NDT = HD / 16;               // dv tiles of O^T
-  static constexpr int KQ = E == 8 ? 32 : 16;       // key padding granularity
-  static constexpr int MAXK = NTM * 4 / E;          // P V steps at NTM key tiles
-  static constexpr int PAD = 16 / (int)sizeof(T);   // 16-byte LDS row padding
-};
-
 // LDS of one tile: K block [Cq][HD + PAD], V^T [HD][Cq + PAD], then per request
 // the query row offset (int64), position (int64) and slot (int32).
 struct TileLds {
@@ -351,7 +338,7 @@ struct TileLds {
 
 template <typename T, int HD>
 __host__ __device__ inline TileLds tile_lds(int C, int tile) {
-  typedef FwdShape<T, HD> S;
+  typedef QkShape<T, HD> S;
   TileLds L;
   L.Cq = (C + S::KQ - 1) / S::KQ * S::KQ;
   L.ldk = HD + S::PAD;
@@ -445,7 +432,7 @@ template <typename T, int HD, int NTM>
 __device__ void fwd_tile_units(const AttnArgs& a, const TileLds& L, const T* ks, const T* vt,
                                const int64_t* mq, const int64_t* mpos, const int32_t* mslot,
                                int nreq, int64_t blk, int rows, int wave, int nwaves, int lane) {
-  typedef FwdShape<T, HD, NTM> S;
+  typedef QkShape<T, HD, NTM> S;
   typedef typename S::Op Op;
   typedef typename S::frag frag;
   typedef typename PartialT<T>::type PT;

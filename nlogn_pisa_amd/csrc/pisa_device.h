@@ -344,6 +344,23 @@ __device__ __forceinline__ void store_vals(void* p, const V (&v)[N]) {
   }
 }
 
+// Shape of the transposed S^T = K Q^T tiles (sparse attention forward, leaf
+// scoring) for head dim HD and at most NTM 16-key tiles: lane group grp owns
+// dimensions [grp HD/4, (grp+1) HD/4) of a row (QL elements, DS reduction steps
+// of E elements).  Keys are padded to KQ (two key tiles per step at E = 8).
+template <typename T, int HD, int NTM = 8>
+struct QkShape {
+  static constexpr int E = sizeof(T) == 4 ? 1 : ((HD / 4) % 8 == 0 ? 8 : 4);
+  typedef MfmaOp<T, E> Op;
+  typedef typename Op::frag frag;
+  static constexpr int QL = HD / 4;                 // row elements per lane group
+  static constexpr int DS = QL / E;                 // reduction steps of S^T
+  static constexpr int NDT = HD / 16;               // dv tiles of O^T
+  static constexpr int KQ = E == 8 ? 32 : 16;       // key padding granularity
+  static constexpr int MAXK = NTM * 4 / E;          // P V steps at NTM key tiles
+  static constexpr int PAD = 16 / (int)sizeof(T);   // 16-byte LDS row padding
+};
+
 // ------------------------------------------------------------------ comparison network
 //
 // Element e of a network of width `width` (power of two, <= 64*J) lives in lane

@@ -156,6 +156,222 @@ __global__ void __launch_bounds__(256) leaf_kernel(LeafArgs a) {
   }
 }
 
+// ------------------------------------------------------------------ transposed tiles
+//
+// The path for D in {16, 32, 64, 128}: S^T = K Q^T as in the sparse attention
+// forward (QkShape), so lane (grp, col) holds the scores of row `col` against
+// keys 16 mt + 4 grp + i and loads one contiguous quarter of its query row.
+// Per-request bookkeeping is computed once per tile into LDS and each wave loads
+// the next unit's query rows while it scores the current one.  A work item of a
+// wave is one 16-row unit (Gp <= 16: 16 / Gp requests) or one request of Gp / 16
+// units (Gp > 16).
+
+struct LeafLds {
+  int Cq, ldk;
+  size_t k_off, q_off, slot_off, bytes;
+};
+
+template <typename T, int HD>
+__host__ __device__ inline LeafLds leaf_lds(int C, int tile) {
+  typedef QkShape<T, HD> S;
+  LeafLds L;
+  L.Cq = (C + S::KQ - 1) / S::KQ * S::KQ;
+  L.ldk = HD + S::PAD;
+  size_t off = 0;
+  L.k_off = off;
+  off += (size_t)L.Cq * L.ldk * sizeof(T);
+  off = (off + 15) / 16 * 16;
+  L.q_off = off;
+  off += (size_t)tile * 8;
+  L.slot_off = off;
+  off += (size_t)tile * 4;
+  L.bytes = (off + 15) / 16 * 16;
+  return L;
+}
+
+template <typename T, int HD, int NTM>
+__global__ void __launch_bounds__(256, 2) leaf_tile_kernel(LeafArgs a) {
+  typedef QkShape<T, HD, NTM> S;
+  typedef typename S::Op Op;
+  typedef typename S::frag frag;
+  constexpr int QL = S::QL, DS = S::DS;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const LeafLds L = leaf_lds<T, HD>(a.C, a.tile);
+  T* ks = reinterpret_cast<T*>(smem + L.k_off);
+  int64_t* mq = reinterpret_cast<int64_t*>(smem + L.q_off);
+  int32_t* mslot = reinterpret_cast<int32_t*>(smem + L.slot_off);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nwaves = (int)(blockDim.x >> 6);
+  const int col = lane & 15, grp = lane >> 4;
+  const int NT = L.Cq / 16;
+  const int Gp = a.Gp;
+  const int nsub = Gp <= 16 ? 1 : Gp / 16;  // units per item
+  const int rpu = Gp <= 16 ? 16 / Gp : 1;   // requests per item
+  const bool lse = a.method == PISA_METHOD_LSE;
+  const bool pisa1 = a.method == PISA_METHOD_PISA1;
+  const T* q = static_cast<const T*>(a.q);
+  constexpr int vec = 16 / (int)sizeof(T);
+  constexpr int vpr = HD / vec;
+  const int ntiles = *a.num_tiles;
+
+  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int g = a.tile_group[tile];
+    const int blk = g % a.M0;
+    const int bh = g / a.M0;
+    const int h = bh % a.Hkv;
+    const int b = bh / a.Hkv;
+    const int start = (tile - a.tile_off[g]) * a.tile;
+    const int nreq = min(a.tile, a.counts[g] - start);
+    const int rows_valid = min(a.C, a.src_rows - blk * a.C);
+    const int32_t* reqs = a.tile_req + (int64_t)tile * a.tile;
+
+    __syncthreads();
+    for (int i = tid; i < nreq; i += blockDim.x) {
+      const int slot = reqs[i];
+      const int64_t item = slot / a.W;
+      const int t = (int)((item / a.Hkv) % a.T);
+      mq[i] = (int64_t)b * a.q_batch + (int64_t)t * a.q_token + (int64_t)h * a.G * HD;
+      mslot[i] = slot;
+    }
+    const T* kb = static_cast<const T*>(a.src) + b * a.src_batch + (int64_t)blk * a.C * a.src_row +
+                  (int64_t)h * HD;
+    for (int idx = tid; idx < L.Cq * vpr; idx += blockDim.x) {
+      const int r = idx / vpr, c = (idx % vpr) * vec;
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (r < rows_valid) v = *reinterpret_cast<const uint4*>(kb + (int64_t)r * a.src_row + c);
+      *reinterpret_cast<uint4*>(ks + r * L.ldk + c) = v;
+    }
+    __syncthreads();
+
+    const int items = (nreq + rpu - 1) / rpu;
+    auto fetch = [&](int r, int j, frag (&f)[DS]) {
+      const int rho = (r * nsub + j) * 16 + col;
+      const int rq = rho / Gp, gh = rho % Gp;
+      if (r < items && rq < nreq && gh < a.G)
+        load_frags(q + mq[rq] + (int64_t)gh * HD + QL * grp, f);
+      else
+        zero_frags(f);
+    };
+    frag qf[DS];
+    fetch(wave, 0, qf);
+    for (int r = wave; r < items; r += nwaves) {
+      float total = 0.f;  // this lane's row: head scores summed over the item's units
+      for (int j = 0; j < nsub; ++j) {
+        frag qn[DS];
+        if (j + 1 < nsub) fetch(r, j + 1, qn);
+        else fetch(r + nwaves, 0, qn);
+        f4 s[NTM];
+#pragma unroll
+        for (int mt = 0; mt < NTM; ++mt) {
+          s[mt] = f4{0.f, 0.f, 0.f, 0.f};
+          if (mt < NT) {
+            frag kf[DS];
+            load_frags(ks + (mt * 16 + col) * L.ldk + QL * grp, kf);
+#pragma unroll
+            for (int d = 0; d < DS; ++d) s[mt] = Op::mma(kf[d], qf[d], s[mt]);
+          }
+        }
+        float head;
+        if (lse) {
+          float m = -INFINITY;
+#pragma unroll
+          for (int mt = 0; mt < NTM; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (mt < NT && mt * 16 + 4 * grp + i < rows_valid) m = fmaxf(m, s[mt][i] * a.scale);
+          m = fmaxf(m, __shfl_xor(m, 16));
+          m = fmaxf(m, __shfl_xor(m, 32));
+          float e = 0.f;
+#pragma unroll
+          for (int mt = 0; mt < NTM; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (mt < NT && mt * 16 + 4 * grp + i < rows_valid) e += __expf(s[mt][i] * a.scale - m);
+          e += __shfl_xor(e, 16);
+          e += __shfl_xor(e, 32);
+          head = m + __logf(e);
+        } else {
+          float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+          for (int mt = 0; mt < NTM; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (mt < NT && mt * 16 + 4 * grp + i < rows_valid) {
+                s1 += s[mt][i];
+                s2 = fmaf(s[mt][i], s[mt][i], s2);
+              }
+          s1 += __shfl_xor(s1, 16);
+          s1 += __shfl_xor(s1, 32);
+          s2 += __shfl_xor(s2, 16);
+          s2 += __shfl_xor(s2, 32);
+          if (pisa1) {
+            head = s1;  // one support row: the leaf mean, scale 1
+          } else {
+            const float cnt = (float)rows_valid;
+            const float mean = s1 / cnt;
+            const float var = fmaxf(s2 / cnt - mean * mean, 0.f);
+            head = a.scale * mean + (float)(0.5 * (double)a.scale * (double)a.scale) * var;
+          }
+        }
+        const int rho = (r * nsub + j) * 16 + col;
+        const bool real = rho / Gp < nreq && rho % Gp < a.G;
+        total += real ? head : 0.f;
+#pragma unroll
+        for (int d = 0; d < DS; ++d) qf[d] = qn[d];
+      }
+      // sum the head rows of each request (consecutive lanes of a 16-lane row)
+      if (Gp >= 16) {
+        float v = total;
+        v += __shfl_xor(v, 1);
+        v += __shfl_xor(v, 2);
+        v += __shfl_xor(v, 4);
+        v += __shfl_xor(v, 8);
+        if (lane == 0 && r < nreq) a.scores[mslot[r]] = v;
+      } else {
+        float v = total;
+        for (int off = 1; off < Gp; off <<= 1) v += __shfl_xor(v, off);
+        const int rq = (r * 16 + col) / Gp;
+        if (grp == 0 && col % Gp == 0 && rq < nreq) a.scores[mslot[rq]] = v;
+      }
+    }
+  }
+}
+
+template <typename T, int HD>
+static void launch_leaf_tile(const LeafArgs& a, int grid, hipStream_t stream) {
+  const LeafLds L = leaf_lds<T, HD>(a.C, a.tile);
+  const int nt = L.Cq / 16;
+  if (nt <= 2) {
+    allow_lds((const void*)leaf_tile_kernel<T, HD, 2>, L.bytes);
+    PISA_TIMED("leaf", stream, hipLaunchKernelGGL((leaf_tile_kernel<T, HD, 2>), dim3(grid), dim3(256), L.bytes, stream, a));
+  } else if (nt <= 4) {
+    allow_lds((const void*)leaf_tile_kernel<T, HD, 4>, L.bytes);
+    PISA_TIMED("leaf", stream, hipLaunchKernelGGL((leaf_tile_kernel<T, HD, 4>), dim3(grid), dim3(256), L.bytes, stream, a));
+  } else {
+    allow_lds((const void*)leaf_tile_kernel<T, HD, 8>, L.bytes);
+    PISA_TIMED("leaf", stream, hipLaunchKernelGGL((leaf_tile_kernel<T, HD, 8>), dim3(grid), dim3(256), L.bytes, stream, a));
+  }
+}
+
+template <typename T>
+static void launch_leaf_tile_t(const LeafArgs& a, int grid, hipStream_t stream) {
+  switch (a.D) {
+    case 16: launch_leaf_tile<T, 16>(a, grid, stream); break;
+    case 32: launch_leaf_tile<T, 32>(a, grid, stream); break;
+    case 64: launch_leaf_tile<T, 64>(a, grid, stream); break;
+    default: launch_leaf_tile<T, 128>(a, grid, stream); break;
+  }
+}
+
+// The transposed-tile kernel serves D in {16, 32, 64, 128} with 16-byte aligned
+// query and key rows; other shapes take the general kernel.
+static bool leaf_tile_path(const LeafArgs& a, int es) {
+  const bool dim = a.D == 16 || a.D == 32 || a.D == 64 || a.D == 128;
+  const bool ptrs = (((uintptr_t)a.q | (uintptr_t)a.src) & 15) == 0;
+  const bool strides = ((a.q_batch | a.q_token | a.src_batch | a.src_row) * es) % 16 == 0;
+  return dim && ptrs && strides;
+}
+
 int launch_leaf(int dtype, const LeafArgs& a, hipStream_t stream) {
   const int es = dtype_size(dtype);
   const int ldk = a.D + 16 / es;
@@ -166,6 +382,15 @@ int launch_leaf(int dtype, const LeafArgs& a, hipStream_t stream) {
     return fail(PISA_ERR_UNSUPPORTED, "key block of %zu bytes exceeds LDS", lds);
   const int cus = device_cus();
   const int grid = cus * 8;
+  if (leaf_tile_path(a, es)) {
+    switch (dtype) {
+      case PISA_F32: launch_leaf_tile_t<float>(a, grid, stream); break;
+      case PISA_F16: launch_leaf_tile_t<f16_t>(a, grid, stream); break;
+      case PISA_BF16: launch_leaf_tile_t<bf16_t>(a, grid, stream); break;
+      default: return fail(PISA_ERR_INVALID, "unknown dtype %d", dtype);
+    }
+    return check_launch("leaf");
+  }
   switch (dtype) {
     case PISA_F32:
       allow_lds((const void*)leaf_kernel<float>, lds);

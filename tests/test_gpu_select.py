@@ -114,6 +114,8 @@ CONFIGS = [
     ("refbench", 1, 8192, 32, 2, 64, 64, 2, 8, "pisa", True, 2, "bf16", 0.0, None),
     ("fp16-b2", 2, 2048, 8, 2, 64, 32, 2, 8, "pisa2", False, 1, "fp16", 0.0, None),
     ("suffix", 1, 4096, 8, 2, 64, 64, 4, 8, "pisa", True, 2, "bf16", 0.0, 100),
+    ("d32", 1, 2048, 8, 2, 32, 32, 4, 8, "pisa2", True, 1, "bf16", 0.0, None),
+    ("d16-fp32", 1, 1024, 4, 2, 16, 16, 2, 8, "pisa", True, 1, "fp32", 0.0, None),
 ]
 
 
@@ -150,18 +152,30 @@ def test_select_is_deterministic(P):
     assert a.dtype == torch.int64 and tuple(a.shape) == (1, 16384, 4, 16)
 
 
+LEAF_SHAPES = [
+    # B, T, Hq, Hkv, D, C, dtype
+    (2, 2048, 8, 2, 64, 64, "bf16"),
+    (1, 1024, 64, 2, 32, 32, "bf16"),     # 32 query heads per kv head: a request spans two units
+    (1, 1000, 4, 2, 16, 16, "fp32"),
+    (1, 700, 6, 2, 128, 128, "fp16"),     # 3 heads per kv head (padded to 4), tail block
+]
+
+
+@pytest.mark.parametrize("shape", LEAF_SHAPES, ids=[f"{s[-1]}-g{s[2] // s[3]}-d{s[4]}" for s in LEAF_SHAPES])
 @pytest.mark.parametrize("method", METHODS)
-def test_leaf_scores_match_oracle(P, method):
-    print(f"leaf_scores {method}", flush=True)
-    q, k = structured_qkv(9, 2, 2048, 8, 2, 64, "bf16", value=False)
+def test_leaf_scores_match_oracle(P, method, shape):
+    batch, length, qh, kh, dim, block, dtype = shape
+    print(f"leaf_scores {method} {shape}", flush=True)
+    q, k = structured_qkv(9, batch, length, qh, kh, dim, dtype, value=False)
     rng = np.random.default_rng(0)
-    cand = rng.integers(-1, 34, size=(2, 2048, 2, 40)).astype(np.int32)
-    pos = O.query_positions(2, 2048, 2048)
-    qg, kg = to_gpu(q, "bf16"), to_gpu(k, "bf16")
-    out = P.leaf_scores(qg, kg, torch.from_numpy(cand).cuda(), 64, method,
+    blocks = -(-length // block)
+    cand = rng.integers(-1, blocks + 2, size=(batch, length, kh, 40)).astype(np.int32)
+    pos = O.query_positions(batch, length, length)
+    qg, kg = to_gpu(q, dtype), to_gpu(k, dtype)
+    out = P.leaf_scores(qg, kg, torch.from_numpy(cand).cuda(), block, method,
                         torch.from_numpy(pos).cuda(), 8, True, 1).cpu().numpy()
-    ref = O.leaf_scores(q, k, cand, 64, method, pos, 8, True, 1,
-                        leaf_means=O.mean_pool(k, 64, "bf16"))
+    ref = O.leaf_scores(q, k, cand, block, method, pos, 8, True, 1,
+                        leaf_means=O.mean_pool(k, block, dtype))
     assert np.array_equal(np.isneginf(out), np.isneginf(ref))
     fin = np.isfinite(ref)
     np.testing.assert_allclose(out[fin], ref[fin], rtol=2e-5, atol=2e-5)
