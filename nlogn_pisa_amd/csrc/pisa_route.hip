@@ -251,6 +251,259 @@ __global__ void __launch_bounds__(512) route_kernel(RouteArgs a) {
   }
 }
 
+// ------------------------------------------------------------------ grouped routing on MFMA
+//
+// route_grouped_kernel: the grouped schedule's routing (levels top..1, then the
+// level-0 candidates), one wave per item.  Scoring of a level is one product
+// S^T = X Q^T per 16 support rows: X stacks the support rows of 16 / R
+// consecutive scoreable candidates (R = b children, or the node's own summary
+// for pisa1), Q^T holds the item's G <= 16 query heads as columns (QkShape
+// layout: lane group grp owns dimensions [grp D/4, (grp+1) D/4)).  Lane
+// (grp, col) then holds head `col`'s dots with rows 4 grp + i, i.e. whole
+// candidates (R <= 4) or half of one (R = 8, joined with the partner lane
+// group): the per-head support score is computed in the lane and summed over
+// the heads by one DPP row reduction.  Each wave loads the next 16 support rows
+// while it scores the current ones.
+
+// Support score of one head over rows v[0..n) (block_scores,
+// top_k_pyramid_torch.py:62-79): LogSumExp of s*v, the binary pisa2 form at
+// support 2, or s*mean + s^2/2*var.
+struct SupportAcc {
+  float a0, a1;  // LSE: max, sum of exp | moments: sum, sum of squares | binary: z0, z1
+  int n;
+};
+
+__device__ __forceinline__ SupportAcc support_acc(const float* v, int count, int n, bool lse,
+                                                  float scale) {
+  SupportAcc r{lse ? -INFINITY : 0.f, 0.f, 0};
+  if (lse) {
+    for (int i = 0; i < count; ++i)
+      if (i < n) r.a0 = fmaxf(r.a0, v[i] * scale);
+    for (int i = 0; i < count; ++i)
+      if (i < n) r.a1 += __expf(v[i] * scale - r.a0);
+  } else {
+    for (int i = 0; i < count; ++i)
+      if (i < n) {
+        r.a0 += v[i];
+        r.a1 = fmaf(v[i], v[i], r.a1);
+      }
+  }
+  r.n = min(count, max(n, 0));
+  return r;
+}
+
+__device__ __forceinline__ SupportAcc support_join(SupportAcc x, SupportAcc y, bool lse) {
+  if (!lse) return SupportAcc{x.a0 + y.a0, x.a1 + y.a1, x.n + y.n};
+  const float m = fmaxf(x.a0, y.a0);
+  if (m == -INFINITY) return x;
+  return SupportAcc{m, x.a1 * __expf(x.a0 - m) + y.a1 * __expf(y.a0 - m), x.n + y.n};
+}
+
+__device__ __forceinline__ float support_final(SupportAcc r, const float* v, bool lse, bool binary,
+                                               float scale) {
+  if (lse) return r.a0 + __logf(r.a1);
+  if (binary) {
+    const float z0 = v[0] * scale, z1 = v[1] * scale;
+    const float d = z0 - z1;
+    return r.n == 2 ? 0.5f * (z0 + z1) + 0.125f * d * d : z0;
+  }
+  const float count = (float)max(r.n, 1);
+  const float mean = r.a0 / count;
+  const float var = fmaxf(r.a1 / count - mean * mean, 0.f);
+  return scale * mean + (float)(0.5 * (double)scale * (double)scale) * var;
+}
+
+// Scores of the candidates of one 16-row support tile (RR rows per candidate):
+// lane (grp, col) holds head col's dots with rows 4 grp + i in sv.
+template <int RR>
+__device__ __forceinline__ void tile_scores(const f4& sv, int mt, const RouteArgs& a,
+                                            const int* ids_s, const int* list_s, float* sc_s,
+                                            int nlist, int len, bool own, bool lse, bool binary,
+                                            int col, int grp) {
+  const float v[4] = {sv[0], sv[1], sv[2], sv[3]};
+  constexpr int cpt = 16 / RR;
+  if constexpr (RR <= 4) {
+    // candidates (4 grp) / RR + j of this tile, rows j RR .. j RR + RR - 1
+#pragma unroll
+    for (int j = 0; j < 4 / RR; ++j) {
+      const int ci = mt * cpt + (4 * grp) / RR + j;
+      int n = 0;
+      if (ci < nlist) n = own ? 1 : len - ids_s[list_s[ci]] * RR;
+      float head;
+      if (own) {
+        head = v[j];
+      } else {
+        const SupportAcc acc = support_acc(v + j * RR, RR, n, lse, a.scale);
+        head = support_final(acc, v + j * RR, lse, binary, a.scale);
+      }
+      const float tot = row_sum16(col < a.G ? head : 0.f);
+      if (col == 0 && ci < nlist) sc_s[list_s[ci]] = tot;
+    }
+  } else {
+    // RR = 8: candidate grp / 2 of this tile over lane groups 2c (children 0-3)
+    // and 2c + 1 (children 4-7)
+    const int ci = mt * cpt + (grp >> 1);
+    int n = 0;
+    if (ci < nlist) n = len - ids_s[list_s[ci]] * RR - 4 * (grp & 1);
+    SupportAcc acc = support_acc(v, 4, n, lse, a.scale);
+    SupportAcc other;
+    other.a0 = __shfl_xor(acc.a0, 16);
+    other.a1 = __shfl_xor(acc.a1, 16);
+    other.n = __shfl_xor(acc.n, 16);
+    acc = (grp & 1) ? support_join(other, acc, lse) : support_join(acc, other, lse);
+    const float head = support_final(acc, v, lse, false, a.scale);
+    const float tot = row_sum16(col < a.G ? head : 0.f);
+    if (col == 0 && (grp & 1) == 0 && ci < nlist) sc_s[list_s[ci]] = tot;
+  }
+}
+
+template <typename T, int HD>
+__global__ void __launch_bounds__(64) route_grouped_kernel(RouteArgs a) {
+  typedef QkShape<T, HD> S;
+  typedef typename S::Op Op;
+  typedef typename S::frag frag;
+  constexpr int QL = S::QL, DS = S::DS;
+  __shared__ int ids_s[kMaxWidth];
+  __shared__ float sc_s[kMaxWidth];
+  __shared__ int list_s[kMaxWidth];
+  __shared__ int cnt_s[2];
+
+  const int item = blockIdx.x;
+  const int h = item % a.Hkv;
+  const int bt = item / a.Hkv;
+  const int t = bt % a.T;
+  const int b = bt / a.T;
+  const int64_t pos = a.positions[b * a.pos_batch + t];
+  const int64_t leaf = pos / a.C;
+  const int lane = threadIdx.x;
+  const int col = lane & 15, grp = lane >> 4;
+  const int K = a.topk;
+  const int levels_traced = a.top + 1;
+  const bool own = a.method == PISA_METHOD_PISA1;  // support = the node's own summary
+  const bool lse = a.method == PISA_METHOD_LSE;
+  const bool binary = !lse && !own && a.branching == 2;
+  const int R = own ? 1 : a.branching;             // support rows per candidate (<= 8)
+  const int cpt = 16 / R;                          // candidates per 16 support rows
+
+  // Q^T: lane (grp, col) holds head col's dimensions [QL grp, QL grp + QL)
+  frag qb[DS];
+  if (col < a.G)
+    load_frags(static_cast<const T*>(a.q) + b * a.q_batch + t * a.q_token +
+                   ((int64_t)h * a.G + col) * HD + QL * grp,
+               qb);
+  else
+    zero_frags(qb);
+
+  int width = a.first_width;
+  for (int e = lane; e < width; e += 64) ids_s[e] = e;
+
+  for (int level = a.top; level >= 0; --level) {
+    const int M = a.lengths[level];
+    const int64_t span_blocks = ipow(a.branching, level);
+    const int64_t span = span_blocks * a.C;
+    if (lane == 0) { cnt_s[0] = 0; cnt_s[1] = 0; }
+    __syncthreads();
+    int nvalid = 0;
+    for (int e = lane; e < width; e += 64) {
+      int id = ids_s[e];
+      if (id >= M) { id = -1; ids_s[e] = -1; }
+      nvalid += (id >= 0 && (int64_t)id * span <= pos) ? 1 : 0;
+    }
+    if (nvalid) atomicAdd(&cnt_s[0], nvalid);
+    __syncthreads();
+    const bool identity = !own && cnt_s[0] <= K;
+    for (int e = lane; e < width; e += 64) {
+      const int id = ids_s[e];
+      const bool valid = id >= 0 && (int64_t)id * span <= pos;
+      const bool forced = valid && is_forced(id, leaf, span_blocks, a.force_first, a.force_recent);
+      const bool scoreable = valid && !forced && !identity;
+      sc_s[e] = valid ? (forced ? kForced : 0.f) : kInvalid;
+      if (level == 0) {
+        a.cand[(int64_t)item * width + e] = id;
+        a.scoreable[(int64_t)item * width + e] = scoreable ? 1 : 0;
+      } else if (scoreable) {
+        list_s[atomicAdd(&cnt_s[1], 1)] = e;
+      }
+    }
+    __syncthreads();
+    if (level == 0) return;
+
+    // score the scoreable candidates, 16 support rows at a time
+    const int nlist = cnt_s[1];
+    const int src_level = own ? level : level - 1;
+    const T* base = static_cast<const T*>(a.summary) + b * a.sum_batch +
+                    ((int64_t)a.offsets[src_level] * a.Hkv + h) * HD;
+    const int64_t rstride = (int64_t)a.Hkv * HD;
+    const int len = a.lengths[src_level];
+    const int ntile = (nlist + cpt - 1) / cpt;
+    auto fetch = [&](int mt, frag (&f)[DS]) {
+      const int ci = mt * cpt + col / R, child = col % R;
+      int64_t row = -1;
+      if (mt < ntile && ci < nlist) {
+        const int64_t r = (int64_t)ids_s[list_s[ci]] * R + child;
+        if (r < len) row = r;
+      }
+      if (row >= 0) load_frags(base + row * rstride + QL * grp, f);
+      else zero_frags(f);
+    };
+    frag xf[DS];
+    fetch(0, xf);
+    for (int mt = 0; mt < ntile; ++mt) {
+      frag xn[DS];
+      fetch(mt + 1, xn);
+      f4 sv = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int d = 0; d < DS; ++d) sv = Op::mma(xf[d], qb[d], sv);
+      switch (R) {
+        case 1: tile_scores<1>(sv, mt, a, ids_s, list_s, sc_s, nlist, len, own, lse, binary, col, grp); break;
+        case 2: tile_scores<2>(sv, mt, a, ids_s, list_s, sc_s, nlist, len, own, lse, binary, col, grp); break;
+        case 4: tile_scores<4>(sv, mt, a, ids_s, list_s, sc_s, nlist, len, own, lse, binary, col, grp); break;
+        default: tile_scores<8>(sv, mt, a, ids_s, list_s, sc_s, nlist, len, own, lse, binary, col, grp); break;
+      }
+#pragma unroll
+      for (int d = 0; d < DS; ++d) xf[d] = xn[d];
+    }
+    __syncthreads();
+
+    const int net = next_pow2(width);
+    float sreg[8];
+    int idv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int e = j * 64 + lane;
+      sreg[j] = e < width ? sc_s[e] : kInvalid;
+      idv[j] = e < width ? ids_s[e] : -1;
+    }
+    if (net <= 64) {
+      float s1[1] = {sreg[0]};
+      int i1[1] = {idv[0]};
+      bitonic_desc<1>(s1, i1, net, lane);
+      idv[0] = i1[0];
+    } else if (net <= 128) {
+      float s2[2] = {sreg[0], sreg[1]};
+      int i2[2] = {idv[0], idv[1]};
+      bitonic_desc<2>(s2, i2, net, lane);
+      idv[0] = i2[0];
+    } else if (net <= 256) {
+      float s4_[4] = {sreg[0], sreg[1], sreg[2], sreg[3]};
+      int i4[4] = {idv[0], idv[1], idv[2], idv[3]};
+      bitonic_desc<4>(s4_, i4, net, lane);
+      idv[0] = i4[0];
+    } else {
+      bitonic_desc<8>(sreg, idv, net, lane);
+    }
+    const int sel = idv[0];
+    if (a.trace && lane < K)
+      a.trace[((int64_t)item * levels_traced + (a.top - level)) * K + lane] = sel;
+    __syncthreads();
+    if (lane < K)
+      for (int c = 0; c < a.branching; ++c)
+        ids_s[lane * a.branching + c] = sel < 0 ? -1 : sel * a.branching + c;
+    __syncthreads();
+    width = a.branching * K;
+  }
+}
+
 // Final leaf network of the grouped schedule (final_kernel,
 // top_k_pyramid_triton.py:279-308, with the Torch sentinels :169-171 and
 // output mask :176).  One wave per item, four items per workgroup.
@@ -341,8 +594,36 @@ static int launch_route_t(const RouteArgs& a, int64_t items, int threads, hipStr
   }
 }
 
+template <typename T>
+static int launch_route_grouped(const RouteArgs& a, int64_t items, hipStream_t stream) {
+  switch (a.D) {
+    case 16: PISA_TIMED("route", stream, hipLaunchKernelGGL((route_grouped_kernel<T, 16>), dim3(items), dim3(64), 0, stream, a)); break;
+    case 32: PISA_TIMED("route", stream, hipLaunchKernelGGL((route_grouped_kernel<T, 32>), dim3(items), dim3(64), 0, stream, a)); break;
+    case 64: PISA_TIMED("route", stream, hipLaunchKernelGGL((route_grouped_kernel<T, 64>), dim3(items), dim3(64), 0, stream, a)); break;
+    default: PISA_TIMED("route", stream, hipLaunchKernelGGL((route_grouped_kernel<T, 128>), dim3(items), dim3(64), 0, stream, a)); break;
+  }
+  return check_launch("route");
+}
+
+// The MFMA routing serves the grouped schedule (level 0 left to the leaf kernel)
+// for D in {16, 32, 64, 128}, G <= 16, b <= 8 and 16-byte aligned rows.
+static bool route_mfma_path(const RouteArgs& a, int es) {
+  const bool dim = a.D == 16 || a.D == 32 || a.D == 64 || a.D == 128;
+  const bool ptrs = (((uintptr_t)a.q | (uintptr_t)a.summary) & 15) == 0;
+  const bool strides = ((a.q_batch | a.q_token | a.sum_batch) * es) % 16 == 0;
+  return !a.fused && dim && a.G <= 16 && a.branching <= 8 && ptrs && strides;
+}
+
 int launch_route(int dtype, const RouteArgs& a, int64_t items, int threads, hipStream_t stream) {
   if (items == 0) return PISA_OK;
+  if (route_mfma_path(a, dtype_size(dtype))) {
+    switch (dtype) {
+      case PISA_F32: return launch_route_grouped<float>(a, items, stream);
+      case PISA_F16: return launch_route_grouped<f16_t>(a, items, stream);
+      case PISA_BF16: return launch_route_grouped<bf16_t>(a, items, stream);
+      default: return fail(PISA_ERR_INVALID, "unknown dtype %d", dtype);
+    }
+  }
   switch (dtype) {
     case PISA_F32: return launch_route_t<float>(a, items, threads, stream);
     case PISA_F16: return launch_route_t<f16_t>(a, items, threads, stream);
