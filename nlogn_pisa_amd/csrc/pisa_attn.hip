@@ -611,54 +611,66 @@ __global__ void __launch_bounds__(64, 2) attn_fwd_tile_direct_kernel(AttnArgs a,
   fwd_tile_units<T, HD, NTM>(a, L, ks, vt, mq, mpos, mslot, 1, blk, rows, 0, 1, threadIdx.x & 63);
 }
 
-// Merge the K partials of each (batch, token, query head) in slot order:
-// M = max lse_s, w_s = e^(lse_s - M), O = sum w_s o_s / sum w_s, LSE = M + ln sum w_s.
-// One wave per (batch, token, kv head); a lane owns one 16-byte chunk of one
-// head's row, so each slot's [G, Dv] partial block is one coalesced read.
+// Merge the K partials of each (batch, token, query head) in slot order with
+// an online rescale: M = max lse_s, w_s = e^(lse_s - M), O = sum w_s o_s / sum w_s,
+// LSE = M + ln sum w_s.  One wave per (batch, token, kv head); a lane owns one
+// 16-byte chunk of one head's row, so each slot's [G, Dv] partial block is one
+// coalesced read.  Slot visibility is one ballot per 64 slots; eight slots'
+// partial chunks and log-sum-exps are loaded before any is used (slots that are
+// not visible are read but never used: their values are selected away).
 template <typename T>
 __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a, int64_t items) {
   typedef typename PartialT<T>::type PT;
   constexpr int V = 16 / sizeof(PT);
+  constexpr int U = 8;  // slots in flight
   const int lane = threadIdx.x & 63;
   const int64_t item = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (item >= items) return;
   const RowInfo ri = row_info(a, item * a.K);
+  const int64_t slot0 = item * a.K;
   const int chunks = a.Dv / V;
   const int work = a.G * chunks;
+  const PT* part = static_cast<const PT*>(a.part_o);
   for (int base = 0; base < work; base += 64) {
     const int idx = min(base + lane, work - 1);
     const bool writer = base + lane < work;
     const int g = idx / chunks, c = idx % chunks;
-    float big = -INFINITY;
-#pragma unroll 8
-    for (int s = 0; s < a.K; ++s) {
-      const int64_t slot = item * a.K + s;
-      if (slot_visible(a, slot_block(a, slot), ri.pos))
-        big = fmaxf(big, a.part_lse[slot * a.G + g]);
-    }
+    float m = -INFINITY, l = 0.f;
     float acc[V];
 #pragma unroll
     for (int v = 0; v < V; ++v) acc[v] = 0.f;
-    float total = 0.f;
-    if (big != -INFINITY) {
-#pragma unroll 4
-      for (int s = 0; s < a.K; ++s) {
-        const int64_t slot = item * a.K + s;
-        if (!slot_visible(a, slot_block(a, slot), ri.pos)) continue;
-        const float w = __expf(a.part_lse[slot * a.G + g] - big);
-        total += w;
+    for (int s0 = 0; s0 < a.K; s0 += 64) {
+      const int n = min(64, a.K - s0);
+      const bool vis_l = lane < n && slot_visible(a, slot_block(a, slot0 + s0 + lane), ri.pos);
+      const uint64_t vmask = __ballot(vis_l);
+      for (int s = 0; s < n; s += U) {
+        float lse[U];
         union {
           uint4 u;
           PT e[V];
-        } x;
-        x.u = *reinterpret_cast<const uint4*>(static_cast<const PT*>(a.part_o) +
-                                              (slot * a.G + g) * a.Dv + c * V);
+        } x[U];
 #pragma unroll
-        for (int v = 0; v < V; ++v) acc[v] = fmaf(w, (float)x.e[v], acc[v]);
+        for (int j = 0; j < U; ++j) {
+          const int64_t row = (slot0 + s0 + min(s + j, n - 1)) * a.G + g;
+          lse[j] = a.part_lse[row];
+          x[j].u = *reinterpret_cast<const uint4*>(part + row * a.Dv + c * V);
+        }
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+          if (s + j < n && ((vmask >> (s + j)) & 1)) {
+            const float mn = fmaxf(m, lse[j]);
+            const float sc = __expf(m - mn);
+            const float w = __expf(lse[j] - mn);
+            l = fmaf(l, sc, w);
+#pragma unroll
+            for (int v = 0; v < V; ++v) acc[v] = fmaf(acc[v], sc, w * (float)x[j].e[v]);
+            m = mn;
+          }
+        }
       }
     }
     if (!writer) continue;
-    const float inv = total > 0.f ? 1.f / total : 0.f;
+    const float inv = l > 0.f ? 1.f / l : 0.f;
     const int64_t orow = item * a.G + g;  // == ((b*T + t)*Hq + h*G + g)
     T* out = static_cast<T*>(a.out) + orow * a.Dv + c * V;
 #pragma unroll
@@ -668,14 +680,10 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a, int64_t i
 #pragma unroll
       for (int v = 0; v < V; ++v) out32[v] = acc[v] * inv;
     }
-    if (c == 0) a.lse_out[orow] = big == -INFINITY ? -INFINITY : big + __logf(total);
+    if (c == 0) a.lse_out[orow] = m == -INFINITY ? -INFINITY : m + __logf(l);
   }
 }
 
-// ------------------------------------------------------------------ backward
-
-// delta[row] = sum_d dO[row, d] * O[row, d] (float32; O before its 16-bit
-// rounding when the forward kept it), one wave per row.
 template <typename T>
 __global__ void __launch_bounds__(256) attn_delta_kernel(AttnArgs a, int64_t rows) {
   const int lane = threadIdx.x & 63;
