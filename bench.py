@@ -60,16 +60,55 @@ def copy_probe():
 
 # ---------------------------------------------------------------- work counts
 
-def tile_count(w, valid, ids):
-    """Tiles of <= TILE requests per (batch, kv head, block) group."""
+def query_window(tokens, row_bytes):
+    """Query tokens per bucketing window (mirrors query_window in csrc/pisa_capi.hip)."""
+    w = 256
+    while w * 2 * max(row_bytes, 1) <= (8 << 20):
+        w *= 2
+    return max(1, min(w, tokens))
+
+
+def tile_count(w, valid, ids, elem):
+    """Tiles of <= TILE requests per (batch, kv head, block) group, bucketed per
+    window of query tokens over the flattened (batch, token) axis."""
     import torch
     blocks = math.ceil(w.keys / w.block_size)
+    G = w.query_heads // w.key_heads
+    window = query_window(w.batch * w.tokens, G * w.head_dim * elem)
+    windows = math.ceil(w.batch * w.tokens / window)
     dev = ids.device
     b = torch.arange(w.batch, device=dev)[:, None, None, None]
+    t = torch.arange(w.tokens, device=dev)[None, :, None, None]
     h = torch.arange(w.key_heads, device=dev)[None, None, :, None]
-    group = ((b * w.key_heads + h) * blocks + ids)[valid]
-    per = torch.bincount(group, minlength=w.batch * w.key_heads * blocks)
+    win = (b * w.tokens + t) // window
+    group = ((win * w.batch * w.key_heads + b * w.key_heads + h) * blocks + ids)[valid]
+    per = torch.bincount(group, minlength=windows * w.batch * w.key_heads * blocks)
     return int(((per + TILE - 1) // TILE).sum())
+
+# kernel names of the bench's timing keys in the rocprofv3 summaries under profiles/
+PROFILED = {"attn_fwd": "attn_fwd_tile_kernel", "leaf": "leaf_tile_kernel",
+            "route": "route_grouped_kernel", "attn_combine": "attn_combine_kernel",
+            "final": "final_kernel"}
+
+
+def profiled_traffic(kernel, workload):
+    """HBM bytes per launch of ``kernel`` from the committed rocprofv3 PMC summary
+    of ``workload`` (profiles/<workload>_kernels.md: FETCH_SIZE and WRITE_SIZE per
+    dispatch, scaled by a plain copy), or None when no summary covers it."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        f"{workload}_kernels.md")
+    name = PROFILED.get(kernel)
+    if not name or not os.path.exists(path):
+        return None
+    for line in open(path):
+        cells = [c.strip().strip("`") for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 5 and cells[0].startswith(name + "<") and cells[0] != name:
+            try:
+                return int(float(cells[4]) * 1e9)   # total GB per dispatch
+            except ValueError:
+                return None
+    return None
+
 
 def selection_counts(P, w, q, k, positions):
     """Exact scoreable request counts per level (from the per-level selections)."""
@@ -105,11 +144,11 @@ def selection_counts(P, w, q, k, positions):
             scoreable &= (valid.sum(-1, keepdim=True) > w.topk)
         counts[level] = int(scoreable.sum())
         if level == 0 and w.method != "pisa1":
-            tiles = tile_count(w, scoreable, cand)
+            tiles = tile_count(w, scoreable, cand, q.element_size())
     return ids, counts, tiles, top, first
 
 
-def attention_counts(w, ids, positions):
+def attention_counts(w, ids, positions, elem):
     """(requests, tiles, visible (row, key) pairs per KV head) of the attention step."""
     import torch
     blocks = math.ceil(w.keys / w.block_size)
@@ -119,7 +158,7 @@ def attention_counts(w, ids, positions):
     keys = torch.minimum(torch.minimum(torch.full_like(ids, w.block_size), w.keys - start),
                          pos - start + 1).clamp(min=0)
     pairs = int(torch.where(vis, keys, 0).sum())
-    return int(vis.sum()), tile_count(w, vis, ids), pairs
+    return int(vis.sum()), tile_count(w, vis, ids, elem), pairs
 
 
 # ---------------------------------------------------------------- CPU baseline
@@ -221,7 +260,7 @@ def main():
 
         print("[bench] work counts", file=sys.stderr, flush=True)
         ids, counts, leaf_tiles, top, first = selection_counts(P, w, q, k, positions)
-        requests, attn_tiles, pairs = attention_counts(w, ids, positions)
+        requests, attn_tiles, pairs = attention_counts(w, ids, positions, q.element_size())
 
     e = q.element_size()
     pe = 4 if e == 4 else 2    # partial rows: fp16 for 16-bit inputs, fp32 for fp32
@@ -248,14 +287,26 @@ def main():
                          "bytes": requests * G * (D * pe + 4) + items * G * (D * e + 4)},
         "pool": {"bound": "hbm", "bytes": w.batch * w.keys * w.key_heads * D * e},
     }
-    dominant = max(per_step, key=per_step.get)
-    dom_ms = per_step[dominant] / max(launches[dominant], 1)
-    info = algo.get(dominant, {"bound": "hbm", "bytes": 0})
-    achieved = info["bytes"] / (dom_ms * 1e-3)
+    # the dominant kernel: its algorithmic bytes per step over its time per step
+    # (= bytes per launch over the average launch: the windowed kernels launch
+    # once per window of query tokens)
+    dominant = max((n for n in per_step if n in algo), key=per_step.get)
+    n_launch = max(launches[dominant], 1)
+    dom_ms = per_step[dominant] / n_launch
+    info = algo[dominant]
+    achieved = info["bytes"] / (per_step[dominant] * 1e-3)
+    traffic = profiled_traffic(dominant, w.name)
     roofline = {"kernel": dominant, "bound": "hbm", "achieved": round(achieved / 1e9, 1),
                 "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4),
-                "traffic": None, "avg_launch_ms": round(dom_ms, 4),
-                "algorithmic_bytes": int(info["bytes"])}
+                "traffic": traffic, "avg_launch_ms": round(dom_ms, 4),
+                "launches_per_step": n_launch,
+                "algorithmic_bytes_per_launch": int(info["bytes"] / n_launch)}
+    # the survey's Q4 gather model of selection bytes (reference schedule)
+    q4_bytes = (w.batch * w.tokens * w.query_heads * D * e + r_int * w.branching * D * e
+                + items * width * 4
+                + math.ceil(r_leaf / 4) * w.block_size * D * e + r_leaf * (G * D * e + 24)
+                + items * (width * 8 + w.topk * 4))
+    gather_bytes = items * 2 * w.topk * w.block_size * D * e
 
     attn_flops = 4 * D * G * pairs
     attn_kernel_ms = per_step.get("attn_fwd", 0) + per_step.get("attn_combine", 0)
@@ -288,6 +339,8 @@ def main():
         "selection_hbm_frac": round(sel_bytes / (sel_ms * 1e-3) / HBM_PEAK, 4),
         "leaf_hbm_frac": round(algo["leaf"]["bytes"] / (leaf_ms * 1e-3) / HBM_PEAK, 4)
         if leaf_ms else None,
+        "selection_q4_model_hbm_frac": round(q4_bytes / (sel_ms * 1e-3) / HBM_PEAK, 4),
+        "sparse_attn_gather_tbps": round(gather_bytes / (att_ms * 1e-3) / 1e12, 2),
         "kernel_ms_per_step": {n: round(t, 4) for n, t in sorted(per_step.items(),
                                                                   key=lambda x: -x[1])},
         "work": {"route_requests": r_int, "leaf_requests": r_leaf, "leaf_tiles": leaf_tiles,

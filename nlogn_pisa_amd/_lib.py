@@ -120,17 +120,22 @@ def _declare(lib):
 
 
 def library():
-    """Load (once) and return the ctypes handle of libpisa_hip.so."""
+    """Load (once) and return the ctypes handle of libpisa_hip.so.
+
+    ``PISA_HIP_LIBRARY`` names another build of the same library (e.g. one
+    compiled with different tuning constants) to load instead.
+    """
     global _lib
     if _lib is not None:
         return _lib
     with _lock:
         if _lib is None:
-            if not os.path.exists(LIBRARY_PATH):
+            path = os.environ.get("PISA_HIP_LIBRARY") or LIBRARY_PATH
+            if not os.path.exists(path):
                 raise RuntimeError(
-                    f"{LIBRARY_PATH} is missing: build it with `python -m nlogn_pisa_amd.build` "
+                    f"{path} is missing: build it with `python -m nlogn_pisa_amd.build` "
                     "(hipcc, gfx950); there is no fallback implementation")
-            lib = ctypes.CDLL(LIBRARY_PATH)
+            lib = ctypes.CDLL(path)
             _declare(lib)
             _lib = lib
     return _lib

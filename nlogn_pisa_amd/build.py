@@ -36,9 +36,9 @@ def hipcc():
     return path
 
 
-def _compile(source):
-    obj = os.path.join(OUT_DIR, os.path.basename(source).replace(".hip", ".o"))
-    cmd = [hipcc(), *FLAGS, "-c", source, "-o", obj]
+def _compile(source, obj_dir, extra):
+    obj = os.path.join(obj_dir, os.path.basename(source).replace(".hip", ".o"))
+    cmd = [hipcc(), *FLAGS, *extra, "-c", source, "-o", obj]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(line for line in proc.stderr.splitlines() if noise not in line)
@@ -47,13 +47,17 @@ def _compile(source):
     return obj, err
 
 
-def build(verbose=True):
-    """Compile every HIP source and link ``libpisa_hip.so``; returns its path."""
-    os.makedirs(OUT_DIR, exist_ok=True)
+def build(verbose=True, library=LIBRARY, extra_flags=(), obj_dir=OUT_DIR):
+    """Compile every HIP source and link ``libpisa_hip.so``; returns its path.
+
+    ``library``, ``extra_flags`` (e.g. ``-D`` tuning constants) and ``obj_dir``
+    build another copy of the library, loadable through ``PISA_HIP_LIBRARY``.
+    """
+    os.makedirs(obj_dir, exist_ok=True)
     sources = sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
     workers = min(len(sources), max(1, min(8, os.cpu_count() or 1)))
     with concurrent.futures.ThreadPoolExecutor(workers) as pool:
-        futures = [pool.submit(_compile, src) for src in sources]
+        futures = [pool.submit(_compile, src, obj_dir, tuple(extra_flags)) for src in sources]
     errors = [f.exception() for f in futures if f.exception() is not None]
     if errors:
         raise RuntimeError("\n".join(str(e) for e in errors))
@@ -61,16 +65,16 @@ def build(verbose=True):
     for obj, err in results:
         if verbose and err.strip():
             print(err, file=sys.stderr)
-    tmp = LIBRARY + ".tmp"
+    tmp = library + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp,
            *(obj for obj, _ in results)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stderr}")
-    os.replace(tmp, LIBRARY)
+    os.replace(tmp, library)
     if verbose:
-        print(f"built {LIBRARY}")
-    return LIBRARY
+        print(f"built {library}")
+    return library
 
 
 if __name__ == "__main__":

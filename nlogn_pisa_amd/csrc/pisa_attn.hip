@@ -325,9 +325,11 @@ __global__ void __launch_bounds__(64) attn_fwd_direct_kernel(AttnArgs a, int64_t
 // is value (r >> 2) D/4 + 4 dt + (r & 3)) so that lane group grp ends with
 // values [grp D/4, (grp+1) D/4) of its row: a lane loads one contiguous
 // quarter of a query row and stores one contiguous quarter of a partial row.
-// Per-request bookkeeping (query row offset, position, slot) is computed once
-// per tile into LDS, and each wave loads the next unit's query rows while it
-// computes the current one.
+// V^T rows are stored in the order the lanes read them (vt_row), and for
+// blocks of up to 64 keys each wave keeps its K fragments in registers for the
+// whole tile.  Per-request bookkeeping (query row offset, position, slot) is
+// computed once per tile into LDS, and each wave loads the next unit's query
+// rows while it computes the current one.
 
 // LDS of one tile: K block [Cq][HD + PAD], V^T [HD][Cq + PAD], then per request
 // the query row offset (int64), position (int64) and slot (int32).
@@ -359,9 +361,32 @@ __host__ __device__ inline TileLds tile_lds(int C, int tile) {
   return L;
 }
 
-// Stage the K block row-major and the V block transposed, zero from `rows` up
-// to Cq keys.  16-bit V^T is written two keys per 32-bit word with consecutive
-// lanes on consecutive key pairs.
+// Tuning constants of the forward tile kernel: query-row prefetch depth
+// (units), key fragments in registers (blocks of up to 64 keys), minimum waves
+// per SIMD requested from the compiler.
+#ifndef PISA_ATTN_DEPTH
+#define PISA_ATTN_DEPTH 2
+#endif
+#ifndef PISA_ATTN_KREG
+#define PISA_ATTN_KREG 0
+#endif
+#ifndef PISA_ATTN_WAVES
+#define PISA_ATTN_WAVES 2
+#endif
+
+// LDS row of value dv in V^T: dv = (D/4) j + 4 dt + c is stored at row
+// 16 dt + 4 j + c, the row that lane col = 4 j + c reads for dv tile dt, so the
+// 16 lanes of a lane group read 16 consecutive rows.
+template <int HD>
+__device__ __forceinline__ int vt_row(int dv) {
+  constexpr int QL = HD / 4;
+  const int j = dv / QL, rem = dv % QL;
+  return 16 * (rem >> 2) + 4 * j + (rem & 3);
+}
+
+// Stage the K block row-major and the V block transposed (rows in vt_row
+// order), zero from `rows` up to Cq keys.  16-bit V^T is written two keys per
+// 32-bit word with consecutive lanes on consecutive key pairs.
 template <typename T, int HD>
 __device__ void stage_tile(const AttnArgs& a, int b, int h, int64_t blk, int rows, T* ks, T* vt,
                            const TileLds& L, int tid, int nthr) {
@@ -391,7 +416,8 @@ __device__ void stage_tile(const AttnArgs& a, int b, int h, int64_t blk, int row
       if (r + 1 < rows) v1.u = *reinterpret_cast<const uint4*>(vb + (int64_t)(r + 1) * a.v_token + c);
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        *reinterpret_cast<uint32_t*>(vt + (c + e) * L.ldv + r) = (uint32_t)v0.e[e] | ((uint32_t)v1.e[e] << 16);
+        *reinterpret_cast<uint32_t*>(vt + vt_row<HD>(c + e) * L.ldv + r) =
+            (uint32_t)v0.e[e] | ((uint32_t)v1.e[e] << 16);
     }
   } else {
     for (int idx = tid; idx < L.Cq * vpr; idx += nthr) {
@@ -399,10 +425,10 @@ __device__ void stage_tile(const AttnArgs& a, int b, int h, int64_t blk, int row
       float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
       if (r < rows) v = *reinterpret_cast<const float4*>(vb + (int64_t)r * a.v_token + c);
       float* vf = reinterpret_cast<float*>(vt);
-      vf[(c + 0) * L.ldv + r] = v.x;
-      vf[(c + 1) * L.ldv + r] = v.y;
-      vf[(c + 2) * L.ldv + r] = v.z;
-      vf[(c + 3) * L.ldv + r] = v.w;
+      vf[vt_row<HD>(c + 0) * L.ldv + r] = v.x;
+      vf[vt_row<HD>(c + 1) * L.ldv + r] = v.y;
+      vf[vt_row<HD>(c + 2) * L.ldv + r] = v.z;
+      vf[vt_row<HD>(c + 3) * L.ldv + r] = v.w;
     }
   }
 }
@@ -440,61 +466,77 @@ __device__ void fwd_tile_units(const AttnArgs& a, const TileLds& L, const T* ks,
   const int col = lane & 15, grp = lane >> 4;
   const int NT = L.Cq / 16;     // key tiles, <= NTM
   const int NK = NT * 4 / E;    // P V steps
-  const int Gp = a.Gp;
-  const int units = (nreq * Gp + 15) / 16;
+  const int Gp = a.Gp;               // a power of two
+  const int gl = 31 - __clz(Gp);     // log2 Gp
+  const int units = (nreq * Gp + 15) >> 4;
   const T* q = static_cast<const T*>(a.q);
 
-  frag qf[DS];
-  {
-    const int rho = wave * 16 + col, rq = rho / Gp, gh = rho % Gp;
-    if (wave < units && rq < nreq && gh < a.G)
-      load_frags(q + mq[rq] + (int64_t)gh * HD + QL * grp, qf);
-    else
-      zero_frags(qf);
+  // key-block A fragments held in registers when they take at most 64 VGPRs
+  // (blocks of up to 64 keys)
+  constexpr bool KREG = PISA_ATTN_KREG && NTM <= 4 && NTM * QL * sizeof(T) <= 256;
+  constexpr int DEPTH = NTM <= 4 ? PISA_ATTN_DEPTH : 1;
+  constexpr int KR = KREG ? NTM : 1;
+  frag kreg[KR][DS];
+#pragma unroll
+  for (int mt = 0; mt < KR; ++mt) {
+    if (KREG && mt < NT) load_frags(ks + (mt * 16 + col) * L.ldk + QL * grp, kreg[mt]);
+    else zero_frags(kreg[mt]);
   }
-  for (int u = wave; u < units; u += nwaves) {
-    // next unit's query rows
-    frag qn[DS];
-    {
-      const int un = u + nwaves;
-      const int rho = un * 16 + col, rq = rho / Gp, gh = rho % Gp;
-      if (un < units && rq < nreq && gh < a.G)
-        load_frags(q + mq[rq] + (int64_t)gh * HD + QL * grp, qn);
-      else
-        zero_frags(qn);
-    }
+
+  // Query rows of unit u.  The load is issued by every lane: rows that do not
+  // exist (padding heads or requests, units past the end) read request 0's
+  // first head instead and are masked out of the softmax and never stored, so
+  // no load sits behind a branch and the compiler keeps later loads in flight.
+  auto fetch = [&](int u, frag (&f)[DS]) {
+    const int rho = (u << 4) + col, rq = rho >> gl, gh = rho & (Gp - 1);
+    const bool ok = u < units && rq < nreq && gh < a.G;
+    load_frags(q + mq[ok ? rq : 0] + (int64_t)(ok ? gh : 0) * HD + QL * grp, f);
+  };
+  // units wave, wave + nwaves, ...: the next DEPTH units' query rows are in
+  // flight while one is computed.  Unit u is computed from `qf`, loads unit u + DEPTH nwaves into `into` (the
+  // buffer the previous unit used); buffers rotate by unrolling, never by
+  // copies, so the loads in flight are not waited for early
+  auto unit = [&](int u, frag (&qf)[DS], frag (&into)[DS]) {
+    fetch(u + DEPTH * nwaves, into);
     // S^T = K Q^T
     f4 s[NTM];
 #pragma unroll
     for (int mt = 0; mt < NTM; ++mt) {
       s[mt] = f4{0.f, 0.f, 0.f, 0.f};
       if (mt < NT) {
-        frag kf[DS];
-        load_frags(ks + (mt * 16 + col) * L.ldk + QL * grp, kf);
+        if constexpr (KREG) {
 #pragma unroll
-        for (int d = 0; d < DS; ++d) s[mt] = Op::mma(kf[d], qf[d], s[mt]);
+          for (int d = 0; d < DS; ++d) s[mt] = Op::mma(kreg[mt][d], qf[d], s[mt]);
+        } else {
+          frag kf[DS];
+          load_frags(ks + (mt * 16 + col) * L.ldk + QL * grp, kf);
+#pragma unroll
+          for (int d = 0; d < DS; ++d) s[mt] = Op::mma(kf[d], qf[d], s[mt]);
+        }
       }
     }
-    // softmax statistics of row `col` (lane groups hold disjoint keys)
-    const int rho = u * 16 + col, rq = rho / Gp, gh = rho % Gp;
+    // softmax statistics of row `col` (lane groups hold disjoint keys); this
+    // lane's keys 16 mt + 4 grp + i are visible below `lim`
+    const int rho = (u << 4) + col, rq = rho >> gl, gh = rho & (Gp - 1);
     const bool valid = rq < nreq && gh < a.G;
-    const int64_t pos = valid ? mpos[rq] : -1;
+    int lim = -1;
+    if (valid) {
+      const int64_t last = a.causal ? mpos[rq] - blk * a.C + 1 : (int64_t)rows;  // keys <= pos
+      lim = (int)min((int64_t)rows, last) - 4 * grp;
+    }
     float m = -INFINITY;
 #pragma unroll
     for (int mt = 0; mt < NTM; ++mt) {
       if (mt < NT) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int key = mt * 16 + 4 * grp + i;
-          const bool ok = valid && key < rows && (!a.causal || blk * a.C + key <= pos);
-          const float z = ok ? s[mt][i] * a.scale : -INFINITY;
+          const float z = mt * 16 + i < lim ? s[mt][i] * a.scale : -INFINITY;
           s[mt][i] = z;
           m = fmaxf(m, z);
         }
       }
     }
-    m = fmaxf(m, __shfl_xor(m, 16));
-    m = fmaxf(m, __shfl_xor(m, 32));
+    m = xor32_max(xor16_max(m));
     const float safe = m == -INFINITY ? 0.f : m;
     float l = 0.f;
 #pragma unroll
@@ -508,8 +550,7 @@ __device__ void fwd_tile_units(const AttnArgs& a, const TileLds& L, const T* ks,
         }
       }
     }
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
+    l = xor32_sum(xor16_sum(l));
     // O^T = V^T P^T, P entering as hi + lo for 16-bit types
     f4 o[NDT];
 #pragma unroll
@@ -527,7 +568,7 @@ __device__ void fwd_tile_units(const AttnArgs& a, const TileLds& L, const T* ks,
         }
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
-          const T* vrow = vt + (QL * (col >> 2) + 4 * dt + (col & 3)) * L.ldv;
+          const T* vrow = vt + (16 * dt + col) * L.ldv;  // vt_row of this lane's A row
           const frag vf = load_vt<T, E>(vrow, kk, grp);
           o[dt] = Op::mma(vf, ph, o[dt]);
           if constexpr (kSplit<T>) o[dt] = Op::mma(vf, pl, o[dt]);
@@ -545,13 +586,19 @@ __device__ void fwd_tile_units(const AttnArgs& a, const TileLds& L, const T* ks,
       store_vals(static_cast<PT*>(a.part_o) + prow * HD + QL * grp, vals);
       if (grp == 0) a.part_lse[prow] = m + __logf(l);
     }
+  };
+  frag qb[DEPTH + 1][DS];
 #pragma unroll
-    for (int d = 0; d < DS; ++d) qf[d] = qn[d];
+  for (int p = 0; p < DEPTH; ++p) fetch(wave + p * nwaves, qb[p]);
+  for (int u0 = wave; u0 < units; u0 += (DEPTH + 1) * nwaves) {
+#pragma unroll
+    for (int p = 0; p <= DEPTH; ++p)
+      if (u0 + p * nwaves < units) unit(u0 + p * nwaves, qb[p], qb[(p + DEPTH) % (DEPTH + 1)]);
   }
 }
 
 template <typename T, int HD, int NTM>
-__global__ void __launch_bounds__(256, 2) attn_fwd_tile_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(256, PISA_ATTN_WAVES) attn_fwd_tile_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const TileLds L = tile_lds<T, HD>(a.C, a.tile);
   T* ks = reinterpret_cast<T*>(smem + L.k_off);
@@ -1055,7 +1102,7 @@ static bool tile_path(const AttnArgs& a) {
 }
 
 template <typename T>
-static int attn_fwd_t(const AttnArgs& a, bool grouped, int64_t slots, int64_t items, hipStream_t stream) {
+static int attn_partials_t(const AttnArgs& a, bool grouped, int64_t slots, hipStream_t stream) {
   const int es = sizeof(T);
   if (tile_path(a)) {
     switch (a.D) {
@@ -1073,19 +1120,28 @@ static int attn_fwd_t(const AttnArgs& a, bool grouped, int64_t slots, int64_t it
     allow_lds((const void*)attn_fwd_direct_kernel<T>, lds);
     PISA_TIMED("attn_fwd_direct", stream, hipLaunchKernelGGL(attn_fwd_direct_kernel<T>, dim3(slots), dim3(64), lds, stream, a, slots));
   }
-  if (items > 0)
-    PISA_TIMED("attn_combine", stream, hipLaunchKernelGGL(attn_combine_kernel<T>, dim3((items + 3) / 4), dim3(256), 0, stream, a, items));
   return check_launch("attention forward");
 }
 
-int launch_attn_fwd(int dtype, const AttnArgs& a, bool grouped, int64_t slots, int64_t items,
-                    hipStream_t stream) {
+int launch_attn_partials(int dtype, const AttnArgs& a, bool grouped, int64_t slots, hipStream_t stream) {
   switch (dtype) {
-    case PISA_F32: return attn_fwd_t<float>(a, grouped, slots, items, stream);
-    case PISA_F16: return attn_fwd_t<f16_t>(a, grouped, slots, items, stream);
-    case PISA_BF16: return attn_fwd_t<bf16_t>(a, grouped, slots, items, stream);
+    case PISA_F32: return attn_partials_t<float>(a, grouped, slots, stream);
+    case PISA_F16: return attn_partials_t<f16_t>(a, grouped, slots, stream);
+    case PISA_BF16: return attn_partials_t<bf16_t>(a, grouped, slots, stream);
     default: return fail(PISA_ERR_INVALID, "unknown dtype %d", dtype);
   }
+}
+
+int launch_attn_combine(int dtype, const AttnArgs& a, int64_t items, hipStream_t stream) {
+  if (items <= 0) return PISA_OK;
+  const dim3 grid((unsigned)((items + 3) / 4)), block(256);
+  switch (dtype) {
+    case PISA_F32: PISA_TIMED("attn_combine", stream, hipLaunchKernelGGL(attn_combine_kernel<float>, grid, block, 0, stream, a, items)); break;
+    case PISA_F16: PISA_TIMED("attn_combine", stream, hipLaunchKernelGGL(attn_combine_kernel<f16_t>, grid, block, 0, stream, a, items)); break;
+    case PISA_BF16: PISA_TIMED("attn_combine", stream, hipLaunchKernelGGL(attn_combine_kernel<bf16_t>, grid, block, 0, stream, a, items)); break;
+    default: return fail(PISA_ERR_INVALID, "unknown dtype %d", dtype);
+  }
+  return check_launch("attention combine");
 }
 
 template <typename T, int HD>

@@ -5,6 +5,8 @@
 #include "pisa_device.h"
 #include "pisa_internal.h"
 
+#include <algorithm>
+
 using namespace pisa;
 
 namespace {
@@ -16,7 +18,29 @@ bool pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
-int padded_group(int g) { return g <= 16 ? next_pow2(g) : (g + 15) / 16 * 16; }
+// Query heads per kv head padded to a power of two (rows of a request in the
+// 16-row MFMA units: 16 / Gp requests per unit, or Gp / 16 units per request).
+int padded_group(int g) { return next_pow2(g); }
+
+}  // namespace
+
+namespace pisa {
+
+// Window budget: q bytes of one kv head per window (0: a single window).
+#ifndef PISA_WINDOW_BYTES
+#define PISA_WINDOW_BYTES (8 << 20)
+#endif
+
+int query_window(int64_t tokens, int64_t row_bytes) {
+  if (PISA_WINDOW_BYTES <= 0) return (int)std::max<int64_t>(1, tokens);
+  int64_t w = 256;
+  while (w * 2 * std::max<int64_t>(row_bytes, 1) <= (int64_t)PISA_WINDOW_BYTES) w *= 2;
+  return (int)std::max<int64_t>(1, std::min<int64_t>(w, tokens));
+}
+
+}  // namespace pisa
+
+namespace {
 
 int check_qk(const pisa_qk_desc* qk) {
   if (!qk) return fail(PISA_ERR_INVALID, "null descriptor");
@@ -41,6 +65,8 @@ struct SelectPlan {
   int64_t groups;
   int M0;
   int G;
+  int window;            // query tokens bucketed and scored per leaf pass
+  int64_t window_slots;  // slots of one window
 };
 
 int plan_select(const pisa_qk_desc* qk, const pisa_select_params* p, SelectPlan& pl) {
@@ -69,6 +95,9 @@ int plan_select(const pisa_qk_desc* qk, const pisa_select_params* p, SelectPlan&
   pl.grouped = p->schedule == PISA_SCHEDULE_GROUPED && p->method != PISA_METHOD_PISA1;
   pl.slots = pl.items * pl.W;
   pl.groups = (int64_t)qk->batch * qk->key_heads * pl.M0;
+  const int64_t flat = (int64_t)qk->batch * qk->query_tokens;
+  pl.window = query_window(flat, (int64_t)G * D * dtype_size(qk->dtype));
+  pl.window_slots = (int64_t)pl.window * qk->key_heads * pl.W;
   return PISA_OK;
 }
 
@@ -83,7 +112,7 @@ void carve_select(const SelectPlan& pl, Carve& c, SelectBuffers& sb) {
   sb.cand = c.take<int32_t>(pl.slots);
   sb.scoreable = c.take<uint8_t>(pl.slots);
   sb.scores = c.take<float>(pl.slots);
-  carve_buckets(c, sb.buckets, pl.slots, pl.groups, kLeafTile);
+  carve_buckets(c, sb.buckets, pl.window_slots, pl.groups, kLeafTile);
 }
 
 LeafArgs leaf_args(const pisa_qk_desc* qk, int method, int block_size, int W, int M0, int G,
@@ -196,14 +225,20 @@ extern "C" int pisa_select(const pisa_qk_desc* qk, const pisa_select_params* p, 
   rc = launch_route(qk->dtype, a, pl.items, threads, st);
   if (rc || !pl.grouped) return rc;
 
+  // leaf scoring one window of query tokens at a time (flattened batch x token)
   LeafRequests req{sb.cand, sb.scoreable, pl.W, qk->key_heads, qk->query_tokens, pl.M0};
-  rc = bucket_leaf(req, pl.slots, sb.buckets, st);
-  if (rc) return rc;
   LeafArgs la = leaf_args(qk, p->method, p->block_size, pl.W, pl.M0, pl.G, q, k,
                           qk->k_stride_batch, qk->k_stride_token, qk->key_tokens, p->block_size,
                           sb.buckets, sb.scores);
-  rc = launch_leaf(qk->dtype, la, st);
-  if (rc) return rc;
+  const int64_t flat = (int64_t)qk->batch * qk->query_tokens;
+  const int64_t per_token = (int64_t)qk->key_heads * pl.W;
+  for (int64_t u0 = 0; u0 < flat; u0 += pl.window) {
+    const int64_t u1 = std::min<int64_t>(flat, u0 + pl.window);
+    rc = bucket_leaf(req, u0 * per_token, u1 * per_token, sb.buckets, st);
+    if (rc) return rc;
+    rc = launch_leaf(qk->dtype, la, st);
+    if (rc) return rc;
+  }
   FinalArgs f;
   f.cand = sb.cand;
   f.scoreable = sb.scoreable;
@@ -227,13 +262,18 @@ extern "C" int pisa_select(const pisa_qk_desc* qk, const pisa_select_params* p, 
 
 namespace {
 
+int leaf_window(const pisa_qk_desc* qk) {
+  return query_window((int64_t)qk->batch * qk->query_tokens,
+                      (int64_t)(qk->query_heads / qk->key_heads) * qk->head_dim * dtype_size(qk->dtype));
+}
+
 void carve_leaf(const pisa_qk_desc* qk, int block_size, int width, Carve& c, uint8_t** mask,
                 Buckets& b) {
   const int M0 = (qk->key_tokens + block_size - 1) / block_size;
   const int64_t slots = (int64_t)qk->batch * qk->query_tokens * qk->key_heads * width;
   const int64_t groups = (int64_t)qk->batch * qk->key_heads * M0;
   *mask = c.take<uint8_t>(slots);
-  carve_buckets(c, b, slots, groups, kLeafTile);
+  carve_buckets(c, b, (int64_t)leaf_window(qk) * qk->key_heads * width, groups, kLeafTile);
 }
 
 }  // namespace
@@ -296,15 +336,23 @@ extern "C" int pisa_leaf_scores(const pisa_qk_desc* qk, const pisa_select_params
   rc = launch_scoreable(m, st);
   if (rc) return rc;
   LeafRequests req{candidates, mask, width, qk->key_heads, qk->query_tokens, M0};
-  rc = bucket_leaf(req, slots, b, st);
-  if (rc) return rc;
   const bool pisa1 = p->method == PISA_METHOD_PISA1;
   const int64_t row = (int64_t)qk->key_heads * qk->head_dim;
   LeafArgs la = leaf_args(qk, p->method, p->block_size, width, M0, G, q, pisa1 ? leaf_means : k,
                           pisa1 ? leaf_means_stride_batch : qk->k_stride_batch,
                           pisa1 ? row : qk->k_stride_token, pisa1 ? M0 : qk->key_tokens,
                           pisa1 ? 1 : p->block_size, b, scores);
-  return launch_leaf(qk->dtype, la, st);
+  const int window = leaf_window(qk);
+  const int64_t flat = (int64_t)qk->batch * qk->query_tokens;
+  for (int64_t u0 = 0; u0 < flat; u0 += window) {
+    const int64_t u1 = std::min<int64_t>(flat, u0 + window);
+    rc = bucket_leaf(req, u0 * width * qk->key_heads, u1 * width * qk->key_heads, b, st);
+    if (rc) return rc;
+    rc = launch_leaf(qk->dtype, la, st);
+    if (rc) return rc;
+  }
+  (void)slots;
+  return PISA_OK;
 }
 
 // ------------------------------------------------------------------ attention
@@ -315,6 +363,8 @@ struct AttnPlan {
   int64_t slots, items, groups;
   int M0, G, Cp;
   bool grouped;
+  int window;            // query tokens bucketed per forward pass
+  int64_t window_slots;
 };
 
 int plan_attn(const pisa_attn_desc* d, AttnPlan& pl) {
@@ -340,6 +390,8 @@ int plan_attn(const pisa_attn_desc* d, AttnPlan& pl) {
   pl.groups = (int64_t)d->batch * d->key_heads * pl.M0;
   pl.Cp = (d->block_size + 15) / 16 * 16;
   pl.grouped = pl.slots >= 4 * pl.groups;
+  pl.window = query_window((int64_t)d->batch * d->query_tokens, (int64_t)pl.G * d->head_dim * es);
+  pl.window_slots = (int64_t)pl.window * d->key_heads * d->topk;
   return PISA_OK;
 }
 
@@ -381,7 +433,7 @@ void carve_attn(const pisa_attn_desc* d, const AttnPlan& pl, bool backward, Carv
     const size_t part_elem = d->dtype == PISA_F32 ? 4 : 2;
     a.part_o = c.take<char>(pl.slots * pl.G * d->value_dim * part_elem);
     a.part_lse = c.take<float>(pl.slots * pl.G);
-    if (pl.grouped) carve_buckets(c, b, pl.slots, pl.groups, kAttnTile);
+    if (pl.grouped) carve_buckets(c, b, pl.window_slots, pl.groups, kAttnTile);
   } else {
     a.delta = c.take<float>(pl.items * pl.G);
     a.part_dq = c.take<float>(pl.slots * pl.G * d->head_dim);
@@ -452,11 +504,23 @@ extern "C" int pisa_sparse_attention_fwd(const pisa_attn_desc* d, const void* q,
   a.lse_out = lse;
   hipStream_t st = (hipStream_t)stream;
   if (pl.grouped) {
-    rc = bucket_attn(attn_requests(d, pl, indices, positions, positions_stride_batch), pl.slots, b, st);
-    if (rc) return rc;
+    // partials one window of query tokens at a time (flattened batch x token)
     bind_buckets(a, b);
+    const AttnRequests req = attn_requests(d, pl, indices, positions, positions_stride_batch);
+    const int64_t flat = (int64_t)d->batch * d->query_tokens;
+    const int64_t per_token = (int64_t)d->key_heads * d->topk;
+    for (int64_t u0 = 0; u0 < flat; u0 += pl.window) {
+      const int64_t u1 = std::min<int64_t>(flat, u0 + pl.window);
+      rc = bucket_attn(req, u0 * per_token, u1 * per_token, b, st);
+      if (rc) return rc;
+      rc = launch_attn_partials(d->dtype, a, true, pl.slots, st);
+      if (rc) return rc;
+    }
+  } else {
+    rc = launch_attn_partials(d->dtype, a, false, pl.slots, st);
+    if (rc) return rc;
   }
-  return launch_attn_fwd(d->dtype, a, pl.grouped, pl.slots, pl.items, st);
+  return launch_attn_combine(d->dtype, a, pl.items, st);
 }
 
 extern "C" int pisa_sparse_attention_bwd(const pisa_attn_desc* d, const void* q, const void* k,
@@ -495,7 +559,7 @@ extern "C" int pisa_sparse_attention_bwd(const pisa_attn_desc* d, const void* q,
   a.dv_token = (int64_t)d->key_heads * d->value_dim;
   a.dv_batch = (int64_t)d->key_tokens * a.dv_token;
   hipStream_t st = (hipStream_t)stream;
-  rc = bucket_attn(attn_requests(d, pl, indices, positions, positions_stride_batch), pl.slots, b, st);
+  rc = bucket_attn(attn_requests(d, pl, indices, positions, positions_stride_batch), 0, pl.slots, b, st);
   if (rc) return rc;
   bind_buckets(a, b);
   return launch_attn_bwd(d->dtype, a, pl.groups, pl.items, st);

@@ -133,6 +133,38 @@ __device__ __forceinline__ float row_max16(float v) {
   return v;
 }
 
+// Combine lanes l and l ^ 16 (xor16) or l and l ^ 32 (xor32) with gfx950's
+// lane-swap instructions: v_permlane16_swap / v_permlane32_swap of a register
+// with itself leave, in every lane, its own value in one result and its
+// partner's in the other, so the sum or max of the two is the all-reduce.
+__device__ __forceinline__ float xor16_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor16_max(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// Sum over aligned groups of n lanes (n in {1, 2, 4, 8, 16}) within each DPP
+// row: quad_perm xor 1 and xor 2, then row_half_mirror and row_mirror (each
+// lane adds the lane mirrored across its 8- or 16-lane group).
+__device__ __forceinline__ float group_sum(float v, int n) {
+  if (n >= 2) v += dpp_f<0xB1>(v);
+  if (n >= 4) v += dpp_f<0x4E>(v);
+  if (n >= 8) v += dpp_f<0x141>(v);
+  if (n >= 16) v += dpp_f<0x140>(v);
+  return v;
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
   v = row_sum16(v);
   v += __shfl_xor(v, 16);

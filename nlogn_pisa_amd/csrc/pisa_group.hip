@@ -5,9 +5,11 @@
 // visible selected block of sparse attention.  Requests are bucketed by
 // group = (batch * Hkv + head) * blocks + block and cut into tiles of at most
 // `tile` requests of one group, so a consumer loads each key block once per
-// tile.  Three launches, no host read of a count (the tile array is sized for
-// the worst case, ceil(slots / tile) + groups, as the reference does):
-//   count   - per-workgroup LDS histogram, one global atomic per non-empty bin;
+// tile.  Three launches per range of slots, no host read of a count (the tile
+// array is sized for the worst case, ceil(slots / tile) + groups, as the
+// reference does):
+//   count   - per-workgroup LDS histogram, one global atomic per non-empty bin
+//             (ranges too small to fill the device: direct global atomics);
 //   scan    - tiles per group, exclusive prefix sum, total tile count;
 //   scatter - LDS ranks plus one reserved global range per bin and workgroup.
 // Request order inside a group is unspecified; every consumer computes each
@@ -22,7 +24,9 @@ namespace pisa {
 
 constexpr int kLdsGroups = 16384;  // 64 KB of int32 bins
 constexpr int kBucketThreads = 256;
-constexpr int64_t kBucketChunk = 32768;
+constexpr int64_t kBucketChunk = 32768;          // slots per workgroup with LDS bins
+constexpr int64_t kSmallChunk = 4096;            // slots per workgroup with global atomics
+constexpr int64_t kLdsMinSlots = kBucketChunk * 256;  // LDS bins from 256 workgroups up
 
 struct LeafSrc {
   LeafRequests r;
@@ -67,12 +71,13 @@ __global__ void fill_i32_kernel(int32_t* p, int64_t n, int32_t v) {
 }
 
 template <typename Src>
-__global__ void __launch_bounds__(kBucketThreads) bucket_count_kernel(Src src, int64_t slots,
-                                                                      int groups, int32_t* counts) {
+__global__ void __launch_bounds__(kBucketThreads) bucket_count_kernel(Src src, int64_t slot_begin,
+                                                                      int64_t slot_end, int64_t chunk,
+                                                                      int groups, int lds,
+                                                                      int32_t* counts) {
   extern __shared__ int hist[];
-  const bool lds = groups <= kLdsGroups;
-  const int64_t begin = (int64_t)blockIdx.x * kBucketChunk;
-  const int64_t end = min(slots, begin + kBucketChunk);
+  const int64_t begin = slot_begin + (int64_t)blockIdx.x * chunk;
+  const int64_t end = min(slot_end, begin + chunk);
   if (lds) {
     for (int g = threadIdx.x; g < groups; g += blockDim.x) hist[g] = 0;
     __syncthreads();
@@ -119,12 +124,12 @@ __global__ void __launch_bounds__(1024) bucket_scan_kernel(const int32_t* counts
 
 template <typename Src>
 __global__ void __launch_bounds__(kBucketThreads) bucket_scatter_kernel(
-    Src src, int64_t slots, int groups, const int32_t* __restrict__ tile_off, int32_t* cursors,
-    int tile, int32_t* __restrict__ tile_group, int32_t* __restrict__ tile_req) {
+    Src src, int64_t slot_begin, int64_t slot_end, int64_t chunk, int groups, int lds,
+    const int32_t* __restrict__ tile_off, int32_t* cursors, int tile,
+    int32_t* __restrict__ tile_group, int32_t* __restrict__ tile_req) {
   extern __shared__ int hist[];
-  const bool lds = groups <= kLdsGroups;
-  const int64_t begin = (int64_t)blockIdx.x * kBucketChunk;
-  const int64_t end = min(slots, begin + kBucketChunk);
+  const int64_t begin = slot_begin + (int64_t)blockIdx.x * chunk;
+  const int64_t end = min(slot_end, begin + chunk);
   if (lds) {
     for (int g = threadIdx.x; g < groups; g += blockDim.x) hist[g] = 0;
     __syncthreads();
@@ -154,10 +159,10 @@ void carve_buckets(Carve& c, Buckets& b, int64_t slots, int64_t groups, int tile
   b.groups = groups;
   b.tile = tile;
   b.max_tiles = (slots + tile - 1) / tile + groups;
-  b.counts = c.take<int32_t>(groups);
-  b.cursors = c.take<int32_t>(groups);
+  b.counts = c.take<int32_t>(2 * groups + 1);  // counts, cursors, tile count: one fill
+  b.cursors = b.counts ? b.counts + groups : nullptr;
+  b.num_tiles = b.counts ? b.counts + 2 * groups : nullptr;
   b.tile_off = c.take<int32_t>(groups);
-  b.num_tiles = c.take<int32_t>(1);
   b.tile_group = c.take<int32_t>(b.max_tiles);
   b.tile_req = c.take<int32_t>(b.max_tiles * tile);
 }
@@ -174,33 +179,44 @@ void fill_f32(float* p, int64_t n, float v, hipStream_t stream) {
   PISA_TIMED("fill", stream, hipLaunchKernelGGL(fill_f32_kernel, dim3(blocks), dim3(256), 0, stream, p, n, v));
 }
 
+// Bucket the requests among slots [slot_begin, slot_end); tiles keep absolute slots.
 template <typename Src>
-static int run_buckets(const Src& src, int64_t slots, Buckets& b, hipStream_t stream) {
-  if (slots >= (int64_t)INT32_MAX || b.groups >= (int64_t)INT32_MAX)
-    return fail(PISA_ERR_UNSUPPORTED, "too many requests to bucket (%lld slots)", (long long)slots);
-  fill_i32(b.counts, b.groups, 0, stream);
-  fill_i32(b.cursors, b.groups, 0, stream);
-  fill_i32(b.num_tiles, 1, 0, stream);
-  if (slots == 0) return check_launch("bucket fill");
-  const int64_t grid = (slots + kBucketChunk - 1) / kBucketChunk;
-  const size_t lds = b.groups <= kLdsGroups ? (size_t)b.groups * sizeof(int) : 0;
+static int run_buckets(const Src& src, int64_t slot_begin, int64_t slot_end, Buckets& b,
+                       hipStream_t stream) {
+  if (slot_end >= (int64_t)INT32_MAX || b.groups >= (int64_t)INT32_MAX)
+    return fail(PISA_ERR_UNSUPPORTED, "too many requests to bucket (%lld slots)", (long long)slot_end);
+  if (slot_end - slot_begin > (b.max_tiles - b.groups) * b.tile)
+    return fail(PISA_ERR_INVALID, "bucket range of %lld slots exceeds its workspace",
+                (long long)(slot_end - slot_begin));
+  fill_i32(b.counts, 2 * b.groups + 1, 0, stream);  // counts, cursors, tile count
+  if (slot_end <= slot_begin) return check_launch("bucket fill");
+  // LDS histograms (one global atomic per workgroup and non-empty bin) when the
+  // range fills the device with kBucketChunk-slot workgroups; otherwise direct
+  // global atomics on kSmallChunk-slot workgroups.
+  const int64_t range = slot_end - slot_begin;
+  const bool use_lds = b.groups <= kLdsGroups && range >= kLdsMinSlots;
+  const int64_t chunk = use_lds ? kBucketChunk : kSmallChunk;
+  const int64_t grid = (range + chunk - 1) / chunk;
+  const size_t lds = use_lds ? (size_t)b.groups * sizeof(int) : 0;
   PISA_TIMED("bucket_count", stream, hipLaunchKernelGGL((bucket_count_kernel<Src>), dim3(grid), dim3(kBucketThreads), lds, stream,
-                     src, slots, (int)b.groups, b.counts));
+                     src, slot_begin, slot_end, chunk, (int)b.groups, use_lds ? 1 : 0, b.counts));
   PISA_TIMED("bucket_scan", stream, hipLaunchKernelGGL(bucket_scan_kernel, dim3(1), dim3(1024), 0, stream, b.counts, b.groups,
                      b.tile, b.tile_off, b.num_tiles));
   PISA_TIMED("bucket_scatter", stream, hipLaunchKernelGGL((bucket_scatter_kernel<Src>), dim3(grid), dim3(kBucketThreads), lds, stream,
-                     src, slots, (int)b.groups, b.tile_off, b.cursors, b.tile, b.tile_group,
-                     b.tile_req));
+                     src, slot_begin, slot_end, chunk, (int)b.groups, use_lds ? 1 : 0, b.tile_off, b.cursors,
+                     b.tile, b.tile_group, b.tile_req));
   return check_launch("bucket");
 }
 
-int bucket_leaf(const LeafRequests& src, int64_t slots, Buckets& b, hipStream_t stream) {
-  return run_buckets(LeafSrc{src}, slots, b, stream);
+int bucket_leaf(const LeafRequests& src, int64_t slot_begin, int64_t slot_end, Buckets& b,
+                hipStream_t stream) {
+  return run_buckets(LeafSrc{src}, slot_begin, slot_end, b, stream);
 }
 
-int bucket_attn(const AttnRequests& src, int64_t slots, Buckets& b, hipStream_t stream) {
-  if (src.index_bits == 64) return run_buckets(AttnSrc<int64_t>{src}, slots, b, stream);
-  return run_buckets(AttnSrc<int32_t>{src}, slots, b, stream);
+int bucket_attn(const AttnRequests& src, int64_t slot_begin, int64_t slot_end, Buckets& b,
+                hipStream_t stream) {
+  if (src.index_bits == 64) return run_buckets(AttnSrc<int64_t>{src}, slot_begin, slot_end, b, stream);
+  return run_buckets(AttnSrc<int32_t>{src}, slot_begin, slot_end, b, stream);
 }
 
 }  // namespace pisa

@@ -81,8 +81,18 @@ struct AttnRequests {
   int32_t topk, heads, tokens, blocks, block_size, causal;
 };
 
-int bucket_leaf(const LeafRequests& src, int64_t slots, Buckets& b, hipStream_t stream);
-int bucket_attn(const AttnRequests& src, int64_t slots, Buckets& b, hipStream_t stream);
+// Bucket the requests among slots [slot_begin, slot_end) (tiles keep absolute
+// slot numbers, groups stay (batch, kv head, block)).
+int bucket_leaf(const LeafRequests& src, int64_t slot_begin, int64_t slot_end, Buckets& b,
+                hipStream_t stream);
+int bucket_attn(const AttnRequests& src, int64_t slot_begin, int64_t slot_end, Buckets& b,
+                hipStream_t stream);
+
+// Query tokens per bucketing window: the q rows of one kv head over a window
+// (row_bytes per token) stay within 8 MiB, so the tiles of a window re-read
+// them from the L2 and the 256 MB MALL instead of HBM.  Windows run over the
+// flattened (batch, token) axis.
+int query_window(int64_t tokens, int64_t row_bytes);
 
 int dtype_size(int dtype);
 // Compute units of the current device (cached per device).
@@ -195,8 +205,9 @@ int launch_final(const FinalArgs& a, hipStream_t stream);
 int launch_scoreable(const MaskArgs& a, hipStream_t stream);
 int launch_leaf(int dtype, const LeafArgs& a, hipStream_t stream);
 int attn_check(const AttnArgs& a, int dtype, bool backward);
-int launch_attn_fwd(int dtype, const AttnArgs& a, bool grouped, int64_t slots, int64_t items,
-                    hipStream_t stream);
+// Forward partials (grouped tiles or one workgroup per slot), then the combine.
+int launch_attn_partials(int dtype, const AttnArgs& a, bool grouped, int64_t slots, hipStream_t stream);
+int launch_attn_combine(int dtype, const AttnArgs& a, int64_t items, hipStream_t stream);
 int launch_attn_bwd(int dtype, const AttnArgs& a, int64_t groups, int64_t items, hipStream_t stream);
 void fill_f32(float* p, int64_t n, float v, hipStream_t stream);
 

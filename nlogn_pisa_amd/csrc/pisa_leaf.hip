@@ -14,6 +14,8 @@
 #include "pisa_device.h"
 #include "pisa_internal.h"
 
+#include <type_traits>
+
 namespace pisa {
 
 
@@ -161,8 +163,10 @@ __global__ void __launch_bounds__(256) leaf_kernel(LeafArgs a) {
 // The path for D in {16, 32, 64, 128}: S^T = K Q^T as in the sparse attention
 // forward (QkShape), so lane (grp, col) holds the scores of row `col` against
 // keys 16 mt + 4 grp + i and loads one contiguous quarter of its query row.
-// Per-request bookkeeping is computed once per tile into LDS and each wave loads
-// the next unit's query rows while it scores the current one.  A work item of a
+// The key block is staged in LDS once per tile and each wave copies its MFMA A
+// fragments into registers once per tile; per-request bookkeeping is computed
+// once per tile into LDS and each wave loads the next unit's query rows while it
+// scores the current one.  A work item of a
 // wave is one 16-row unit (Gp <= 16: 16 / Gp requests) or one request of Gp / 16
 // units (Gp > 16).
 
@@ -189,12 +193,29 @@ __host__ __device__ inline LeafLds leaf_lds(int C, int tile) {
   return L;
 }
 
+// Tuning constants of the leaf tile kernel: query-row prefetch depth (units),
+// key fragments in registers (blocks of up to 64 keys), and the minimum waves
+// per SIMD requested from the compiler at up to 64 keys.
+#ifndef PISA_LEAF_DEPTH
+#define PISA_LEAF_DEPTH 2
+#endif
+#ifndef PISA_LEAF_KREG
+#define PISA_LEAF_KREG 0
+#endif
+#ifndef PISA_LEAF_WAVES
+#define PISA_LEAF_WAVES 3
+#endif
+
 template <typename T, int HD, int NTM>
-__global__ void __launch_bounds__(256, 2) leaf_tile_kernel(LeafArgs a) {
+__global__ void __launch_bounds__(256, (NTM <= 4 ? PISA_LEAF_WAVES : 2)) leaf_tile_kernel(LeafArgs a) {
   typedef QkShape<T, HD, NTM> S;
   typedef typename S::Op Op;
   typedef typename S::frag frag;
   constexpr int QL = S::QL, DS = S::DS;
+  constexpr int DEPTH = PISA_LEAF_DEPTH;
+  // key-block A fragments held in registers when they take at most 64 VGPRs
+  constexpr bool KREG = PISA_LEAF_KREG && NTM <= 4 && NTM * QL * sizeof(T) <= 256;
+  constexpr int KR = KREG ? NTM : 1;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const LeafLds L = leaf_lds<T, HD>(a.C, a.tile);
   T* ks = reinterpret_cast<T*>(smem + L.k_off);
@@ -204,9 +225,13 @@ __global__ void __launch_bounds__(256, 2) leaf_tile_kernel(LeafArgs a) {
   const int nwaves = (int)(blockDim.x >> 6);
   const int col = lane & 15, grp = lane >> 4;
   const int NT = L.Cq / 16;
-  const int Gp = a.Gp;
-  const int nsub = Gp <= 16 ? 1 : Gp / 16;  // units per item
-  const int rpu = Gp <= 16 ? 16 / Gp : 1;   // requests per item
+  const int Gp = a.Gp;                       // a power of two
+  const int gl = 31 - __clz(Gp);             // log2 Gp
+  const int nsl = gl > 4 ? gl - 4 : 0;       // log2 units per item
+  const int rpl = gl < 4 ? 4 - gl : 0;       // log2 requests per item
+  const int nsub = 1 << nsl;                 // units per item
+  const int rpu = 1 << rpl;                  // requests per item
+  const float half_scale2 = (float)(0.5 * (double)a.scale * (double)a.scale);
   const bool lse = a.method == PISA_METHOD_LSE;
   const bool pisa1 = a.method == PISA_METHOD_PISA1;
   const T* q = static_cast<const T*>(a.q);
@@ -243,97 +268,124 @@ __global__ void __launch_bounds__(256, 2) leaf_tile_kernel(LeafArgs a) {
     }
     __syncthreads();
 
-    const int items = (nreq + rpu - 1) / rpu;
-    auto fetch = [&](int r, int j, frag (&f)[DS]) {
-      const int rho = (r * nsub + j) * 16 + col;
-      const int rq = rho / Gp, gh = rho % Gp;
-      if (r < items && rq < nreq && gh < a.G)
-        load_frags(q + mq[rq] + (int64_t)gh * HD + QL * grp, f);
-      else
-        zero_frags(f);
-    };
-    frag qf[DS];
-    fetch(wave, 0, qf);
-    for (int r = wave; r < items; r += nwaves) {
-      float total = 0.f;  // this lane's row: head scores summed over the item's units
-      for (int j = 0; j < nsub; ++j) {
-        frag qn[DS];
-        if (j + 1 < nsub) fetch(r, j + 1, qn);
-        else fetch(r + nwaves, 0, qn);
-        f4 s[NTM];
+    // this wave's A fragments of the whole key block, read from LDS once per tile
+    frag kreg[KR][DS];
 #pragma unroll
-        for (int mt = 0; mt < NTM; ++mt) {
-          s[mt] = f4{0.f, 0.f, 0.f, 0.f};
-          if (mt < NT) {
+    for (int mt = 0; mt < KR; ++mt) {
+      if (KREG && mt < NT) load_frags(ks + (mt * 16 + col) * L.ldk + QL * grp, kreg[mt]);
+      else zero_frags(kreg[mt]);
+    }
+
+    const int items = (nreq + rpu - 1) >> rpl;
+    // Query rows of unit j of item r.  The load is issued by every lane: rows
+    // that do not exist (padding heads or requests, units past the end) read
+    // request 0's first head instead and their scores are never used, so no
+    // load sits behind a branch and the compiler can keep later loads in flight.
+    auto fetch = [&](int r, int j, frag (&f)[DS]) {
+      const int rho = (((r << nsl) + j) << 4) + col;
+      const int rq = rho >> gl, gh = rho & (Gp - 1);
+      const bool ok = r < items && rq < nreq && gh < a.G;
+      load_frags(q + mq[ok ? rq : 0] + (int64_t)(ok ? gh : 0) * HD + QL * grp, f);
+    };
+    // this wave's units k = 0, 1, ...: item wave + nwaves (k >> nsl), unit k & (nsub - 1);
+    // query rows of the next DEPTH units are in flight while unit k is scored
+    const int my_items = wave < items ? (items - 1 - wave) / nwaves + 1 : 0;
+    const int nunits = my_items << nsl;
+    auto fetch_k = [&](int k, frag (&f)[DS]) {
+      fetch(k < nunits ? wave + nwaves * (k >> nsl) : items, k & (nsub - 1), f);
+    };
+    const int lim = rows_valid - 4 * grp;  // this lane's keys 16 mt + i are valid below lim
+    float total = 0.f;  // this lane's row: head scores summed over the item's units
+    // unit k: scored from `cur`, loads unit k + DEPTH into `into` (the buffer
+    // unit k - 1 used); buffers rotate by unrolling, never by copies, so the
+    // loads in flight are not waited for early.  FULL: every key of the block
+    // is valid (no masks).
+    auto unit = [&](auto full_tag, int k, frag (&cur)[DS], frag (&into)[DS]) {
+      constexpr bool FULL = decltype(full_tag)::value;
+      fetch_k(k + DEPTH, into);
+      const int r = wave + nwaves * (k >> nsl), j = k & (nsub - 1);
+      f4 s[NTM];
+#pragma unroll
+      for (int mt = 0; mt < NTM; ++mt) {
+        s[mt] = f4{0.f, 0.f, 0.f, 0.f};
+        if (mt < NT) {
+          if constexpr (KREG) {
+#pragma unroll
+            for (int d = 0; d < DS; ++d) s[mt] = Op::mma(kreg[mt][d], cur[d], s[mt]);
+          } else {
             frag kf[DS];
             load_frags(ks + (mt * 16 + col) * L.ldk + QL * grp, kf);
 #pragma unroll
-            for (int d = 0; d < DS; ++d) s[mt] = Op::mma(kf[d], qf[d], s[mt]);
+            for (int d = 0; d < DS; ++d) s[mt] = Op::mma(kf[d], cur[d], s[mt]);
           }
         }
-        float head;
-        if (lse) {
-          float m = -INFINITY;
-#pragma unroll
-          for (int mt = 0; mt < NTM; ++mt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              if (mt < NT && mt * 16 + 4 * grp + i < rows_valid) m = fmaxf(m, s[mt][i] * a.scale);
-          m = fmaxf(m, __shfl_xor(m, 16));
-          m = fmaxf(m, __shfl_xor(m, 32));
-          float e = 0.f;
-#pragma unroll
-          for (int mt = 0; mt < NTM; ++mt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              if (mt < NT && mt * 16 + 4 * grp + i < rows_valid) e += __expf(s[mt][i] * a.scale - m);
-          e += __shfl_xor(e, 16);
-          e += __shfl_xor(e, 32);
-          head = m + __logf(e);
-        } else {
-          float s1 = 0.f, s2 = 0.f;
-#pragma unroll
-          for (int mt = 0; mt < NTM; ++mt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              if (mt < NT && mt * 16 + 4 * grp + i < rows_valid) {
-                s1 += s[mt][i];
-                s2 = fmaf(s[mt][i], s[mt][i], s2);
-              }
-          s1 += __shfl_xor(s1, 16);
-          s1 += __shfl_xor(s1, 32);
-          s2 += __shfl_xor(s2, 16);
-          s2 += __shfl_xor(s2, 32);
-          if (pisa1) {
-            head = s1;  // one support row: the leaf mean, scale 1
-          } else {
-            const float cnt = (float)rows_valid;
-            const float mean = s1 / cnt;
-            const float var = fmaxf(s2 / cnt - mean * mean, 0.f);
-            head = a.scale * mean + (float)(0.5 * (double)a.scale * (double)a.scale) * var;
-          }
-        }
-        const int rho = (r * nsub + j) * 16 + col;
-        const bool real = rho / Gp < nreq && rho % Gp < a.G;
-        total += real ? head : 0.f;
-#pragma unroll
-        for (int d = 0; d < DS; ++d) qf[d] = qn[d];
       }
-      // sum the head rows of each request (consecutive lanes of a 16-lane row)
+      auto valid = [&](int mt, int i) { return mt < NT && (FULL || mt * 16 + i < lim); };
+      float head;
+      if (lse) {
+        float m = -INFINITY;
+#pragma unroll
+        for (int mt = 0; mt < NTM; ++mt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (valid(mt, i)) m = fmaxf(m, s[mt][i] * a.scale);
+        m = xor32_max(xor16_max(m));
+        float e = 0.f;
+#pragma unroll
+        for (int mt = 0; mt < NTM; ++mt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (valid(mt, i)) e += __expf(s[mt][i] * a.scale - m);
+        e = xor32_sum(xor16_sum(e));
+        head = m + __logf(e);
+      } else {
+        float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+        for (int mt = 0; mt < NTM; ++mt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (valid(mt, i)) {
+              s1 += s[mt][i];
+              s2 = fmaf(s[mt][i], s[mt][i], s2);
+            }
+        s1 = xor32_sum(xor16_sum(s1));
+        s2 = xor32_sum(xor16_sum(s2));
+        if (pisa1) {
+          head = s1;  // one support row: the leaf mean, scale 1
+        } else {
+          const float cnt = (float)rows_valid;
+          const float mean = s1 / cnt;
+          const float var = fmaxf(s2 / cnt - mean * mean, 0.f);
+          head = a.scale * mean + half_scale2 * var;
+        }
+      }
+      const int rho = (((r << nsl) + j) << 4) + col;
+      const bool real = (rho >> gl) < nreq && (rho & (Gp - 1)) < a.G;
+      total += real ? head : 0.f;
+      if (j + 1 < nsub) return;
+      // item done: sum the head rows of each request (aligned lanes of a 16-lane row)
       if (Gp >= 16) {
-        float v = total;
-        v += __shfl_xor(v, 1);
-        v += __shfl_xor(v, 2);
-        v += __shfl_xor(v, 4);
-        v += __shfl_xor(v, 8);
+        const float v = group_sum(total, 16);
         if (lane == 0 && r < nreq) a.scores[mslot[r]] = v;
       } else {
-        float v = total;
-        for (int off = 1; off < Gp; off <<= 1) v += __shfl_xor(v, off);
-        const int rq = (r * 16 + col) / Gp;
-        if (grp == 0 && col % Gp == 0 && rq < nreq) a.scores[mslot[rq]] = v;
+        const float v = group_sum(total, Gp);
+        const int rq = ((r << 4) + col) >> gl;
+        if (grp == 0 && (col & (Gp - 1)) == 0 && rq < nreq) a.scores[mslot[rq]] = v;
       }
-    }
+      total = 0.f;
+    };
+    auto run = [&](auto full_tag) {
+      frag qb[DEPTH + 1][DS];
+#pragma unroll
+      for (int p = 0; p < DEPTH; ++p) fetch_k(p, qb[p]);
+      for (int k0 = 0; k0 < nunits; k0 += DEPTH + 1) {
+#pragma unroll
+        for (int p = 0; p <= DEPTH; ++p)
+          if (k0 + p < nunits) unit(full_tag, k0 + p, qb[p], qb[(p + DEPTH) % (DEPTH + 1)]);
+      }
+    };
+    if (rows_valid == NT * 16) run(std::true_type{});
+    else run(std::false_type{});
   }
 }
 

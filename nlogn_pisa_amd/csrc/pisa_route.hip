@@ -436,20 +436,20 @@ __global__ void __launch_bounds__(64) route_grouped_kernel(RouteArgs a) {
     const int64_t rstride = (int64_t)a.Hkv * HD;
     const int len = a.lengths[src_level];
     const int ntile = (nlist + cpt - 1) / cpt;
+    // Support rows of tile mt.  Every lane issues its load: rows that do not
+    // exist (past the list, or past the level's tail) read row 0 of the level
+    // instead and are masked out of the support scores, so no load sits behind
+    // a branch and the compiler keeps the next tile's loads in flight.
     auto fetch = [&](int mt, frag (&f)[DS]) {
-      const int ci = mt * cpt + col / R, child = col % R;
-      int64_t row = -1;
-      if (mt < ntile && ci < nlist) {
-        const int64_t r = (int64_t)ids_s[list_s[ci]] * R + child;
-        if (r < len) row = r;
-      }
-      if (row >= 0) load_frags(base + row * rstride + QL * grp, f);
-      else zero_frags(f);
+      const int ci = mt * cpt + col / R, child = col % R;  // ci < nlist implies mt < ntile
+      const int id = ci < nlist ? ids_s[list_s[ci]] : 0;
+      const int64_t r = (int64_t)id * R + child;
+      const bool ok = ci < nlist && r < len;
+      load_frags(base + (ok ? r : 0) * rstride + QL * grp, f);
     };
-    frag xf[DS];
-    fetch(0, xf);
-    for (int mt = 0; mt < ntile; ++mt) {
-      frag xn[DS];
+    // tile mt: scored from `xf`, loads tile mt + 1 into `xn`; the two buffers
+    // alternate by unrolling, never by copies
+    auto tile = [&](int mt, frag (&xf)[DS], frag (&xn)[DS]) {
       fetch(mt + 1, xn);
       f4 sv = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -460,8 +460,12 @@ __global__ void __launch_bounds__(64) route_grouped_kernel(RouteArgs a) {
         case 4: tile_scores<4>(sv, mt, a, ids_s, list_s, sc_s, nlist, len, own, lse, binary, col, grp); break;
         default: tile_scores<8>(sv, mt, a, ids_s, list_s, sc_s, nlist, len, own, lse, binary, col, grp); break;
       }
-#pragma unroll
-      for (int d = 0; d < DS; ++d) xf[d] = xn[d];
+    };
+    frag xb[2][DS];
+    fetch(0, xb[0]);
+    for (int mt = 0; mt < ntile; mt += 2) {
+      tile(mt, xb[0], xb[1]);
+      if (mt + 1 < ntile) tile(mt + 1, xb[1], xb[0]);
     }
     __syncthreads();
 

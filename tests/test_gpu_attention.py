@@ -63,6 +63,8 @@ CASES = [
     ("fp32-d16", 1, 128, 256, 4, 1, 16, 16, 6, "fp32", True, None),
     ("fp16-d16-c48", 2, 200, 200, 4, 2, 16, 48, 3, "fp16", True, None),
     ("bf16-c128", 1, 512, 640, 8, 2, 128, 128, 3, "bf16", True, None),
+    # 2048-token windows over the flattened (batch, token) axis: two, the first across batches
+    ("bf16-windows", 2, 1500, 1500, 16, 1, 128, 64, 6, "bf16", True, None),
 ]
 
 
