@@ -41,6 +41,8 @@ def parse():
     ap.add_argument("--tokens", type=int, default=None, help="config 4 length")
     ap.add_argument("--cpu-sample", type=int, default=384, help="oracle tokens timed on the CPU")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--backward", action="store_true",
+                    help="also time sparse attention forward + backward (a training step's attention)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 1 GiB device copy (calibrates rocprofv3 FETCH/WRITE_SIZE)")
     return ap.parse_args()
@@ -250,6 +252,33 @@ def main():
         att_ms = sum(m[1].elapsed_time(m[2]) for m in marks) / args.steps
         step_ms = sel_ms + att_ms
 
+        train_ms = None
+        if args.backward:
+            print("[bench] attention forward + backward", file=sys.stderr, flush=True)
+            ids = select()
+            gen = torch.Generator(device="cpu").manual_seed(7)
+            dout = torch.randn(q.shape[:3] + (v.shape[-1],), generator=gen).to(dev, q.dtype)
+            leaves = [x.detach().requires_grad_(True) for x in (q, k, v)]
+
+            def train():
+                with torch.enable_grad():
+                    out = P.sparse_attention(*leaves, ids, block_size=w.block_size)
+                    out.backward(dout)
+                for x in leaves:
+                    x.grad = None
+
+            for _ in range(args.warmup):
+                train()
+            torch.cuda.synchronize()
+            t0 = torch.cuda.Event(enable_timing=True)
+            t1 = torch.cuda.Event(enable_timing=True)
+            t0.record(stream)
+            for _ in range(args.steps):
+                train()
+            t1.record(stream)
+            torch.cuda.synchronize()
+            train_ms = t0.elapsed_time(t1) / args.steps
+
         print("[bench] kernel timing", file=sys.stderr, flush=True)
         _lib.profile_begin()
         for _ in range(2):
@@ -349,6 +378,10 @@ def main():
         "roofline": roofline,
         "wall_s_timed": round(wall, 3),
     }
+    if train_ms is not None:
+        # forward 4 D G P flops, backward 10 D G P (S recomputed)
+        result["attn_fwd_bwd_ms"] = round(train_ms, 3)
+        result["attn_fwd_bwd_tflops"] = round(14 * D * G * pairs / (train_ms * 1e-3) / 1e12, 2)
     del sel_kernels
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)

@@ -5,14 +5,20 @@
 // visible selected block of sparse attention.  Requests are bucketed by
 // group = (batch * Hkv + head) * blocks + block and cut into tiles of at most
 // `tile` requests of one group, so a consumer loads each key block once per
-// tile.  Three launches per range of slots, no host read of a count (the tile
-// array is sized for the worst case, ceil(slots / tile) + groups, as the
-// reference does):
-//   count   - per-workgroup LDS histogram, one global atomic per non-empty bin
-//             (ranges too small to fill the device: direct global atomics);
+// tile.  No host read of a count: the tile array is sized for the worst case,
+// ceil(slots / tile) + groups, as the reference does.
+//
+// Counting sort over a range of slots (groups that fit LDS bins): W workgroups
+// each take one contiguous chunk of the range and
+//   hist    - write the LDS histogram of their chunk as row w of a [W, groups]
+//             matrix (no global atomics);
+//   offsets - one thread per group turns its column into exclusive offsets
+//             (requests of that group in earlier chunks) and the group total;
 //   scan    - tiles per group, exclusive prefix sum, total tile count;
-//   scatter - LDS ranks plus one reserved global range per bin and workgroup.
-// Request order inside a group is unspecified; every consumer computes each
+//   scatter - each workgroup ranks its requests from its row of offsets plus
+//             LDS atomics, and writes them into their tiles.
+// Groups beyond the LDS bins use global atomics on counts and cursors instead.
+// Request order inside a chunk is unspecified; every consumer computes each
 // request independently of its tile-mates.
 
 #include "pisa_device.h"
@@ -23,10 +29,10 @@
 namespace pisa {
 
 constexpr int kLdsGroups = 16384;  // 64 KB of int32 bins
+constexpr int kMaxBucketGroups = 1024;  // counting-sort workgroups (histogram rows) per range
 constexpr int kBucketThreads = 256;
-constexpr int64_t kBucketChunk = 32768;          // slots per workgroup with LDS bins
-constexpr int64_t kSmallChunk = 4096;            // slots per workgroup with global atomics
-constexpr int64_t kLdsMinSlots = kBucketChunk * 256;  // LDS bins from 256 workgroups up
+constexpr int64_t kSmallChunk = 4096;    // slots per workgroup with global atomics
+constexpr int64_t kMinChunk = 2048;      // fewest slots per counting-sort workgroup
 
 struct LeafSrc {
   LeafRequests r;
@@ -58,6 +64,87 @@ struct AttnSrc {
   }
 };
 
+// Row w of hist: the number of requests of each group among slots
+// [begin + w chunk, begin + (w + 1) chunk).
+template <typename Src>
+__global__ void __launch_bounds__(kBucketThreads) bucket_hist_kernel(Src src, int64_t slot_begin,
+                                                                     int64_t slot_end, int64_t chunk,
+                                                                     int groups, int32_t* hist) {
+  extern __shared__ int bins[];
+  const int64_t begin = slot_begin + (int64_t)blockIdx.x * chunk;
+  const int64_t end = min(slot_end, begin + chunk);
+  for (int g = threadIdx.x; g < groups; g += blockDim.x) bins[g] = 0;
+  __syncthreads();
+  // four independent slots per thread and step, so their loads overlap
+  for (int64_t s0 = begin + threadIdx.x; s0 < end; s0 += 4 * (int64_t)blockDim.x) {
+    int g[4];
+    bool ok[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t s = s0 + (int64_t)u * blockDim.x;
+      ok[u] = s < end && src.get(s, g[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (ok[u]) atomicAdd(&bins[g[u]], 1);
+  }
+  __syncthreads();
+  int32_t* row = hist + (int64_t)blockIdx.x * groups;
+  for (int g = threadIdx.x; g < groups; g += blockDim.x) row[g] = bins[g];
+}
+
+// Column g of hist becomes exclusive offsets; counts[g] = the group's total.
+__global__ void __launch_bounds__(256) bucket_offsets_kernel(int32_t* hist, int rows, int groups,
+                                                             int32_t* counts) {
+  const int g = blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= groups) return;
+  constexpr int B = 16;  // rows loaded before their offsets are stored
+  int32_t run = 0;
+  for (int w0 = 0; w0 < rows; w0 += B) {
+    int32_t v[B];
+#pragma unroll
+    for (int u = 0; u < B; ++u) v[u] = w0 + u < rows ? hist[(int64_t)(w0 + u) * groups + g] : 0;
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      if (w0 + u < rows) hist[(int64_t)(w0 + u) * groups + g] = run;
+      run += v[u];
+    }
+  }
+  counts[g] = run;
+}
+
+// Place the requests of chunk w: rank = offset of its group in row w + LDS rank.
+template <typename Src>
+__global__ void __launch_bounds__(kBucketThreads) bucket_place_kernel(
+    Src src, int64_t slot_begin, int64_t slot_end, int64_t chunk, int groups,
+    const int32_t* __restrict__ hist, const int32_t* __restrict__ tile_off, int tile,
+    int32_t* __restrict__ tile_group, int32_t* __restrict__ tile_req) {
+  extern __shared__ int bins[];
+  const int64_t begin = slot_begin + (int64_t)blockIdx.x * chunk;
+  const int64_t end = min(slot_end, begin + chunk);
+  const int32_t* row = hist + (int64_t)blockIdx.x * groups;
+  for (int g = threadIdx.x; g < groups; g += blockDim.x) bins[g] = row[g];
+  __syncthreads();
+  for (int64_t s0 = begin + threadIdx.x; s0 < end; s0 += 4 * (int64_t)blockDim.x) {
+    int g[4];
+    bool ok[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t s = s0 + (int64_t)u * blockDim.x;
+      ok[u] = s < end && src.get(s, g[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (!ok[u]) continue;
+      const int rank = atomicAdd(&bins[g[u]], 1);
+      const int t = tile_off[g[u]] + rank / tile;
+      const int within = rank % tile;
+      tile_req[(int64_t)t * tile + within] = (int32_t)(s0 + (int64_t)u * blockDim.x);
+      if (within == 0) tile_group[t] = g[u];
+    }
+  }
+}
+
 __global__ void fill_f32_kernel(float* p, int64_t n, float v) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x)
@@ -70,29 +157,16 @@ __global__ void fill_i32_kernel(int32_t* p, int64_t n, int32_t v) {
     p[i] = v;
 }
 
+// Global-atomic counting (groups beyond the LDS bins).
 template <typename Src>
 __global__ void __launch_bounds__(kBucketThreads) bucket_count_kernel(Src src, int64_t slot_begin,
                                                                       int64_t slot_end, int64_t chunk,
-                                                                      int groups, int lds,
                                                                       int32_t* counts) {
-  extern __shared__ int hist[];
   const int64_t begin = slot_begin + (int64_t)blockIdx.x * chunk;
   const int64_t end = min(slot_end, begin + chunk);
-  if (lds) {
-    for (int g = threadIdx.x; g < groups; g += blockDim.x) hist[g] = 0;
-    __syncthreads();
-  }
   for (int64_t s = begin + threadIdx.x; s < end; s += blockDim.x) {
     int g;
-    if (src.get(s, g)) {
-      if (lds) atomicAdd(&hist[g], 1);
-      else atomicAdd(&counts[g], 1);
-    }
-  }
-  if (lds) {
-    __syncthreads();
-    for (int g = threadIdx.x; g < groups; g += blockDim.x)
-      if (hist[g]) atomicAdd(&counts[g], hist[g]);
+    if (src.get(s, g)) atomicAdd(&counts[g], 1);
   }
 }
 
@@ -124,30 +198,15 @@ __global__ void __launch_bounds__(1024) bucket_scan_kernel(const int32_t* counts
 
 template <typename Src>
 __global__ void __launch_bounds__(kBucketThreads) bucket_scatter_kernel(
-    Src src, int64_t slot_begin, int64_t slot_end, int64_t chunk, int groups, int lds,
+    Src src, int64_t slot_begin, int64_t slot_end, int64_t chunk,
     const int32_t* __restrict__ tile_off, int32_t* cursors, int tile,
     int32_t* __restrict__ tile_group, int32_t* __restrict__ tile_req) {
-  extern __shared__ int hist[];
   const int64_t begin = slot_begin + (int64_t)blockIdx.x * chunk;
   const int64_t end = min(slot_end, begin + chunk);
-  if (lds) {
-    for (int g = threadIdx.x; g < groups; g += blockDim.x) hist[g] = 0;
-    __syncthreads();
-    for (int64_t s = begin + threadIdx.x; s < end; s += blockDim.x) {
-      int g;
-      if (src.get(s, g)) atomicAdd(&hist[g], 1);
-    }
-    __syncthreads();
-    for (int g = threadIdx.x; g < groups; g += blockDim.x) {
-      const int c = hist[g];
-      if (c) hist[g] = atomicAdd(&cursors[g], c);
-    }
-    __syncthreads();
-  }
   for (int64_t s = begin + threadIdx.x; s < end; s += blockDim.x) {
     int g;
     if (!src.get(s, g)) continue;
-    const int rank = lds ? atomicAdd(&hist[g], 1) : atomicAdd(&cursors[g], 1);
+    const int rank = atomicAdd(&cursors[g], 1);
     const int t = tile_off[g] + rank / tile;
     const int within = rank % tile;
     tile_req[(int64_t)t * tile + within] = (int32_t)s;
@@ -165,6 +224,7 @@ void carve_buckets(Carve& c, Buckets& b, int64_t slots, int64_t groups, int tile
   b.tile_off = c.take<int32_t>(groups);
   b.tile_group = c.take<int32_t>(b.max_tiles);
   b.tile_req = c.take<int32_t>(b.max_tiles * tile);
+  b.hist = groups <= kLdsGroups ? c.take<int32_t>(kMaxBucketGroups * groups) : nullptr;
 }
 
 static void fill_i32(int32_t* p, int64_t n, int32_t v, hipStream_t stream) {
@@ -188,23 +248,40 @@ static int run_buckets(const Src& src, int64_t slot_begin, int64_t slot_end, Buc
   if (slot_end - slot_begin > (b.max_tiles - b.groups) * b.tile)
     return fail(PISA_ERR_INVALID, "bucket range of %lld slots exceeds its workspace",
                 (long long)(slot_end - slot_begin));
-  fill_i32(b.counts, 2 * b.groups + 1, 0, stream);  // counts, cursors, tile count
-  if (slot_end <= slot_begin) return check_launch("bucket fill");
-  // LDS histograms (one global atomic per workgroup and non-empty bin) when the
-  // range fills the device with kBucketChunk-slot workgroups; otherwise direct
-  // global atomics on kSmallChunk-slot workgroups.
   const int64_t range = slot_end - slot_begin;
-  const bool use_lds = b.groups <= kLdsGroups && range >= kLdsMinSlots;
-  const int64_t chunk = use_lds ? kBucketChunk : kSmallChunk;
+  if (range <= 0) {
+    fill_i32(b.counts, 2 * b.groups + 1, 0, stream);  // counts, cursors, tile count
+    return check_launch("bucket fill");
+  }
+  if (b.hist) {
+    // counting sort: rows = chunks of at least kMinChunk slots, at most kMaxBucketGroups
+    const int64_t rows = std::max<int64_t>(1, std::min<int64_t>(kMaxBucketGroups, range / kMinChunk));
+    const int64_t chunk = (range + rows - 1) / rows;
+    const size_t lds = (size_t)b.groups * sizeof(int);
+    allow_lds((const void*)bucket_hist_kernel<Src>, lds);
+    allow_lds((const void*)bucket_place_kernel<Src>, lds);
+    PISA_TIMED("bucket_count", stream, hipLaunchKernelGGL((bucket_hist_kernel<Src>), dim3(rows), dim3(kBucketThreads), lds, stream,
+                       src, slot_begin, slot_end, chunk, (int)b.groups, b.hist));
+    PISA_TIMED("bucket_count", stream, hipLaunchKernelGGL(bucket_offsets_kernel, dim3((b.groups + 255) / 256), dim3(256), 0, stream,
+                       b.hist, (int)rows, (int)b.groups, b.counts));
+    PISA_TIMED("bucket_scan", stream, hipLaunchKernelGGL(bucket_scan_kernel, dim3(1), dim3(1024), 0, stream, b.counts, b.groups,
+                       b.tile, b.tile_off, b.num_tiles));
+    PISA_TIMED("bucket_scatter", stream, hipLaunchKernelGGL((bucket_place_kernel<Src>), dim3(rows), dim3(kBucketThreads), lds, stream,
+                       src, slot_begin, slot_end, chunk, (int)b.groups, b.hist, b.tile_off, b.tile,
+                       b.tile_group, b.tile_req));
+    return check_launch("bucket");
+  }
+  // global atomics on counts and cursors
+  fill_i32(b.counts, 2 * b.groups + 1, 0, stream);  // counts, cursors, tile count
+  const int64_t chunk = kSmallChunk;
   const int64_t grid = (range + chunk - 1) / chunk;
-  const size_t lds = use_lds ? (size_t)b.groups * sizeof(int) : 0;
-  PISA_TIMED("bucket_count", stream, hipLaunchKernelGGL((bucket_count_kernel<Src>), dim3(grid), dim3(kBucketThreads), lds, stream,
-                     src, slot_begin, slot_end, chunk, (int)b.groups, use_lds ? 1 : 0, b.counts));
+  PISA_TIMED("bucket_count", stream, hipLaunchKernelGGL((bucket_count_kernel<Src>), dim3(grid), dim3(kBucketThreads), 0, stream,
+                     src, slot_begin, slot_end, chunk, b.counts));
   PISA_TIMED("bucket_scan", stream, hipLaunchKernelGGL(bucket_scan_kernel, dim3(1), dim3(1024), 0, stream, b.counts, b.groups,
                      b.tile, b.tile_off, b.num_tiles));
-  PISA_TIMED("bucket_scatter", stream, hipLaunchKernelGGL((bucket_scatter_kernel<Src>), dim3(grid), dim3(kBucketThreads), lds, stream,
-                     src, slot_begin, slot_end, chunk, (int)b.groups, use_lds ? 1 : 0, b.tile_off, b.cursors,
-                     b.tile, b.tile_group, b.tile_req));
+  PISA_TIMED("bucket_scatter", stream, hipLaunchKernelGGL((bucket_scatter_kernel<Src>), dim3(grid), dim3(kBucketThreads), 0, stream,
+                     src, slot_begin, slot_end, chunk, b.tile_off, b.cursors, b.tile, b.tile_group,
+                     b.tile_req));
   return check_launch("bucket");
 }
 

@@ -59,6 +59,7 @@ struct Buckets {
   int32_t* tile_group;  // [max_tiles]
   int32_t* tile_req;    // [max_tiles * tile]
   int32_t* num_tiles;   // [1]
+  int32_t* hist;        // [kMaxBucketGroups rows][groups]: per-workgroup histograms, then offsets
   int64_t groups;
   int64_t max_tiles;
   int tile;

@@ -65,6 +65,8 @@ CASES = [
     ("bf16-c128", 1, 512, 640, 8, 2, 128, 128, 3, "bf16", True, None),
     # 2048-token windows over the flattened (batch, token) axis: two, the first across batches
     ("bf16-windows", 2, 1500, 1500, 16, 1, 128, 64, 6, "bf16", True, None),
+    # 3 x 8 x 1024 = 24576 (batch, kv head, block) groups: bucketing with global atomics
+    ("bf16-wide", 3, 40, 65536, 8, 8, 16, 64, 4, "bf16", True, None),
 ]
 
 
