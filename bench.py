@@ -252,7 +252,7 @@ def main():
         att_ms = sum(m[1].elapsed_time(m[2]) for m in marks) / args.steps
         step_ms = sel_ms + att_ms
 
-        train_ms = None
+        train_ms, train_kernels = None, {}
         if args.backward:
             print("[bench] attention forward + backward", file=sys.stderr, flush=True)
             ids = select()
@@ -278,6 +278,9 @@ def main():
             t1.record(stream)
             torch.cuda.synchronize()
             train_ms = t0.elapsed_time(t1) / args.steps
+            _lib.profile_begin()
+            train()
+            train_kernels = {n: round(total, 4) for n, (cnt, total) in _lib.profile_end().items()}
 
         print("[bench] kernel timing", file=sys.stderr, flush=True)
         _lib.profile_begin()
@@ -382,6 +385,7 @@ def main():
         # forward 4 D G P flops, backward 10 D G P (S recomputed)
         result["attn_fwd_bwd_ms"] = round(train_ms, 3)
         result["attn_fwd_bwd_tflops"] = round(14 * D * G * pairs / (train_ms * 1e-3) / 1e12, 2)
+        result["attn_fwd_bwd_kernel_ms"] = dict(sorted(train_kernels.items(), key=lambda x: -x[1]))
     del sel_kernels
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)

@@ -120,6 +120,18 @@ int pisa_build_pyramid(const void* keys, int64_t k_stride_batch, int64_t k_strid
                        int32_t block_size, int32_t branching, int32_t max_level,
                        void* storage, int64_t storage_stride_batch, int32_t dtype, void* stream);
 
+/* PyramidCache.append (xmixers/xmixers/utils/attention_cache.py:121-140, the
+ * per-level mean_pool calls over the changed range): the key buffer grew from
+ * `previous` to `tokens` valid tokens; recompute level-0 nodes from
+ * floor(previous / block_size) on and, on each level l < levels, the ancestors
+ * of the changed nodes (first changed node / branching), in packed storage whose
+ * level l starts at row starts[l] (host array).  Nodes equal pisa_build_pyramid's. */
+int pisa_pyramid_append(const void* keys, int64_t k_stride_batch, int64_t k_stride_token,
+                        int32_t batch, int32_t previous, int32_t tokens, int32_t heads, int32_t dim,
+                        int32_t block_size, int32_t branching, int32_t levels,
+                        const int32_t* starts, void* storage, int64_t storage_stride_batch,
+                        int32_t dtype, void* stream);
+
 /* Workspace bytes for pisa_select / pisa_leaf_scores. */
 size_t pisa_select_workspace_size(const pisa_qk_desc* qk, const pisa_select_params* p);
 

@@ -67,6 +67,22 @@ struct Buckets {
 
 void carve_buckets(Carve& c, Buckets& b, int64_t slots, int64_t groups, int tile);
 
+// The tiles a consumer workgroup walks when workgroups are dealt round-robin
+// to the 8 XCDs: XCD x = blockIdx.x % 8 takes the contiguous eighth
+// [ntiles x / 8, ntiles (x + 1) / 8) of the (batch, kv head, block)-ordered
+// tile list, its workgroups striding by gridDim.x / 8, so the tiles an XCD runs
+// together come from few kv heads and share their query rows in its L2.  The
+// eighths partition the list for any placement; gridDim.x must be a multiple of 8.
+struct XcdTiles {
+  int begin, end, step;
+};
+
+__device__ __forceinline__ XcdTiles xcd_tiles(int ntiles) {
+  const int x = (int)(blockIdx.x & 7);
+  return XcdTiles{(int)((int64_t)ntiles * x / 8) + (int)(blockIdx.x >> 3),
+                  (int)((int64_t)ntiles * (x + 1) / 8), (int)(gridDim.x >> 3)};
+}
+
 // Sources of bucketed requests.
 struct LeafRequests {
   const int32_t* cand;      // [B,T,Hkv,W]

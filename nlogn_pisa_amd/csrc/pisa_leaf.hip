@@ -239,7 +239,8 @@ __global__ void __launch_bounds__(256, (NTM <= 4 ? PISA_LEAF_WAVES : 2)) leaf_ti
   constexpr int vpr = HD / vec;
   const int ntiles = *a.num_tiles;
 
-  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+  const XcdTiles walk = xcd_tiles(ntiles);
+  for (int tile = walk.begin; tile < walk.end; tile += walk.step) {
     const int g = a.tile_group[tile];
     const int blk = g % a.M0;
     const int bh = g / a.M0;

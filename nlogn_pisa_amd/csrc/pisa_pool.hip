@@ -165,6 +165,77 @@ static int pool_dispatch(int dtype, const void* src, int64_t src_batch, int64_t 
   }
 }
 
+// Incremental pyramid update (PyramidCache.append, attention_cache.py:121-140)
+// for a few changed leaves: thread t owns VEC consecutive elements of the
+// Hkv*D row of batch blockIdx.y and recomputes, level by level, the changed
+// nodes of its columns: level 0 nodes [changed, ceil(tokens / C)) from the
+// keys, level l nodes [changed_l = changed_{l-1} / b, ceil(count_{l-1} / b))
+// from level l - 1 (its own earlier writes, or nodes an earlier append left).
+// Same arithmetic as pool_kernel (exact sums, one rounding), so the nodes equal
+// a full rebuild's.
+struct LevelStarts {
+  int32_t v[PISA_MAX_LEVELS];
+};
+
+template <typename T, int VEC>
+__global__ void __launch_bounds__(256) append_kernel(const T* __restrict__ keys, int64_t k_batch,
+                                                     int64_t k_token, int tokens, int C, int b,
+                                                     int levels, LevelStarts starts, int changed,
+                                                     T* storage, int64_t s_batch, int row_elems) {
+  const int c = (blockIdx.x * blockDim.x + threadIdx.x) * VEC;
+  if (c >= row_elems) return;
+  const T* kb = keys + blockIdx.y * k_batch + c;
+  T* sb = storage + blockIdx.y * s_batch + c;
+  auto mean = [&](const T* src, int64_t stride, int n, T* dst) {
+    double acc[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] = 0.0;
+    for (int r = 0; r < n; ++r) {
+      float v[VEC];
+      load_f<VEC>(src + (int64_t)r * stride, v);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc[e] += (double)v[e];
+    }
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) dst[e] = from_f<T>((float)(acc[e] / (double)n));
+  };
+  int count = (tokens + C - 1) / C;
+  for (int node = changed; node < count; ++node)
+    mean(kb + (int64_t)node * C * k_token, k_token, min(C, tokens - node * C),
+         sb + (int64_t)(starts.v[0] + node) * row_elems);
+  for (int l = 1; l < levels; ++l) {
+    changed /= b;
+    const int next = (count + b - 1) / b;
+    for (int node = changed; node < next; ++node)
+      mean(sb + (int64_t)(starts.v[l - 1] + node * b) * row_elems, row_elems,
+           min(b, count - node * b), sb + (int64_t)(starts.v[l] + node) * row_elems);
+    count = next;
+  }
+}
+
+template <typename T>
+static int launch_append(const void* keys, int64_t k_batch, int64_t k_token, int batch, int tokens,
+                         int row_elems, int C, int b, int levels, const LevelStarts& starts,
+                         int changed, void* storage, int64_t s_batch, hipStream_t stream) {
+  constexpr int vec = 16 / (int)sizeof(T);
+  const bool aligned = row_elems % vec == 0 && k_batch % vec == 0 && k_token % vec == 0 &&
+                       s_batch % vec == 0 && (uintptr_t)keys % 16 == 0 &&
+                       (uintptr_t)storage % 16 == 0;
+  const T* k = static_cast<const T*>(keys);
+  T* s = static_cast<T*>(storage);
+  if (aligned) {
+    const int threads = row_elems / vec;
+    dim3 grid((threads + 255) / 256, batch);
+    PISA_TIMED("pool_append", stream, hipLaunchKernelGGL((append_kernel<T, vec>), grid, dim3(256), 0, stream, k, k_batch,
+                       k_token, tokens, C, b, levels, starts, changed, s, s_batch, row_elems));
+  } else {
+    dim3 grid((row_elems + 255) / 256, batch);
+    PISA_TIMED("pool_append", stream, hipLaunchKernelGGL((append_kernel<T, 1>), grid, dim3(256), 0, stream, k, k_batch,
+                       k_token, tokens, C, b, levels, starts, changed, s, s_batch, row_elems));
+  }
+  return check_launch("pyramid append");
+}
+
 }  // namespace pisa
 
 using namespace pisa;
@@ -243,6 +314,51 @@ extern "C" int pisa_build_pyramid(const void* keys, int64_t k_stride_batch, int6
     rc = pool_dispatch(dtype, base + (int64_t)offsets[l - 1] * row * es, storage_stride_batch, row,
                        batch, lengths[l - 1], row, branching, base + (int64_t)offsets[l] * row * es,
                        storage_stride_batch, row, (hipStream_t)stream);
+  }
+  return rc;
+}
+
+extern "C" int pisa_pyramid_append(const void* keys, int64_t k_stride_batch, int64_t k_stride_token,
+                                   int32_t batch, int32_t previous, int32_t tokens, int32_t heads,
+                                   int32_t dim, int32_t block_size, int32_t branching,
+                                   int32_t levels, const int32_t* starts, void* storage,
+                                   int64_t storage_stride_batch, int32_t dtype, void* stream) {
+  if (!keys || !storage || !starts) return fail(PISA_ERR_INVALID, "null argument");
+  if (block_size < 1 || branching < 2 || heads < 1 || dim < 1 || batch < 0)
+    return fail(PISA_ERR_INVALID, "bad pyramid append shape");
+  if (previous < 0 || tokens < previous) return fail(PISA_ERR_INVALID, "appends only grow the cache");
+  if (levels < 1 || levels > PISA_MAX_LEVELS)
+    return fail(PISA_ERR_INVALID, "levels must be in [1, %d]", PISA_MAX_LEVELS);
+  const int es = dtype_size(dtype);
+  if (!es) return fail(PISA_ERR_INVALID, "unknown dtype %d", dtype);
+  if (tokens == previous || batch == 0) return PISA_OK;
+  const int row = heads * dim;
+  const int changed = previous / block_size;
+  const int count0 = (tokens + block_size - 1) / block_size;
+  hipStream_t st = (hipStream_t)stream;
+  if (count0 - changed <= 4) {
+    LevelStarts ls{};
+    for (int l = 0; l < levels; ++l) ls.v[l] = starts[l];
+    switch (dtype) {
+      case PISA_F32: return launch_append<float>(keys, k_stride_batch, k_stride_token, batch, tokens, row, block_size, branching, levels, ls, changed, storage, storage_stride_batch, st);
+      case PISA_F16: return launch_append<f16_t>(keys, k_stride_batch, k_stride_token, batch, tokens, row, block_size, branching, levels, ls, changed, storage, storage_stride_batch, st);
+      default: return launch_append<bf16_t>(keys, k_stride_batch, k_stride_token, batch, tokens, row, block_size, branching, levels, ls, changed, storage, storage_stride_batch, st);
+    }
+  }
+  // many changed leaves: one parallel pooling launch per level over the changed range
+  char* base = static_cast<char*>(storage);
+  const char* kb = static_cast<const char*>(keys);
+  int first = changed, count = count0;
+  int rc = pool_dispatch(dtype, kb + (int64_t)first * block_size * k_stride_token * es, k_stride_batch,
+                         k_stride_token, batch, tokens - first * block_size, row, block_size,
+                         base + ((int64_t)starts[0] + first) * row * es, storage_stride_batch, row, st);
+  for (int l = 1; l < levels && rc == PISA_OK; ++l) {
+    first /= branching;
+    const int next = (count + branching - 1) / branching;
+    rc = pool_dispatch(dtype, base + ((int64_t)starts[l - 1] + (int64_t)first * branching) * row * es,
+                       storage_stride_batch, row, batch, count - first * branching, row, branching,
+                       base + ((int64_t)starts[l] + first) * row * es, storage_stride_batch, row, st);
+    count = next;
   }
   return rc;
 }

@@ -110,3 +110,40 @@ def test_synthetic_inputs_are_deterministic():
     means = k.reshape(1, 64, 64, 4, 64).mean(2)
     assert means.std() > 0.35
     assert config(2).needles == 0.01 and config(3).per_sequence_seed
+
+
+def test_tensor_cache_growth_and_errors():
+    """``attention_cache.py:8-48``: power-of-two capacity, copy on growth, fixed shape."""
+    cache = P.TensorCache()
+    with pytest.raises(ValueError, match="the token cache is empty"):
+        cache.tensor
+    chunks = [torch.randn(2, n, 3, 4) for n in (1, 2, 5, 1, 9)]
+    capacities = []
+    for chunk in chunks:
+        cache.append(chunk)
+        capacities.append(cache.buffer.shape[1])
+    assert capacities == [1, 4, 8, 16, 32]
+    assert torch.equal(cache.tensor, torch.cat(chunks, 1))
+    with pytest.raises(ValueError, match=r"nonempty \[B,T,H,D\] floating tensor"):
+        cache.append(torch.zeros(2, 0, 3, 4))
+    with pytest.raises(ValueError, match=r"nonempty \[B,T,H,D\] floating tensor"):
+        cache.append(torch.zeros(2, 1, 3, 4, dtype=torch.int32))
+    with pytest.raises(ValueError, match="cannot change"):
+        cache.append(torch.zeros(2, 1, 3, 5))
+
+
+def test_pyramid_cache_layout():
+    """Level capacities: next power of two of the leaves, divided by b (rounded up) to 1."""
+    cache = P.PyramidCache(block_size=64, branching=2)
+    cache.reserve(torch.zeros(1, 1, 2, 8), 5)
+    assert cache.capacities == (8, 4, 2, 1) and cache.starts == (0, 8, 12, 14)
+    assert cache.storage.shape == (1, 15, 2, 8)
+    cache.reserve(torch.zeros(1, 1, 2, 8), 8)       # fits: no re-layout
+    assert cache.capacities == (8, 4, 2, 1)
+    wide = P.PyramidCache(block_size=16, branching=4)
+    wide.reserve(torch.zeros(1, 1, 2, 8), 17)
+    assert wide.capacities == (32, 8, 2, 1) and wide.starts == (0, 32, 40, 42)
+    with pytest.raises(ValueError, match="branching must be at least 2"):
+        P.PyramidCache(branching=1)
+    with pytest.raises(ValueError, match="runs on a ROCm GPU"):
+        P.PyramidCache().append(torch.zeros(1, 4, 2, 8))
