@@ -222,10 +222,15 @@ def main():
     positions = P.query_positions(q, k)
     dname = {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[w.dtype]
 
+    # Decode keeps the key pyramid in a PyramidCache that each generated token
+    # appends to; the step reads it (its append is timed on its own below).
+    decode = w.tokens == 1
+    cache = (P.PyramidCache.from_keys(k, w.block_size, w.branching) if decode else None)
+
     def select():
         return P.select_blocks(q, k, method=w.method, block_size=w.block_size, topk=w.topk,
                                force_first=w.force_first, force_recent=w.force_recent,
-                               backend="auto", branching=w.branching)
+                               backend="auto", branching=w.branching, pyramid=cache)
 
     def attend(ids):
         return P.sparse_attention_with_lse(q, k, v, ids, block_size=w.block_size)
@@ -251,6 +256,26 @@ def main():
         sel_ms = sum(m[0].elapsed_time(m[1]) for m in marks) / args.steps
         att_ms = sum(m[1].elapsed_time(m[2]) for m in marks) / args.steps
         step_ms = sel_ms + att_ms
+
+        append_ms = None
+        if decode:
+            print("[bench] pyramid cache append", file=sys.stderr, flush=True)
+            del cache
+            start = w.keys - args.warmup - args.steps
+            grow = P.PyramidCache.from_keys(k[:, :start], w.block_size, w.branching)
+            for n in range(start, start + args.warmup):
+                grow.append(k[:, n:n + 1])
+            torch.cuda.synchronize()
+            t0 = torch.cuda.Event(enable_timing=True)
+            t1 = torch.cuda.Event(enable_timing=True)
+            t0.record(stream)
+            for n in range(start + args.warmup, w.keys):
+                grow.append(k[:, n:n + 1])
+            t1.record(stream)
+            torch.cuda.synchronize()
+            append_ms = t0.elapsed_time(t1) / args.steps
+            cache = grow
+            del grow
 
         train_ms, train_kernels = None, {}
         if args.backward:
@@ -363,7 +388,8 @@ def main():
                    "query_heads": w.query_heads, "kv_heads": w.key_heads, "head_dim": D,
                    "block_size": w.block_size, "branching": w.branching, "topk": w.topk,
                    "method": w.method, "forced": f"first + {w.force_recent} recent",
-                   "step": "select_blocks + sparse_attention forward (O, LSE)"},
+                   "step": "select_blocks + sparse_attention forward (O, LSE)"
+                           + (" over a PyramidCache" if decode else "")},
         "selection_ms": round(sel_ms, 3),
         "sparse_attn_ms": round(att_ms, 3),
         "sparse_attn_tflops": round(attn_flops / (att_ms * 1e-3) / 1e12, 2),
@@ -381,6 +407,8 @@ def main():
         "roofline": roofline,
         "wall_s_timed": round(wall, 3),
     }
+    if append_ms is not None:
+        result["pyramid_append_ms"] = round(append_ms, 4)
     if train_ms is not None:
         # forward 4 D G P flops, backward 10 D G P (S recomputed)
         result["attn_fwd_bwd_ms"] = round(train_ms, 3)

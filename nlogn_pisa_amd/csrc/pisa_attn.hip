@@ -373,6 +373,10 @@ __host__ __device__ inline TileLds tile_lds(int C, int tile) {
 #ifndef PISA_ATTN_WAVES
 #define PISA_ATTN_WAVES 2
 #endif
+// 1: every backward takes the LDS-staged kernel (for comparisons).
+#ifndef PISA_BWD_LDS
+#define PISA_BWD_LDS 0
+#endif
 
 // LDS row of value dv in V^T: dv = (D/4) j + 4 dt + c is stored at row
 // 16 dt + 4 j + c, the row that lane col = 4 j + c reads for dv tile dt, so the
@@ -384,26 +388,32 @@ __device__ __forceinline__ int vt_row(int dv) {
   return 16 * (rem >> 2) + 4 * j + (rem & 3);
 }
 
-// Stage the K block row-major and the V block transposed (rows in vt_row
-// order), zero from `rows` up to Cq keys.  16-bit V^T is written two keys per
-// 32-bit word with consecutive lanes on consecutive key pairs.
+// Copy `rows` rows of HD elements (row stride `stride`) into LDS rows of
+// `ld` elements, zero from `rows` up to Cq rows.
 template <typename T, int HD>
-__device__ void stage_tile(const AttnArgs& a, int b, int h, int64_t blk, int rows, T* ks, T* vt,
-                           const TileLds& L, int tid, int nthr) {
+__device__ void stage_rows(const T* src, int64_t stride, int rows, int Cq, T* dst, int ld, int tid,
+                           int nthr) {
   constexpr int vec = 16 / (int)sizeof(T);
   constexpr int vpr = HD / vec;
-  const T* kb = static_cast<const T*>(a.k) + (int64_t)b * a.k_batch + blk * a.C * a.k_token +
-                (int64_t)h * HD;
-  const T* vb = static_cast<const T*>(a.v) + (int64_t)b * a.v_batch + blk * a.C * a.v_token +
-                (int64_t)h * HD;
-  for (int idx = tid; idx < L.Cq * vpr; idx += nthr) {
+  for (int idx = tid; idx < Cq * vpr; idx += nthr) {
     const int r = idx / vpr, c = (idx % vpr) * vec;
     uint4 v = make_uint4(0, 0, 0, 0);
-    if (r < rows) v = *reinterpret_cast<const uint4*>(kb + (int64_t)r * a.k_token + c);
-    *reinterpret_cast<uint4*>(ks + r * L.ldk + c) = v;
+    if (r < rows) v = *reinterpret_cast<const uint4*>(src + (int64_t)r * stride + c);
+    *reinterpret_cast<uint4*>(dst + r * ld + c) = v;
   }
+}
+
+// Copy `rows` rows of HD elements transposed into LDS: element (r, c) goes to
+// row vt_row(c), column r; zero from `rows` up to Cq columns.  16-bit values
+// are written two rows per 32-bit word with consecutive lanes on consecutive
+// row pairs.
+template <typename T, int HD>
+__device__ void stage_transposed(const T* src, int64_t stride, int rows, int Cq, T* dst, int ld,
+                                 int tid, int nthr) {
+  constexpr int vec = 16 / (int)sizeof(T);
+  constexpr int vpr = HD / vec;
   if constexpr (sizeof(T) == 2) {
-    const int pairs = L.Cq / 2;
+    const int pairs = Cq / 2;
     for (int idx = tid; idx < pairs * vpr; idx += nthr) {
       const int r = (idx % pairs) * 2, c = (idx / pairs) * vec;
       union {
@@ -412,25 +422,38 @@ __device__ void stage_tile(const AttnArgs& a, int b, int h, int64_t blk, int row
       } v0, v1;
       v0.u = make_uint4(0, 0, 0, 0);
       v1.u = make_uint4(0, 0, 0, 0);
-      if (r < rows) v0.u = *reinterpret_cast<const uint4*>(vb + (int64_t)r * a.v_token + c);
-      if (r + 1 < rows) v1.u = *reinterpret_cast<const uint4*>(vb + (int64_t)(r + 1) * a.v_token + c);
+      if (r < rows) v0.u = *reinterpret_cast<const uint4*>(src + (int64_t)r * stride + c);
+      if (r + 1 < rows) v1.u = *reinterpret_cast<const uint4*>(src + (int64_t)(r + 1) * stride + c);
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        *reinterpret_cast<uint32_t*>(vt + vt_row<HD>(c + e) * L.ldv + r) =
+        *reinterpret_cast<uint32_t*>(dst + vt_row<HD>(c + e) * ld + r) =
             (uint32_t)v0.e[e] | ((uint32_t)v1.e[e] << 16);
     }
   } else {
-    for (int idx = tid; idx < L.Cq * vpr; idx += nthr) {
-      const int r = idx % L.Cq, c = (idx / L.Cq) * vec;
+    for (int idx = tid; idx < Cq * vpr; idx += nthr) {
+      const int r = idx % Cq, c = (idx / Cq) * vec;
       float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (r < rows) v = *reinterpret_cast<const float4*>(vb + (int64_t)r * a.v_token + c);
-      float* vf = reinterpret_cast<float*>(vt);
-      vf[vt_row<HD>(c + 0) * L.ldv + r] = v.x;
-      vf[vt_row<HD>(c + 1) * L.ldv + r] = v.y;
-      vf[vt_row<HD>(c + 2) * L.ldv + r] = v.z;
-      vf[vt_row<HD>(c + 3) * L.ldv + r] = v.w;
+      if (r < rows) v = *reinterpret_cast<const float4*>(src + (int64_t)r * stride + c);
+      float* df = reinterpret_cast<float*>(dst);
+      df[vt_row<HD>(c + 0) * ld + r] = v.x;
+      df[vt_row<HD>(c + 1) * ld + r] = v.y;
+      df[vt_row<HD>(c + 2) * ld + r] = v.z;
+      df[vt_row<HD>(c + 3) * ld + r] = v.w;
     }
   }
+}
+
+// Stage the K block row-major and the V block transposed (rows in vt_row
+// order), zero from `rows` up to Cq keys.
+template <typename T, int HD>
+__device__ void stage_tile(const AttnArgs& a, int b, int h, int64_t blk, int rows, T* ks, T* vt,
+                           const TileLds& L, int tid, int nthr) {
+  const T* kb = static_cast<const T*>(a.k) + (int64_t)b * a.k_batch + blk * a.C * a.k_token +
+                (int64_t)h * HD;
+  const T* vb = static_cast<const T*>(a.v) + (int64_t)b * a.v_batch + blk * a.C * a.v_token +
+                (int64_t)h * HD;
+  stage_rows<T, HD>(kb, a.k_token, rows, L.Cq, ks, L.ldk, tid, nthr);
+  stage_transposed<T, HD>(vb, a.v_token, rows, L.Cq, vt, L.ldv, tid, nthr);
 }
 
 // A fragment of V^T for P V step kk: row `vrow` (a permuted dv), the keys whose
@@ -985,7 +1008,9 @@ __global__ void __launch_bounds__(512) attn_bwd_grouped_kernel(AttnArgs a) {
 }
 
 // dK/dV of every key: the sum of its block's tile partials in tile order
-// (zero for blocks no row selected).  One workgroup per (batch, head, block).
+// (zero for blocks no row selected).  One workgroup per (batch, head, block);
+// a thread owns 4 consecutive columns of a key row and has four tiles' loads
+// in flight at a time.
 template <typename T>
 __global__ void __launch_bounds__(256) attn_dkv_reduce_kernel(AttnArgs a, int64_t groups) {
   const int64_t g = blockIdx.x;
@@ -997,44 +1022,372 @@ __global__ void __launch_bounds__(256) attn_dkv_reduce_kernel(AttnArgs a, int64_
   const int rows = (int)min((int64_t)a.C, (int64_t)a.N - blk * a.C);
   const int first = a.tile_off[g];
   const int n = (a.counts[g] + a.tile - 1) / a.tile;
-  const int width = a.D + a.Dv;
-  for (int idx = threadIdx.x; idx < rows * width; idx += blockDim.x) {
-    const int r = idx / width, c = idx % width;
-    float s = 0.f;
-    for (int j = 0; j < n; ++j) s += a.part_dkv[((int64_t)(first + j) * Cp + r) * width + c];
+  const int width = a.D + a.Dv;  // a multiple of 4
+  const int quads = width / 4;
+  const int64_t tile_stride = (int64_t)Cp * width / 4;
+  const float4* part = reinterpret_cast<const float4*>(a.part_dkv) + (int64_t)first * tile_stride;
+  for (int idx = threadIdx.x; idx < rows * quads; idx += blockDim.x) {
+    const int r = idx / quads, c = (idx % quads) * 4;
+    const float4* src = part + (int64_t)r * quads + c / 4;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    int j = 0;
+    for (; j + 4 <= n; j += 4) {
+      float4 v[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[k] = src[(int64_t)(j + k) * tile_stride];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        acc.x += v[k].x;
+        acc.y += v[k].y;
+        acc.z += v[k].z;
+        acc.w += v[k].w;
+      }
+    }
+    for (; j < n; ++j) {
+      const float4 v = src[(int64_t)j * tile_stride];
+      acc.x += v.x;
+      acc.y += v.y;
+      acc.z += v.z;
+      acc.w += v.w;
+    }
     const int64_t tok = blk * a.C + r;
-    if (c < a.D)
-      static_cast<T*>(a.dk)[(int64_t)b * a.dk_batch + tok * a.dk_token + (int64_t)h * a.D + c] = from_f<T>(s);
-    else
-      static_cast<T*>(a.dv)[(int64_t)b * a.dv_batch + tok * a.dv_token + (int64_t)h * a.Dv + (c - a.D)] =
-          from_f<T>(s);
+    const float vals[4] = {acc.x, acc.y, acc.z, acc.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int cc = c + e;
+      if (cc < a.D)
+        static_cast<T*>(a.dk)[(int64_t)b * a.dk_batch + tok * a.dk_token + (int64_t)h * a.D + cc] = from_f<T>(vals[e]);
+      else
+        static_cast<T*>(a.dv)[(int64_t)b * a.dv_batch + tok * a.dv_token + (int64_t)h * a.Dv + (cc - a.D)] =
+            from_f<T>(vals[e]);
+    }
   }
 }
 
-// dQ of each (batch, token, query head): its visible slots' partials in slot order.
+// dQ of each (batch, token, kv head): the [G, D] partials of its visible slots
+// summed in slot order.  One wave per item; a lane owns 16-byte chunks
+// lane, lane + 64, ... of the item's G D values, and four slots' chunks are
+// loaded before any is added.  Slot visibility is one ballot per 64 slots.
 template <typename T>
 __global__ void __launch_bounds__(256) attn_dq_combine_kernel(AttnArgs a, int64_t items) {
   const int lane = threadIdx.x & 63;
   const int64_t item = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (item >= items) return;
   const RowInfo ri = row_info(a, item * a.K);
-  for (int gh = 0; gh < a.G; ++gh) {
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < a.K; ++s) {
-      const int64_t slot = item * a.K + s;
-      if (!slot_visible(a, slot_block(a, slot), ri.pos)) continue;
+  const int chunks = a.G * a.D / 4;
+  const float4* part = reinterpret_cast<const float4*>(a.part_dq);
+  T* out = static_cast<T*>(a.dq) + item * a.G * a.D;
+  for (int c0 = 0; c0 < chunks; c0 += 256) {
+    float4 acc[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int d = lane + 64 * j;
-        if (d < a.D) acc[j] += a.part_dq[(slot * a.G + gh) * a.D + d];
+    for (int j = 0; j < 4; ++j) acc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s0 = 0; s0 < a.K; s0 += 64) {
+      const int sl = s0 + lane;
+      const bool vis = sl < a.K && slot_visible(a, slot_block(a, item * a.K + sl), ri.pos);
+      uint64_t mask = __ballot(vis);
+      while (mask) {
+        // up to four visible slots at a time, in slot order
+        int64_t sidx[4];
+        int cnt = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          sidx[k] = -1;
+          if (mask) {
+            const int bit = __ffsll((unsigned long long)mask) - 1;
+            mask &= mask - 1;
+            sidx[k] = item * a.K + s0 + bit;
+            ++cnt;
+          }
+        }
+        float4 v[4][4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int c = c0 + lane + 64 * j;
+            v[k][j] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (k < cnt && c < chunks) v[k][j] = part[sidx[k] * chunks + c];
+          }
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            acc[j].x += v[k][j].x;
+            acc[j].y += v[k][j].y;
+            acc[j].z += v[k][j].z;
+            acc[j].w += v[k][j].w;
+          }
       }
     }
-    T* out = static_cast<T*>(a.dq) + (item * a.G + gh) * a.D;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int d = lane + 64 * j;
-      if (d < a.D) out[d] = from_f<T>(acc[j]);
+      const int c = c0 + lane + 64 * j;
+      if (c < chunks) {
+        T* o = out + 4 * c;
+        o[0] = from_f<T>(acc[j].x);
+        o[1] = from_f<T>(acc[j].y);
+        o[2] = from_f<T>(acc[j].z);
+        o[3] = from_f<T>(acc[j].w);
+      }
     }
+  }
+}
+
+// ------------------------------------------------------------------ backward, register tiles
+//
+// 16-bit inputs with D == Dv in {32, 64, 128} and blocks of up to 16 NT keys.
+// One workgroup of two waves per tile.  Both waves take every 16-row unit
+// (row = request x Gp + head) of the tile; wave w owns half w of the head dim
+// of dK, dV and dQ, so the waves never exchange data and each keeps its half
+// of dK and dV of all of the block's keys in registers for the whole tile:
+//   S = Q K^T and dP = dO V^T with a lane per key (rows 4 grp + i),
+//   P = exp(scale S - LSE), dS = P (dP - delta),
+//   dV += P^T dO and dK += dS^T Q, where P^T and dS^T are the A operands exactly
+//     as computed and Q, dO enter transposed: a selection product per fragment
+//     (B = 0/1 matrix) turns a row-per-lane fragment into a column-per-lane
+//     one, exactly, on the matrix cores,
+//   dQ^T = K^T dS^T, with dS^T turned to a row per lane by an identity product,
+//     written as the slot's partial.
+// P and dS enter as 16-bit hi + lo pairs concatenated along the reduction
+// (k = 8 grp + e: e < 4 hi, e >= 4 lo of the same row), so one 16x16x32 product
+// takes both halves.  Nothing is staged per unit, so units need no barrier;
+// each wave loads the next unit's rows while it computes the current one.
+
+struct BwdTileLds {
+  int Cq, ldk, ldt;
+  size_t ks, vs, kt, mq, mo, mpos, mslot, bytes;
+};
+
+template <typename T, int HD>
+__host__ __device__ inline BwdTileLds bwd_tile_lds(int NT, int tile) {
+  constexpr int PAD = 16 / (int)sizeof(T);
+  BwdTileLds L;
+  L.Cq = 16 * NT;
+  L.ldk = HD + PAD;
+  L.ldt = L.Cq + PAD;
+  size_t off = 0;
+  auto take = [&](size_t bytes) { const size_t at = off; off = (off + bytes + 15) / 16 * 16; return at; };
+  L.ks = take((size_t)L.Cq * L.ldk * sizeof(T));
+  L.vs = take((size_t)L.Cq * L.ldk * sizeof(T));
+  L.kt = take((size_t)HD * L.ldt * sizeof(T));
+  L.mq = take((size_t)tile * 8);
+  L.mo = take((size_t)tile * 8);
+  L.mpos = take((size_t)tile * 8);
+  L.mslot = take((size_t)tile * 4);
+  L.bytes = off;
+  return L;
+}
+
+// Whether the register-tile backward serves NT key tiles: a wave's dK and dV
+// take 8 NT (HD / 32) accumulator registers, at most 128 here.
+template <int HD>
+constexpr bool bwd_tile_fits(int NT) {
+  return NT * (HD / 32) <= 16;
+}
+
+template <typename T, int HD, int NT>
+__global__ void __launch_bounds__(128, 1) attn_bwd_tile_kernel(AttnArgs a) {
+  typedef QkShape<T, HD> Sh;
+  typedef typename Sh::Op Op;     // 16x16x32
+  typedef typename Sh::frag frag;
+  typedef MfmaOp<T, 4> Op4;       // 16x16x16 (the identity product)
+  typedef typename Op4::frag frag4;
+  static_assert(Sh::E == 8, "16-bit types with head dims of at least 32");
+  constexpr int QL = Sh::QL, DS = Sh::DS, NDT = Sh::NDT;
+  constexpr int NH = NDT / 2;     // this wave's 16-wide tiles of dK/dV and of dQ^T
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int hf = tid >> 6;        // head-dim half
+  const BwdTileLds L = bwd_tile_lds<T, HD>(NT, a.tile);
+  T* ks = reinterpret_cast<T*>(smem + L.ks);
+  T* vs = reinterpret_cast<T*>(smem + L.vs);
+  T* kt = reinterpret_cast<T*>(smem + L.kt);
+  int64_t* mq = reinterpret_cast<int64_t*>(smem + L.mq);
+  int64_t* mo = reinterpret_cast<int64_t*>(smem + L.mo);
+  int64_t* mpos = reinterpret_cast<int64_t*>(smem + L.mpos);
+  int32_t* mslot = reinterpret_cast<int32_t*>(smem + L.mslot);
+  const int col = lane & 15, grp = lane >> 4;
+  const int Gp = a.Gp, gl = 31 - __clz(Gp);
+  const int Cp = (a.C + 15) / 16 * 16;
+  const int Hq = a.Hkv * a.G;
+  const T* qg = static_cast<const T*>(a.q);
+  const T* og = static_cast<const T*>(a.dout);
+  const f4 zero4 = f4{0.f, 0.f, 0.f, 0.f};
+
+  // Selection fragment: B[k][n] = 1 iff the d of reduction index k (lane group
+  // grp, element e: d = QL grp + 8 ds + e) is column n's
+  // d = QL (2 hf + n / 8) + 8 ds + n % 8 (the same for every ds), so output
+  // tile ds of a wave covers d in [2 hf QL, 2 hf QL + 2 QL).  Identity of the
+  // 16x16x16 product: I[k][n] = 1 iff 4 grp + e == n.
+  frag sel;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) Op::set(sel, e, grp == 2 * hf + (col >> 3) && e == (col & 7) ? 1.f : 0.f);
+  frag4 ident;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) Op4::set(ident, e, 4 * grp + e == col ? 1.f : 0.f);
+
+  struct Rows {
+    frag q[DS], o[DS];
+    float lse[4], del[4];
+  };
+
+  const int ntiles = *a.num_tiles;
+  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int g = a.tile_group[tile];
+    const int64_t blk = g % a.M0;
+    const int bh = g / a.M0;
+    const int h = bh % a.Hkv, b = bh / a.Hkv;
+    const int start = (tile - a.tile_off[g]) * a.tile;
+    const int nreq = min(a.tile, a.counts[g] - start);
+    const int rows = (int)min((int64_t)a.C, (int64_t)a.N - blk * a.C);
+    const int32_t* reqs = a.tile_req + (int64_t)tile * a.tile;
+    __syncthreads();  // both waves are done with the previous tile's LDS
+    for (int i = tid; i < nreq; i += blockDim.x) {
+      const int32_t slot = reqs[i];
+      const RowInfo ri = row_info(a, slot);
+      mq[i] = (int64_t)ri.b * a.q_batch + (int64_t)ri.t * a.q_token + (int64_t)h * a.G * HD;
+      mo[i] = ((int64_t)ri.b * a.T + ri.t) * Hq + (int64_t)h * a.G;
+      mpos[i] = ri.pos;
+      mslot[i] = slot;
+    }
+    {
+      const T* kb = static_cast<const T*>(a.k) + (int64_t)b * a.k_batch + blk * a.C * a.k_token +
+                    (int64_t)h * HD;
+      const T* vb = static_cast<const T*>(a.v) + (int64_t)b * a.v_batch + blk * a.C * a.v_token +
+                    (int64_t)h * HD;
+      stage_rows<T, HD>(kb, a.k_token, rows, L.Cq, ks, L.ldk, tid, blockDim.x);
+      stage_rows<T, HD>(vb, a.v_token, rows, L.Cq, vs, L.ldk, tid, blockDim.x);
+      stage_transposed<T, HD>(kb, a.k_token, rows, L.Cq, kt, L.ldt, tid, blockDim.x);
+    }
+    __syncthreads();
+
+    f4 dk[NT][NH], dv[NT][NH];
+#pragma unroll
+    for (int m = 0; m < NT; ++m)
+#pragma unroll
+      for (int t = 0; t < NH; ++t) dk[m][t] = dv[m][t] = zero4;
+
+    const int units = (nreq * Gp + 15) >> 4;
+    // Rows of unit u: Q and dO of row `col` as A fragments, LSE and delta of
+    // rows 4 grp + i.  Every lane loads: rows that do not exist read request
+    // 0's first head and are masked (P = 0) and never stored.
+    auto fetch = [&](int u, Rows& r) {
+      {
+        const int rho = (u << 4) + col, rq = rho >> gl, gh = rho & (Gp - 1);
+        const bool ok = u < units && rq < nreq && gh < a.G;
+        const int rr = ok ? rq : 0, hh = ok ? gh : 0;
+        load_frags(qg + mq[rr] + (int64_t)hh * HD + QL * grp, r.q);
+        load_frags(og + (mo[rr] + hh) * HD + QL * grp, r.o);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int rho = (u << 4) + 4 * grp + i, rq = rho >> gl, gh = rho & (Gp - 1);
+        const bool ok = u < units && rq < nreq && gh < a.G;
+        const int64_t orow = mo[ok ? rq : 0] + (ok ? gh : 0);
+        r.lse[i] = a.lse[orow];
+        r.del[i] = a.delta[orow];
+      }
+    };
+    auto unit = [&](int u, Rows& r, Rows& into) {
+      fetch(u + 1, into);
+      // this half of Q and dO with a column per lane (rows 4 grp + e), as
+      // 16-bit words; the exact values of the selection products
+      uint2 qt[NH], ot[NH];
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds) {
+        const f4 cq = Op::mma(r.q[ds], sel, zero4);
+        const f4 co = Op::mma(r.o[ds], sel, zero4);
+        qt[ds] = make_uint2(Pack16<T>::pack(cq[0], cq[1]), Pack16<T>::pack(cq[2], cq[3]));
+        ot[ds] = make_uint2(Pack16<T>::pack(co[0], co[1]), Pack16<T>::pack(co[2], co[3]));
+      }
+      // visible keys of rows 4 grp + i: key < lim[i]
+      int lim[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int rho = (u << 4) + 4 * grp + i, rq = rho >> gl, gh = rho & (Gp - 1);
+        lim[i] = 0;
+        if (rq < nreq && gh < a.G) {
+          const int64_t last = a.causal ? mpos[rq] - blk * a.C + 1 : (int64_t)rows;
+          lim[i] = (int)min((int64_t)rows, last);
+        }
+      }
+      f4 dq[NH];
+#pragma unroll
+      for (int t = 0; t < NH; ++t) dq[t] = zero4;
+#pragma unroll
+      for (int m = 0; m < NT; ++m) {
+        __builtin_amdgcn_sched_barrier(0);
+        const int key = 16 * m + col;
+        f4 s = zero4, dp = zero4;
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) {
+          frag kf[1], vf[1];
+          load_frags(ks + key * L.ldk + QL * grp + 8 * ds, kf);
+          load_frags(vs + key * L.ldk + QL * grp + 8 * ds, vf);
+          s = Op::mma(r.q[ds], kf[0], s);
+          dp = Op::mma(r.o[ds], vf[0], dp);
+        }
+        float p[4], d[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          p[i] = key < lim[i] ? __expf(s[i] * a.scale - r.lse[i]) : 0.f;
+          d[i] = p[i] * (dp[i] - r.del[i]);
+        }
+        const uint4 pw = split_hi_lo<T>(p), dw = split_hi_lo<T>(d);
+        const frag pa = as_frag<frag>(pw), da = as_frag<frag>(dw);
+#pragma unroll
+        for (int t = 0; t < NH; ++t) {
+          dv[m][t] = Op::mma(pa, as_frag<frag>(make_uint4(ot[t].x, ot[t].y, ot[t].x, ot[t].y)), dv[m][t]);
+          dk[m][t] = Op::mma(da, as_frag<frag>(make_uint4(qt[t].x, qt[t].y, qt[t].x, qt[t].y)), dk[m][t]);
+        }
+        // dS^T with a row per lane (keys 16 m + 4 grp + i), hi then lo
+        const f4 th = Op4::mma(as_frag<frag4>(make_uint2(dw.x, dw.y)), ident, zero4);
+        const f4 tl = Op4::mma(as_frag<frag4>(make_uint2(dw.z, dw.w)), ident, zero4);
+        const frag db = as_frag<frag>(make_uint4(Pack16<T>::pack(th[0], th[1]), Pack16<T>::pack(th[2], th[3]),
+                                                 Pack16<T>::pack(tl[0], tl[1]), Pack16<T>::pack(tl[2], tl[3])));
+#pragma unroll
+        for (int t = 0; t < NH; ++t) {
+          const int dt = hf * NH + t;
+          const uint2 k4 = *reinterpret_cast<const uint2*>(kt + (16 * dt + col) * L.ldt + 16 * m + 4 * grp);
+          dq[t] = Op::mma(as_frag<frag>(make_uint4(k4.x, k4.y, k4.x, k4.y)), db, dq[t]);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // dQ^T tile dt holds d = QL grp + 4 dt + i of row `col`
+      const int rho = (u << 4) + col, rq = rho >> gl, gh = rho & (Gp - 1);
+      if (rq < nreq && gh < a.G) {
+        float vals[QL / 2];
+#pragma unroll
+        for (int t = 0; t < NH; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) vals[4 * t + i] = dq[t][i] * a.scale;
+        store_vals(a.part_dq + ((int64_t)mslot[rq] * a.G + gh) * HD + QL * grp + 4 * hf * NH, vals);
+      }
+    };
+    Rows buf[2];
+    fetch(0, buf[0]);
+    for (int u0 = 0; u0 < units; u0 += 2) {
+      unit(u0, buf[0], buf[1]);
+      if (u0 + 1 < units) unit(u0 + 1, buf[1], buf[0]);
+    }
+
+    // this half of the tile's dK (scaled) and dV partial: key 16 m + 4 grp + i,
+    // d = QL (2 hf + col / 8) + 8 t + col % 8
+    float* part = a.part_dkv + (int64_t)tile * Cp * (2 * HD);
+#pragma unroll
+    for (int m = 0; m < NT; ++m)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = 16 * m + 4 * grp + i;
+        if (key < Cp) {
+#pragma unroll
+          for (int t = 0; t < NH; ++t) {
+            const int d = QL * (2 * hf + (col >> 3)) + 8 * t + (col & 7);
+            part[(int64_t)key * (2 * HD) + d] = dk[m][t][i] * a.scale;
+            part[(int64_t)key * (2 * HD) + HD + d] = dv[m][t][i];
+          }
+        }
+      }
   }
 }
 
@@ -1144,8 +1497,44 @@ int launch_attn_combine(int dtype, const AttnArgs& a, int64_t items, hipStream_t
   return check_launch("attention combine");
 }
 
+template <typename T, int HD, int NT>
+static void launch_bwd_tile(const AttnArgs& a, hipStream_t stream) {
+  const size_t lds = bwd_tile_lds<T, HD>(NT, a.tile).bytes;
+  allow_lds((const void*)attn_bwd_tile_kernel<T, HD, NT>, lds);
+  // two workgroups of two waves fill a CU (one wave per SIMD); all resident
+  PISA_TIMED("attn_bwd", stream, hipLaunchKernelGGL((attn_bwd_tile_kernel<T, HD, NT>), dim3(2 * device_cus()), dim3(128), lds, stream, a));
+}
+
+// The register-tile backward for 16-bit types: blocks of up to 64 keys (128
+// below head dim 128); other shapes take the LDS-staged kernel.
+template <typename T, int HD>
+static bool launch_bwd_tiles(const AttnArgs& a, hipStream_t stream) {
+  if constexpr (sizeof(T) != 2 || HD < 32) {
+    return false;
+  } else {
+    const int nt = (a.C + 31) / 32 * 2;
+    if (bwd_tile_lds<T, HD>(nt, a.tile).bytes > (size_t)device_lds_limit()) return false;
+    if (nt == 2) {
+      launch_bwd_tile<T, HD, 2>(a, stream);
+      return true;
+    }
+    if (nt == 4) {
+      launch_bwd_tile<T, HD, 4>(a, stream);
+      return true;
+    }
+    if constexpr (bwd_tile_fits<HD>(8)) {
+      if (nt == 8) {
+        launch_bwd_tile<T, HD, 8>(a, stream);
+        return true;
+      }
+    }
+    return false;
+  }
+}
+
 template <typename T, int HD>
 static void launch_bwd_kernel(const AttnArgs& a, hipStream_t stream) {
+  if (!PISA_BWD_LDS && tile_path(a) && launch_bwd_tiles<T, HD>(a, stream)) return;
   const int Cp = (a.C + 15) / 16 * 16;
   const size_t lds = bwd_lds(a, sizeof(T));
   allow_lds((const void*)attn_bwd_grouped_kernel<T, HD>, lds);

@@ -326,6 +326,63 @@ struct MfmaOp<float, 1> {
   }
 };
 
+// Two floats as one 32-bit word of 16-bit values (a in the low half), rounded
+// to nearest even, and the floats a word holds.
+typedef float f2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf2v __attribute__((ext_vector_type(2)));
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+
+template <typename T>
+struct Pack16;
+
+template <>
+struct Pack16<bf16_t> {
+  static __device__ __forceinline__ uint32_t pack(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2v){a, b}, bf2v));
+  }
+  static __device__ __forceinline__ float lo(uint32_t w) { return __uint_as_float(w << 16); }
+  static __device__ __forceinline__ float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+};
+
+template <>
+struct Pack16<f16_t> {
+  static __device__ __forceinline__ uint32_t pack(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2v){a, b}, h2v));
+  }
+  static __device__ __forceinline__ float lo(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
+  }
+  static __device__ __forceinline__ float hi(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+  }
+};
+
+// Four floats as a 16x16x32 operand of 16-bit hi + lo pairs: words 0-1 the
+// values rounded to 16 bits (elements 0-3), words 2-3 the rounding errors
+// rounded to 16 bits (elements 4-7).
+template <typename T>
+__device__ __forceinline__ uint4 split_hi_lo(const float (&x)[4]) {
+  typedef Pack16<T> K;
+  const uint32_t h01 = K::pack(x[0], x[1]), h23 = K::pack(x[2], x[3]);
+  const uint32_t l01 = K::pack(x[0] - K::lo(h01), x[1] - K::hi(h01));
+  const uint32_t l23 = K::pack(x[2] - K::lo(h23), x[3] - K::hi(h23));
+  return make_uint4(h01, h23, l01, l23);
+}
+
+template <typename F>
+__device__ __forceinline__ F as_frag(const uint4& u) {
+  F f;
+  __builtin_memcpy(&f, &u, 16);
+  return f;
+}
+
+template <typename F>
+__device__ __forceinline__ F as_frag(const uint2& u) {
+  F f;
+  __builtin_memcpy(&f, &u, 8);
+  return f;
+}
+
 // Copy N fragments from memory with the widest accesses the total size allows
 // (the address must be aligned to that width).
 template <typename F, int N>

@@ -67,6 +67,10 @@ CASES = [
     ("bf16-windows", 2, 1500, 1500, 16, 1, 128, 64, 6, "bf16", True, None),
     # 3 x 8 x 1024 = 24576 (batch, kv head, block) groups: bucketing with global atomics
     ("bf16-wide", 3, 40, 65536, 8, 8, 16, 64, 4, "bf16", True, None),
+    # register-tile backward: fp16 at head dim 128, 128-key blocks at head dim 64, G = 3
+    ("fp16-d128", 1, 384, 384, 8, 2, 128, 64, 4, "fp16", True, None),
+    ("bf16-d64-c128", 1, 512, 640, 8, 2, 64, 128, 3, "bf16", True, None),
+    ("bf16-g3", 2, 200, 260, 6, 2, 64, 64, 3, "bf16", True, None),
 ]
 
 
