@@ -29,6 +29,14 @@ FLAGS = [
 ]
 
 
+# Per-source flags.  The attention kernels keep MFMA results in VGPRs (the
+# backward's accumulators fill the VGPR file; AGPR-form products would copy
+# every S/dP tile out of the accumulation registers before the VALU reads it).
+SOURCE_FLAGS = {
+    "pisa_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
+
 def hipcc():
     path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not os.path.exists(path):
@@ -38,7 +46,8 @@ def hipcc():
 
 def _compile(source, obj_dir, extra):
     obj = os.path.join(obj_dir, os.path.basename(source).replace(".hip", ".o"))
-    cmd = [hipcc(), *FLAGS, *extra, "-c", source, "-o", obj]
+    cmd = [hipcc(), *FLAGS, *SOURCE_FLAGS.get(os.path.basename(source), []), *extra, "-c", source,
+           "-o", obj]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(line for line in proc.stderr.splitlines() if noise not in line)

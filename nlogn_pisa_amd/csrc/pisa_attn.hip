@@ -22,6 +22,8 @@
 // is split across the waves by head-dim tiles and written as a partial per
 // slot, summed per row in slot order.
 
+#include <type_traits>
+
 #include "pisa_device.h"
 #include "pisa_internal.h"
 
@@ -377,6 +379,10 @@ __host__ __device__ inline TileLds tile_lds(int C, int tile) {
 #ifndef PISA_BWD_LDS
 #define PISA_BWD_LDS 0
 #endif
+// 0: the register-tile backward never shares P/dS between waves.
+#ifndef PISA_BWD_SHARE
+#define PISA_BWD_SHARE 1
+#endif
 
 // LDS row of value dv in V^T: dv = (D/4) j + 4 dt + c is stored at row
 // 16 dt + 4 j + c, the row that lane col = 4 j + c reads for dv tile dt, so the
@@ -404,12 +410,13 @@ __device__ void stage_rows(const T* src, int64_t stride, int rows, int Cq, T* ds
 }
 
 // Copy `rows` rows of HD elements transposed into LDS: element (r, c) goes to
-// row vt_row(c), column r; zero from `rows` up to Cq columns.  16-bit values
-// are written two rows per 32-bit word with consecutive lanes on consecutive
-// row pairs.
-template <typename T, int HD>
+// row vt_row(c) (or row c when !VT), column r; zero from `rows` up to Cq
+// columns.  16-bit values are written two rows per 32-bit word with consecutive
+// lanes on consecutive row pairs.
+template <typename T, int HD, bool VT = true>
 __device__ void stage_transposed(const T* src, int64_t stride, int rows, int Cq, T* dst, int ld,
                                  int tid, int nthr) {
+  auto row_of = [](int c) { return VT ? vt_row<HD>(c) : c; };
   constexpr int vec = 16 / (int)sizeof(T);
   constexpr int vpr = HD / vec;
   if constexpr (sizeof(T) == 2) {
@@ -426,7 +433,7 @@ __device__ void stage_transposed(const T* src, int64_t stride, int rows, int Cq,
       if (r + 1 < rows) v1.u = *reinterpret_cast<const uint4*>(src + (int64_t)(r + 1) * stride + c);
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        *reinterpret_cast<uint32_t*>(dst + vt_row<HD>(c + e) * ld + r) =
+        *reinterpret_cast<uint32_t*>(dst + row_of(c + e) * ld + r) =
             (uint32_t)v0.e[e] | ((uint32_t)v1.e[e] << 16);
     }
   } else {
@@ -435,10 +442,10 @@ __device__ void stage_transposed(const T* src, int64_t stride, int rows, int Cq,
       float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
       if (r < rows) v = *reinterpret_cast<const float4*>(src + (int64_t)r * stride + c);
       float* df = reinterpret_cast<float*>(dst);
-      df[vt_row<HD>(c + 0) * ld + r] = v.x;
-      df[vt_row<HD>(c + 1) * ld + r] = v.y;
-      df[vt_row<HD>(c + 2) * ld + r] = v.z;
-      df[vt_row<HD>(c + 3) * ld + r] = v.w;
+      df[row_of(c + 0) * ld + r] = v.x;
+      df[row_of(c + 1) * ld + r] = v.y;
+      df[row_of(c + 2) * ld + r] = v.z;
+      df[row_of(c + 3) * ld + r] = v.w;
     }
   }
 }
@@ -502,7 +509,7 @@ __device__ void fwd_tile_units(const AttnArgs& a, const TileLds& L, const T* ks,
   frag kreg[KR][DS];
 #pragma unroll
   for (int mt = 0; mt < KR; ++mt) {
-    if (KREG && mt < NT) load_frags(ks + (mt * 16 + col) * L.ldk + QL * grp, kreg[mt]);
+    if (KREG && mt < NT) load_row_frags<E>(ks + (mt * 16 + col) * L.ldk + E * grp, kreg[mt]);
     else zero_frags(kreg[mt]);
   }
 
@@ -513,7 +520,7 @@ __device__ void fwd_tile_units(const AttnArgs& a, const TileLds& L, const T* ks,
   auto fetch = [&](int u, frag (&f)[DS]) {
     const int rho = (u << 4) + col, rq = rho >> gl, gh = rho & (Gp - 1);
     const bool ok = u < units && rq < nreq && gh < a.G;
-    load_frags(q + mq[ok ? rq : 0] + (int64_t)(ok ? gh : 0) * HD + QL * grp, f);
+    load_row_frags<E>(q + mq[ok ? rq : 0] + (int64_t)(ok ? gh : 0) * HD + E * grp, f);
   };
   // units wave, wave + nwaves, ...: the next DEPTH units' query rows are in
   // flight while one is computed.  Unit u is computed from `qf`, loads unit u + DEPTH nwaves into `into` (the
@@ -532,7 +539,7 @@ __device__ void fwd_tile_units(const AttnArgs& a, const TileLds& L, const T* ks,
           for (int d = 0; d < DS; ++d) s[mt] = Op::mma(kreg[mt][d], qf[d], s[mt]);
         } else {
           frag kf[DS];
-          load_frags(ks + (mt * 16 + col) * L.ldk + QL * grp, kf);
+          load_row_frags<E>(ks + (mt * 16 + col) * L.ldk + E * grp, kf);
 #pragma unroll
           for (int d = 0; d < DS; ++d) s[mt] = Op::mma(kf[d], qf[d], s[mt]);
         }
@@ -1136,10 +1143,11 @@ __global__ void __launch_bounds__(256) attn_dq_combine_kernel(AttnArgs a, int64_
 // ------------------------------------------------------------------ backward, register tiles
 //
 // 16-bit inputs with D == Dv in {32, 64, 128} and blocks of up to 16 NT keys.
-// One workgroup of two waves per tile.  Both waves take every 16-row unit
-// (row = request x Gp + head) of the tile; wave w owns half w of the head dim
-// of dK, dV and dQ, so the waves never exchange data and each keeps its half
-// of dK and dV of all of the block's keys in registers for the whole tile:
+// One workgroup of W waves (2 or 4) per tile.  Every wave takes every 16-row
+// unit (row = request x Gp + head) of the tile; wave w owns a 1/W slice of the
+// head dim of dK, dV and dQ, so the waves never exchange data and each keeps
+// its slice of dK and dV of all of the block's keys in registers for the whole
+// tile (four slices leave room for two waves per SIMD at head dim 128):
 //   S = Q K^T and dP = dO V^T with a lane per key (rows 4 grp + i),
 //   P = exp(scale S - LSE), dS = P (dP - delta),
 //   dV += P^T dO and dK += dS^T Q, where P^T and dS^T are the A operands exactly
@@ -1178,15 +1186,22 @@ __host__ __device__ inline BwdTileLds bwd_tile_lds(int NT, int tile) {
   return L;
 }
 
-// Whether the register-tile backward serves NT key tiles: a wave's dK and dV
-// take 8 NT (HD / 32) accumulator registers, at most 128 here.
+// Waves per workgroup of the register-tile backward: a half of the head dim
+// per wave.
 template <int HD>
-constexpr bool bwd_tile_fits(int NT) {
-  return NT * (HD / 32) <= 16;
+constexpr int bwd_tile_waves() {
+  return 2;
 }
 
-template <typename T, int HD, int NT>
-__global__ void __launch_bounds__(128, 1) attn_bwd_tile_kernel(AttnArgs a) {
+// Whether the register-tile backward serves NT key tiles: a wave's dK and dV
+// take 8 NT (HD / 16) / W accumulator registers, at most 128 here.
+template <int HD>
+constexpr bool bwd_tile_fits(int NT) {
+  return NT * (HD / 16) * 8 / bwd_tile_waves<HD>() <= 128;
+}
+
+template <typename T, int HD, int NT, int W>
+__global__ void __launch_bounds__(64 * W, W == 4 ? 2 : 1) attn_bwd_tile_kernel(AttnArgs a) {
   typedef QkShape<T, HD> Sh;
   typedef typename Sh::Op Op;     // 16x16x32
   typedef typename Sh::frag frag;
@@ -1194,10 +1209,14 @@ __global__ void __launch_bounds__(128, 1) attn_bwd_tile_kernel(AttnArgs a) {
   typedef typename Op4::frag frag4;
   static_assert(Sh::E == 8, "16-bit types with head dims of at least 32");
   constexpr int QL = Sh::QL, DS = Sh::DS, NDT = Sh::NDT;
-  constexpr int NH = NDT / 2;     // this wave's 16-wide tiles of dK/dV and of dQ^T
+  constexpr int NS = 2 * DS / W;  // this wave's 16-wide tiles of dK/dV
+  constexpr int NQ = NDT / W;     // this wave's 16-wide tiles of dQ^T
+  static_assert(NS >= 1 && NQ >= 1, "a head-dim slice per wave");
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int tid = threadIdx.x, lane = tid & 63;
-  const int hf = tid >> 6;        // head-dim half
+  const int w = tid >> 6;         // head-dim slice
+  const int hw = w & 1;           // the selection fragment's half
+  const int dsb = (w >> 1) * NS;  // first ds of the slice
   const BwdTileLds L = bwd_tile_lds<T, HD>(NT, a.tile);
   T* ks = reinterpret_cast<T*>(smem + L.ks);
   T* vs = reinterpret_cast<T*>(smem + L.vs);
@@ -1215,13 +1234,13 @@ __global__ void __launch_bounds__(128, 1) attn_bwd_tile_kernel(AttnArgs a) {
   const f4 zero4 = f4{0.f, 0.f, 0.f, 0.f};
 
   // Selection fragment: B[k][n] = 1 iff the d of reduction index k (lane group
-  // grp, element e: d = QL grp + 8 ds + e) is column n's
-  // d = QL (2 hf + n / 8) + 8 ds + n % 8 (the same for every ds), so output
-  // tile ds of a wave covers d in [2 hf QL, 2 hf QL + 2 QL).  Identity of the
-  // 16x16x16 product: I[k][n] = 1 iff 4 grp + e == n.
+  // grp, element e: d = 32 ds + 8 grp + e) is column n's d = 32 ds + 16 hw + n
+  // (the same for every ds); the wave's dK/dV tiles are ds = dsb .. dsb + NS - 1
+  // of its half hw.  Identity of the 16x16x16 product: I[k][n] = 1 iff
+  // 4 grp + e == n.
   frag sel;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) Op::set(sel, e, grp == 2 * hf + (col >> 3) && e == (col & 7) ? 1.f : 0.f);
+  for (int e = 0; e < 8; ++e) Op::set(sel, e, grp == 2 * hw + (col >> 3) && e == (col & 7) ? 1.f : 0.f);
   frag4 ident;
 #pragma unroll
   for (int e = 0; e < 4; ++e) Op4::set(ident, e, 4 * grp + e == col ? 1.f : 0.f);
@@ -1241,7 +1260,7 @@ __global__ void __launch_bounds__(128, 1) attn_bwd_tile_kernel(AttnArgs a) {
     const int nreq = min(a.tile, a.counts[g] - start);
     const int rows = (int)min((int64_t)a.C, (int64_t)a.N - blk * a.C);
     const int32_t* reqs = a.tile_req + (int64_t)tile * a.tile;
-    __syncthreads();  // both waves are done with the previous tile's LDS
+    __syncthreads();  // every wave is done with the previous tile's LDS
     for (int i = tid; i < nreq; i += blockDim.x) {
       const int32_t slot = reqs[i];
       const RowInfo ri = row_info(a, slot);
@@ -1257,15 +1276,15 @@ __global__ void __launch_bounds__(128, 1) attn_bwd_tile_kernel(AttnArgs a) {
                     (int64_t)h * HD;
       stage_rows<T, HD>(kb, a.k_token, rows, L.Cq, ks, L.ldk, tid, blockDim.x);
       stage_rows<T, HD>(vb, a.v_token, rows, L.Cq, vs, L.ldk, tid, blockDim.x);
-      stage_transposed<T, HD>(kb, a.k_token, rows, L.Cq, kt, L.ldt, tid, blockDim.x);
+      stage_transposed<T, HD, false>(kb, a.k_token, rows, L.Cq, kt, L.ldt, tid, blockDim.x);
     }
     __syncthreads();
 
-    f4 dk[NT][NH], dv[NT][NH];
+    f4 dk[NT][NS], dv[NT][NS];
 #pragma unroll
     for (int m = 0; m < NT; ++m)
 #pragma unroll
-      for (int t = 0; t < NH; ++t) dk[m][t] = dv[m][t] = zero4;
+      for (int t = 0; t < NS; ++t) dk[m][t] = dv[m][t] = zero4;
 
     const int units = (nreq * Gp + 15) >> 4;
     // Rows of unit u: Q and dO of row `col` as A fragments, LSE and delta of
@@ -1276,8 +1295,8 @@ __global__ void __launch_bounds__(128, 1) attn_bwd_tile_kernel(AttnArgs a) {
         const int rho = (u << 4) + col, rq = rho >> gl, gh = rho & (Gp - 1);
         const bool ok = u < units && rq < nreq && gh < a.G;
         const int rr = ok ? rq : 0, hh = ok ? gh : 0;
-        load_frags(qg + mq[rr] + (int64_t)hh * HD + QL * grp, r.q);
-        load_frags(og + (mo[rr] + hh) * HD + QL * grp, r.o);
+        load_row_frags<8>(qg + mq[rr] + (int64_t)hh * HD + 8 * grp, r.q);
+        load_row_frags<8>(og + (mo[rr] + hh) * HD + 8 * grp, r.o);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -1290,16 +1309,20 @@ __global__ void __launch_bounds__(128, 1) attn_bwd_tile_kernel(AttnArgs a) {
     };
     auto unit = [&](int u, Rows& r, Rows& into) {
       fetch(u + 1, into);
-      // this half of Q and dO with a column per lane (rows 4 grp + e), as
+      // this slice of Q and dO with a column per lane (rows 4 grp + e), as
       // 16-bit words; the exact values of the selection products
-      uint2 qt[NH], ot[NH];
+      uint2 qt[NS], ot[NS];
+      auto turn = [&](auto first) {
 #pragma unroll
-      for (int ds = 0; ds < DS; ++ds) {
-        const f4 cq = Op::mma(r.q[ds], sel, zero4);
-        const f4 co = Op::mma(r.o[ds], sel, zero4);
-        qt[ds] = make_uint2(Pack16<T>::pack(cq[0], cq[1]), Pack16<T>::pack(cq[2], cq[3]));
-        ot[ds] = make_uint2(Pack16<T>::pack(co[0], co[1]), Pack16<T>::pack(co[2], co[3]));
-      }
+        for (int j = 0; j < NS; ++j) {
+          const f4 cq = Op::mma(r.q[decltype(first)::value + j], sel, zero4);
+          const f4 co = Op::mma(r.o[decltype(first)::value + j], sel, zero4);
+          qt[j] = make_uint2(Pack16<T>::pack(cq[0], cq[1]), Pack16<T>::pack(cq[2], cq[3]));
+          ot[j] = make_uint2(Pack16<T>::pack(co[0], co[1]), Pack16<T>::pack(co[2], co[3]));
+        }
+      };
+      if (dsb == 0) turn(std::integral_constant<int, 0>{});
+      else turn(std::integral_constant<int, (NS < DS ? NS : 0)>{});
       // visible keys of rows 4 grp + i: key < lim[i]
       int lim[4];
 #pragma unroll
@@ -1311,9 +1334,9 @@ __global__ void __launch_bounds__(128, 1) attn_bwd_tile_kernel(AttnArgs a) {
           lim[i] = (int)min((int64_t)rows, last);
         }
       }
-      f4 dq[NH];
+      f4 dq[NQ];
 #pragma unroll
-      for (int t = 0; t < NH; ++t) dq[t] = zero4;
+      for (int t = 0; t < NQ; ++t) dq[t] = zero4;
 #pragma unroll
       for (int m = 0; m < NT; ++m) {
         __builtin_amdgcn_sched_barrier(0);
@@ -1322,8 +1345,8 @@ __global__ void __launch_bounds__(128, 1) attn_bwd_tile_kernel(AttnArgs a) {
 #pragma unroll
         for (int ds = 0; ds < DS; ++ds) {
           frag kf[1], vf[1];
-          load_frags(ks + key * L.ldk + QL * grp + 8 * ds, kf);
-          load_frags(vs + key * L.ldk + QL * grp + 8 * ds, vf);
+          load_frags(ks + key * L.ldk + 8 * grp + 32 * ds, kf);
+          load_frags(vs + key * L.ldk + 8 * grp + 32 * ds, vf);
           s = Op::mma(r.q[ds], kf[0], s);
           dp = Op::mma(r.o[ds], vf[0], dp);
         }
@@ -1336,7 +1359,7 @@ __global__ void __launch_bounds__(128, 1) attn_bwd_tile_kernel(AttnArgs a) {
         const uint4 pw = split_hi_lo<T>(p), dw = split_hi_lo<T>(d);
         const frag pa = as_frag<frag>(pw), da = as_frag<frag>(dw);
 #pragma unroll
-        for (int t = 0; t < NH; ++t) {
+        for (int t = 0; t < NS; ++t) {
           dv[m][t] = Op::mma(pa, as_frag<frag>(make_uint4(ot[t].x, ot[t].y, ot[t].x, ot[t].y)), dv[m][t]);
           dk[m][t] = Op::mma(da, as_frag<frag>(make_uint4(qt[t].x, qt[t].y, qt[t].x, qt[t].y)), dk[m][t]);
         }
@@ -1346,22 +1369,22 @@ __global__ void __launch_bounds__(128, 1) attn_bwd_tile_kernel(AttnArgs a) {
         const frag db = as_frag<frag>(make_uint4(Pack16<T>::pack(th[0], th[1]), Pack16<T>::pack(th[2], th[3]),
                                                  Pack16<T>::pack(tl[0], tl[1]), Pack16<T>::pack(tl[2], tl[3])));
 #pragma unroll
-        for (int t = 0; t < NH; ++t) {
-          const int dt = hf * NH + t;
+        for (int t = 0; t < NQ; ++t) {
+          const int dt = w * NQ + t;
           const uint2 k4 = *reinterpret_cast<const uint2*>(kt + (16 * dt + col) * L.ldt + 16 * m + 4 * grp);
           dq[t] = Op::mma(as_frag<frag>(make_uint4(k4.x, k4.y, k4.x, k4.y)), db, dq[t]);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
-      // dQ^T tile dt holds d = QL grp + 4 dt + i of row `col`
+      // dQ^T tile dt holds d = 16 dt + 4 grp + i of row `col` (K^T rows are
+      // d): a wave writes whole 64-byte runs of the row, its d in one piece
       const int rho = (u << 4) + col, rq = rho >> gl, gh = rho & (Gp - 1);
       if (rq < nreq && gh < a.G) {
-        float vals[QL / 2];
+        float* dst = a.part_dq + ((int64_t)mslot[rq] * a.G + gh) * HD + 4 * grp;
 #pragma unroll
-        for (int t = 0; t < NH; ++t)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) vals[4 * t + i] = dq[t][i] * a.scale;
-        store_vals(a.part_dq + ((int64_t)mslot[rq] * a.G + gh) * HD + QL * grp + 4 * hf * NH, vals);
+        for (int t = 0; t < NQ; ++t)
+          *reinterpret_cast<float4*>(dst + 16 * (w * NQ + t)) =
+              make_float4(dq[t][0] * a.scale, dq[t][1] * a.scale, dq[t][2] * a.scale, dq[t][3] * a.scale);
       }
     };
     Rows buf[2];
@@ -1371,8 +1394,8 @@ __global__ void __launch_bounds__(128, 1) attn_bwd_tile_kernel(AttnArgs a) {
       if (u0 + 1 < units) unit(u0 + 1, buf[1], buf[0]);
     }
 
-    // this half of the tile's dK (scaled) and dV partial: key 16 m + 4 grp + i,
-    // d = QL (2 hf + col / 8) + 8 t + col % 8
+    // this slice of the tile's dK (scaled) and dV partial: key 16 m + 4 grp + i,
+    // d = 32 (dsb + t) + 16 hw + col
     float* part = a.part_dkv + (int64_t)tile * Cp * (2 * HD);
 #pragma unroll
     for (int m = 0; m < NT; ++m)
@@ -1381,8 +1404,275 @@ __global__ void __launch_bounds__(128, 1) attn_bwd_tile_kernel(AttnArgs a) {
         const int key = 16 * m + 4 * grp + i;
         if (key < Cp) {
 #pragma unroll
-          for (int t = 0; t < NH; ++t) {
-            const int d = QL * (2 * hf + (col >> 3)) + 8 * t + (col & 7);
+          for (int t = 0; t < NS; ++t) {
+            const int d = 32 * (dsb + t) + 16 * hw + col;
+            part[(int64_t)key * (2 * HD) + d] = dk[m][t][i] * a.scale;
+            part[(int64_t)key * (2 * HD) + HD + d] = dv[m][t][i];
+          }
+        }
+      }
+  }
+}
+
+// ------------------------------------------------------------------ backward, shared P/dS
+//
+// The register-tile backward with four waves that compute each key tile's
+// P and dS once: in a unit, wave w computes S, dP, P, dS and dS^T of key tiles
+// w, w + 4, ... and leaves their 16-bit hi + lo fragments in LDS; after a
+// barrier every wave applies all key tiles to its quarter of the head dim of
+// dK, dV (registers, whole tile) and dQ (the slot's partial), and a second
+// barrier frees the exchange for the next unit.  The unit's Q and dO rows are
+// loaded once per workgroup (each wave a quarter of the rows, 16 contiguous
+// bytes per lane) into LDS during the previous unit.  Same products and operand
+// layouts as attn_bwd_tile_kernel; two workgroups fill a CU (two waves per SIMD).
+
+template <typename T, int HD>
+__host__ __device__ inline size_t bwd_share_lds(int NT, int tile) {
+  // tile staging, the P/dS exchange [NT][3][64] uint4, Q and dO rows [2][16][HD + 8]
+  return bwd_tile_lds<T, HD>(NT, tile).bytes + (size_t)NT * 64 * 48 +
+         (size_t)2 * 16 * (HD + 16 / sizeof(T)) * sizeof(T);
+}
+
+template <typename T, int HD, int NT>
+__global__ void __launch_bounds__(256, 2) attn_bwd_share_kernel(AttnArgs a) {
+  typedef QkShape<T, HD> Sh;
+  typedef typename Sh::Op Op;     // 16x16x32
+  typedef typename Sh::frag frag;
+  typedef MfmaOp<T, 4> Op4;       // 16x16x16 (the identity product)
+  typedef typename Op4::frag frag4;
+  static_assert(Sh::E == 8, "16-bit types with head dims of at least 32");
+  constexpr int W = 4;
+  constexpr int QL = Sh::QL, DS = Sh::DS, NDT = Sh::NDT;
+  constexpr int NS = 2 * DS / W;  // this wave's 16-wide tiles of dK/dV
+  constexpr int NQ = NDT / W;     // this wave's 16-wide tiles of dQ^T
+  constexpr int MW = (NT + W - 1) / W;  // key tiles a wave scores
+  static_assert(NS >= 1 && NQ >= 1, "a head-dim quarter per wave");
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = tid >> 6;         // head-dim quarter
+  const int hw = w & 1;           // the selection fragment's half
+  const int dsb = (w >> 1) * NS;  // first ds of the quarter
+  const BwdTileLds L = bwd_tile_lds<T, HD>(NT, a.tile);
+  T* ks = reinterpret_cast<T*>(smem + L.ks);
+  T* vs = reinterpret_cast<T*>(smem + L.vs);
+  T* kt = reinterpret_cast<T*>(smem + L.kt);
+  int64_t* mq = reinterpret_cast<int64_t*>(smem + L.mq);
+  int64_t* mo = reinterpret_cast<int64_t*>(smem + L.mo);
+  int64_t* mpos = reinterpret_cast<int64_t*>(smem + L.mpos);
+  int32_t* mslot = reinterpret_cast<int32_t*>(smem + L.mslot);
+  uint4* xch = reinterpret_cast<uint4*>(smem + L.bytes);  // [NT][3][64]: P, dS, dS^T
+  constexpr int LDQ = HD + 16 / (int)sizeof(T);
+  T* qo = reinterpret_cast<T*>(smem + L.bytes + (size_t)NT * 64 * 48);  // [2][16][LDQ]: Q, dO
+  const int col = lane & 15, grp = lane >> 4;
+  const int Gp = a.Gp, gl = 31 - __clz(Gp);
+  const int Cp = (a.C + 15) / 16 * 16;
+  const int Hq = a.Hkv * a.G;
+  const T* qg = static_cast<const T*>(a.q);
+  const T* og = static_cast<const T*>(a.dout);
+  const f4 zero4 = f4{0.f, 0.f, 0.f, 0.f};
+
+  // selection and identity fragments as in attn_bwd_tile_kernel
+  frag sel;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) Op::set(sel, e, grp == 2 * hw + (col >> 3) && e == (col & 7) ? 1.f : 0.f);
+  frag4 ident;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) Op4::set(ident, e, 4 * grp + e == col ? 1.f : 0.f);
+
+  static_assert(HD == 128, "rows of 16 lanes x 16 bytes");
+
+  const int ntiles = *a.num_tiles;
+  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int g = a.tile_group[tile];
+    const int64_t blk = g % a.M0;
+    const int bh = g / a.M0;
+    const int h = bh % a.Hkv, b = bh / a.Hkv;
+    const int start = (tile - a.tile_off[g]) * a.tile;
+    const int nreq = min(a.tile, a.counts[g] - start);
+    const int rows = (int)min((int64_t)a.C, (int64_t)a.N - blk * a.C);
+    const int32_t* reqs = a.tile_req + (int64_t)tile * a.tile;
+    __syncthreads();  // every wave is done with the previous tile's LDS
+    for (int i = tid; i < nreq; i += blockDim.x) {
+      const int32_t slot = reqs[i];
+      const RowInfo ri = row_info(a, slot);
+      mq[i] = (int64_t)ri.b * a.q_batch + (int64_t)ri.t * a.q_token + (int64_t)h * a.G * HD;
+      mo[i] = ((int64_t)ri.b * a.T + ri.t) * Hq + (int64_t)h * a.G;
+      mpos[i] = ri.pos;
+      mslot[i] = slot;
+    }
+    {
+      const T* kb = static_cast<const T*>(a.k) + (int64_t)b * a.k_batch + blk * a.C * a.k_token +
+                    (int64_t)h * HD;
+      const T* vb = static_cast<const T*>(a.v) + (int64_t)b * a.v_batch + blk * a.C * a.v_token +
+                    (int64_t)h * HD;
+      stage_rows<T, HD>(kb, a.k_token, rows, L.Cq, ks, L.ldk, tid, blockDim.x);
+      stage_rows<T, HD>(vb, a.v_token, rows, L.Cq, vs, L.ldk, tid, blockDim.x);
+      stage_transposed<T, HD, false>(kb, a.k_token, rows, L.Cq, kt, L.ldt, tid, blockDim.x);
+    }
+    __syncthreads();
+
+    f4 dk[NT][NS], dv[NT][NS];
+#pragma unroll
+    for (int m = 0; m < NT; ++m)
+#pragma unroll
+      for (int t = 0; t < NS; ++t) dk[m][t] = dv[m][t] = zero4;
+
+    const int units = (nreq * Gp + 15) >> 4;
+    // Rows of a unit in flight, two sets by unit parity: Q and dO of row
+    // 4 w + grp, elements 8 col .. 8 col + 7 (each wave a quarter of the rows),
+    // LSE and delta of rows 4 grp + i.
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    u32x4 nq[2], no[2];
+    float nl[2][4], nd[2][4];
+    auto fetch = [&](int u, auto P) {
+      constexpr int p = decltype(P)::value;
+      {
+        const int rho = (u << 4) + 4 * w + grp, rq = rho >> gl, gh = rho & (Gp - 1);
+        const bool ok = u < units && rq < nreq && gh < a.G;
+        const int rr = ok ? rq : 0, hh = ok ? gh : 0;
+        nq[p] = *reinterpret_cast<const u32x4*>(qg + mq[rr] + (int64_t)hh * HD + 8 * col);
+        no[p] = *reinterpret_cast<const u32x4*>(og + (mo[rr] + hh) * HD + 8 * col);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int rho = (u << 4) + 4 * grp + i, rq = rho >> gl, gh = rho & (Gp - 1);
+        const bool ok = u < units && rq < nreq && gh < a.G;
+        const int64_t orow = mo[ok ? rq : 0] + (ok ? gh : 0);
+        nl[p][i] = a.lse[orow];
+        nd[p][i] = a.delta[orow];
+      }
+    };
+    auto put = [&](auto P) {
+      constexpr int p = decltype(P)::value;
+      *reinterpret_cast<u32x4*>(qo + (4 * w + grp) * LDQ + 8 * col) = nq[p];
+      *reinterpret_cast<u32x4*>(qo + (16 + 4 * w + grp) * LDQ + 8 * col) = no[p];
+    };
+    struct Rows {
+      frag q[DS], o[DS];
+      float lse[4], del[4];
+    };
+    // unit u with its LSE/delta in set P; loads unit u + 1 into the other set
+    auto unit = [&](int u, auto P) {
+      constexpr int p = decltype(P)::value;
+      typedef std::integral_constant<int, 1 - p> Q;
+      // this unit's rows (put in LDS before the previous unit's last barrier)
+      Rows r;
+      load_row_frags<8>(qo + col * LDQ + 8 * grp, r.q);
+      load_row_frags<8>(qo + (16 + col) * LDQ + 8 * grp, r.o);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        r.lse[i] = nl[p][i];
+        r.del[i] = nd[p][i];
+      }
+      fetch(u + 1, Q{});
+      // scores of this wave's key tiles: P, dS (hi + lo) and dS^T into the exchange
+      int lim[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int rho = (u << 4) + 4 * grp + i, rq = rho >> gl, gh = rho & (Gp - 1);
+        lim[i] = 0;
+        if (rq < nreq && gh < a.G) {
+          const int64_t last = a.causal ? mpos[rq] - blk * a.C + 1 : (int64_t)rows;
+          lim[i] = (int)min((int64_t)rows, last);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < MW; ++j) {
+        const int m = w + W * j;
+        if (m < NT) {
+          const int key = 16 * m + col;
+          f4 s = zero4, dp = zero4;
+#pragma unroll
+          for (int ds = 0; ds < DS; ++ds) {
+            frag kf[1], vf[1];
+            load_frags(ks + key * L.ldk + 8 * grp + 32 * ds, kf);
+            load_frags(vs + key * L.ldk + 8 * grp + 32 * ds, vf);
+            s = Op::mma(r.q[ds], kf[0], s);
+            dp = Op::mma(r.o[ds], vf[0], dp);
+          }
+          float p[4], d[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            p[i] = key < lim[i] ? __expf(s[i] * a.scale - r.lse[i]) : 0.f;
+            d[i] = p[i] * (dp[i] - r.del[i]);
+          }
+          const uint4 pw = split_hi_lo<T>(p), dw = split_hi_lo<T>(d);
+          const f4 th = Op4::mma(as_frag<frag4>(make_uint2(dw.x, dw.y)), ident, zero4);
+          const f4 tl = Op4::mma(as_frag<frag4>(make_uint2(dw.z, dw.w)), ident, zero4);
+          const uint4 tw = make_uint4(Pack16<T>::pack(th[0], th[1]), Pack16<T>::pack(th[2], th[3]),
+                                      Pack16<T>::pack(tl[0], tl[1]), Pack16<T>::pack(tl[2], tl[3]));
+          xch[(m * 3 + 0) * 64 + lane] = pw;
+          xch[(m * 3 + 1) * 64 + lane] = dw;
+          xch[(m * 3 + 2) * 64 + lane] = tw;
+        }
+      }
+      // this quarter of Q and dO with a column per lane (rows 4 grp + e)
+      uint2 qt[NS], ot[NS];
+      auto turn = [&](auto first) {
+#pragma unroll
+        for (int j = 0; j < NS; ++j) {
+          const f4 cq = Op::mma(r.q[decltype(first)::value + j], sel, zero4);
+          const f4 co = Op::mma(r.o[decltype(first)::value + j], sel, zero4);
+          qt[j] = make_uint2(Pack16<T>::pack(cq[0], cq[1]), Pack16<T>::pack(cq[2], cq[3]));
+          ot[j] = make_uint2(Pack16<T>::pack(co[0], co[1]), Pack16<T>::pack(co[2], co[3]));
+        }
+      };
+      if (dsb == 0) turn(std::integral_constant<int, 0>{});
+      else turn(std::integral_constant<int, (NS < DS ? NS : 0)>{});
+      __syncthreads();  // every key tile's P and dS is in the exchange; this unit's rows are read
+      put(Q{});
+      f4 dq[NQ];
+#pragma unroll
+      for (int t = 0; t < NQ; ++t) dq[t] = zero4;
+#pragma unroll
+      for (int m = 0; m < NT; ++m) {
+        const frag pa = as_frag<frag>(xch[(m * 3 + 0) * 64 + lane]);
+        const frag da = as_frag<frag>(xch[(m * 3 + 1) * 64 + lane]);
+        const frag db = as_frag<frag>(xch[(m * 3 + 2) * 64 + lane]);
+#pragma unroll
+        for (int t = 0; t < NS; ++t) {
+          dv[m][t] = Op::mma(pa, as_frag<frag>(make_uint4(ot[t].x, ot[t].y, ot[t].x, ot[t].y)), dv[m][t]);
+          dk[m][t] = Op::mma(da, as_frag<frag>(make_uint4(qt[t].x, qt[t].y, qt[t].x, qt[t].y)), dk[m][t]);
+        }
+#pragma unroll
+        for (int t = 0; t < NQ; ++t) {
+          const int dt = w * NQ + t;
+          const uint2 k4 = *reinterpret_cast<const uint2*>(kt + (16 * dt + col) * L.ldt + 16 * m + 4 * grp);
+          dq[t] = Op::mma(as_frag<frag>(make_uint4(k4.x, k4.y, k4.x, k4.y)), db, dq[t]);
+        }
+      }
+      const int rho = (u << 4) + col, rq = rho >> gl, gh = rho & (Gp - 1);
+      if (rq < nreq && gh < a.G) {
+        float* dst = a.part_dq + ((int64_t)mslot[rq] * a.G + gh) * HD + 4 * grp;
+#pragma unroll
+        for (int t = 0; t < NQ; ++t)
+          *reinterpret_cast<float4*>(dst + 16 * (w * NQ + t)) =
+              make_float4(dq[t][0] * a.scale, dq[t][1] * a.scale, dq[t][2] * a.scale, dq[t][3] * a.scale);
+      }
+      __syncthreads();  // the exchange is free and the next unit's rows are in LDS
+    };
+    typedef std::integral_constant<int, 0> P0;
+    typedef std::integral_constant<int, 1> P1;
+    fetch(0, P0{});
+    put(P0{});
+    __syncthreads();
+    for (int u0 = 0; u0 < units; u0 += 2) {
+      unit(u0, P0{});
+      if (u0 + 1 < units) unit(u0 + 1, P1{});
+    }
+
+    // this quarter of the tile's dK (scaled) and dV partial: key 16 m + 4 grp + i,
+    // d = 32 (dsb + t) + 16 hw + col
+    float* part = a.part_dkv + (int64_t)tile * Cp * (2 * HD);
+#pragma unroll
+    for (int m = 0; m < NT; ++m)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = 16 * m + 4 * grp + i;
+        if (key < Cp) {
+#pragma unroll
+          for (int t = 0; t < NS; ++t) {
+            const int d = 32 * (dsb + t) + 16 * hw + col;
             part[(int64_t)key * (2 * HD) + d] = dk[m][t][i] * a.scale;
             part[(int64_t)key * (2 * HD) + HD + d] = dv[m][t][i];
           }
@@ -1498,11 +1788,20 @@ int launch_attn_combine(int dtype, const AttnArgs& a, int64_t items, hipStream_t
 }
 
 template <typename T, int HD, int NT>
+static void launch_bwd_share(const AttnArgs& a, hipStream_t stream) {
+  const size_t lds = bwd_share_lds<T, HD>(NT, a.tile);
+  allow_lds((const void*)attn_bwd_share_kernel<T, HD, NT>, lds);
+  // two workgroups per CU, all resident
+  PISA_TIMED("attn_bwd", stream, hipLaunchKernelGGL((attn_bwd_share_kernel<T, HD, NT>), dim3(2 * device_cus()), dim3(256), lds, stream, a));
+}
+
+template <typename T, int HD, int NT>
 static void launch_bwd_tile(const AttnArgs& a, hipStream_t stream) {
+  constexpr int W = bwd_tile_waves<HD>();
   const size_t lds = bwd_tile_lds<T, HD>(NT, a.tile).bytes;
-  allow_lds((const void*)attn_bwd_tile_kernel<T, HD, NT>, lds);
-  // two workgroups of two waves fill a CU (one wave per SIMD); all resident
-  PISA_TIMED("attn_bwd", stream, hipLaunchKernelGGL((attn_bwd_tile_kernel<T, HD, NT>), dim3(2 * device_cus()), dim3(128), lds, stream, a));
+  allow_lds((const void*)attn_bwd_tile_kernel<T, HD, NT, W>, lds);
+  // two workgroups per CU, all resident
+  PISA_TIMED("attn_bwd", stream, hipLaunchKernelGGL((attn_bwd_tile_kernel<T, HD, NT, W>), dim3(2 * device_cus()), dim3(64 * W), lds, stream, a));
 }
 
 // The register-tile backward for 16-bit types: blocks of up to 64 keys (128
@@ -1514,6 +1813,14 @@ static bool launch_bwd_tiles(const AttnArgs& a, hipStream_t stream) {
   } else {
     const int nt = (a.C + 31) / 32 * 2;
     if (bwd_tile_lds<T, HD>(nt, a.tile).bytes > (size_t)device_lds_limit()) return false;
+    if constexpr (HD == 128) {
+      // shared P/dS when two workgroups fit a CU
+      if (PISA_BWD_SHARE && nt <= 4 && 2 * bwd_share_lds<T, HD>(nt, a.tile) <= (size_t)device_lds_limit()) {
+        if (nt == 2) launch_bwd_share<T, HD, 2>(a, stream);
+        else launch_bwd_share<T, HD, 4>(a, stream);
+        return true;
+      }
+    }
     if (nt == 2) {
       launch_bwd_tile<T, HD, 2>(a, stream);
       return true;

@@ -406,6 +406,28 @@ __device__ __forceinline__ void load_frags(const void* p, F (&f)[N]) {
   }
 }
 
+// N fragments of E elements of one row in the MFMA reduction order
+// k = 4 E s + E grp + e (fragment s, lane group grp, element e): `p` points at
+// element E grp of the row.  Each load instruction of a wave then reads 4 E
+// contiguous elements of every row it touches (the four lane groups side by
+// side), so a 16-row gather costs one memory segment per row and instruction.
+template <int E, typename F, int N, typename T>
+__device__ __forceinline__ void load_row_frags(const T* p, F (&f)[N]) {
+#pragma unroll
+  for (int s = 0; s < N; ++s) {
+    if constexpr (sizeof(F) == 16) {
+      const uint4 t = *reinterpret_cast<const uint4*>(p + 4 * E * s);
+      __builtin_memcpy(&f[s], &t, 16);
+    } else if constexpr (sizeof(F) == 8) {
+      const uint2 t = *reinterpret_cast<const uint2*>(p + 4 * E * s);
+      __builtin_memcpy(&f[s], &t, 8);
+    } else {
+      const uint32_t t = *reinterpret_cast<const uint32_t*>(p + 4 * E * s);
+      __builtin_memcpy(&f[s], &t, 4);
+    }
+  }
+}
+
 template <typename F, int N>
 __device__ __forceinline__ void zero_frags(F (&f)[N]) {
   __builtin_memset(f, 0, sizeof(f));

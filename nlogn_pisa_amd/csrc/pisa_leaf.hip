@@ -211,7 +211,7 @@ __global__ void __launch_bounds__(256, (NTM <= 4 ? PISA_LEAF_WAVES : 2)) leaf_ti
   typedef QkShape<T, HD, NTM> S;
   typedef typename S::Op Op;
   typedef typename S::frag frag;
-  constexpr int QL = S::QL, DS = S::DS;
+  constexpr int E = S::E, QL = S::QL, DS = S::DS;
   constexpr int DEPTH = PISA_LEAF_DEPTH;
   // key-block A fragments held in registers when they take at most 64 VGPRs
   constexpr bool KREG = PISA_LEAF_KREG && NTM <= 4 && NTM * QL * sizeof(T) <= 256;
@@ -273,7 +273,7 @@ __global__ void __launch_bounds__(256, (NTM <= 4 ? PISA_LEAF_WAVES : 2)) leaf_ti
     frag kreg[KR][DS];
 #pragma unroll
     for (int mt = 0; mt < KR; ++mt) {
-      if (KREG && mt < NT) load_frags(ks + (mt * 16 + col) * L.ldk + QL * grp, kreg[mt]);
+      if (KREG && mt < NT) load_row_frags<E>(ks + (mt * 16 + col) * L.ldk + E * grp, kreg[mt]);
       else zero_frags(kreg[mt]);
     }
 
@@ -286,7 +286,7 @@ __global__ void __launch_bounds__(256, (NTM <= 4 ? PISA_LEAF_WAVES : 2)) leaf_ti
       const int rho = (((r << nsl) + j) << 4) + col;
       const int rq = rho >> gl, gh = rho & (Gp - 1);
       const bool ok = r < items && rq < nreq && gh < a.G;
-      load_frags(q + mq[ok ? rq : 0] + (int64_t)(ok ? gh : 0) * HD + QL * grp, f);
+      load_row_frags<E>(q + mq[ok ? rq : 0] + (int64_t)(ok ? gh : 0) * HD + E * grp, f);
     };
     // this wave's units k = 0, 1, ...: item wave + nwaves (k >> nsl), unit k & (nsub - 1);
     // query rows of the next DEPTH units are in flight while unit k is scored
@@ -315,7 +315,7 @@ __global__ void __launch_bounds__(256, (NTM <= 4 ? PISA_LEAF_WAVES : 2)) leaf_ti
             for (int d = 0; d < DS; ++d) s[mt] = Op::mma(kreg[mt][d], cur[d], s[mt]);
           } else {
             frag kf[DS];
-            load_frags(ks + (mt * 16 + col) * L.ldk + QL * grp, kf);
+            load_row_frags<E>(ks + (mt * 16 + col) * L.ldk + E * grp, kf);
 #pragma unroll
             for (int d = 0; d < DS; ++d) s[mt] = Op::mma(kf[d], cur[d], s[mt]);
           }

@@ -362,7 +362,7 @@ __global__ void __launch_bounds__(64) route_grouped_kernel(RouteArgs a) {
   typedef QkShape<T, HD> S;
   typedef typename S::Op Op;
   typedef typename S::frag frag;
-  constexpr int QL = S::QL, DS = S::DS;
+  constexpr int E = S::E, QL = S::QL, DS = S::DS;
   __shared__ int ids_s[kMaxWidth];
   __shared__ float sc_s[kMaxWidth];
   __shared__ int list_s[kMaxWidth];
@@ -385,12 +385,12 @@ __global__ void __launch_bounds__(64) route_grouped_kernel(RouteArgs a) {
   const int R = own ? 1 : a.branching;             // support rows per candidate (<= 8)
   const int cpt = 16 / R;                          // candidates per 16 support rows
 
-  // Q^T: lane (grp, col) holds head col's dimensions [QL grp, QL grp + QL)
+  // Q^T: lane (grp, col) holds head col's dimensions 4 E s + E grp + e of step s
   frag qb[DS];
   if (col < a.G)
-    load_frags(static_cast<const T*>(a.q) + b * a.q_batch + t * a.q_token +
-                   ((int64_t)h * a.G + col) * HD + QL * grp,
-               qb);
+    load_row_frags<E>(static_cast<const T*>(a.q) + b * a.q_batch + t * a.q_token +
+                          ((int64_t)h * a.G + col) * HD + E * grp,
+                      qb);
   else
     zero_frags(qb);
 
@@ -445,7 +445,7 @@ __global__ void __launch_bounds__(64) route_grouped_kernel(RouteArgs a) {
       const int id = ci < nlist ? ids_s[list_s[ci]] : 0;
       const int64_t r = (int64_t)id * R + child;
       const bool ok = ci < nlist && r < len;
-      load_frags(base + (ok ? r : 0) * rstride + QL * grp, f);
+      load_row_frags<E>(base + (ok ? r : 0) * rstride + E * grp, f);
     };
     // tile mt: scored from `xf`, loads tile mt + 1 into `xn`; the two buffers
     // alternate by unrolling, never by copies
