@@ -333,20 +333,23 @@ __global__ void __launch_bounds__(64) attn_fwd_direct_kernel(AttnArgs a, int64_t
 // computed once per tile into LDS, and each wave loads the next unit's query
 // rows while it computes the current one.
 
-// LDS of one tile: K block [Cq][HD + PAD], V^T [HD][Cq + PAD], then per request
-// the query row offset (int64), position (int64) and slot (int32).
+// LDS of one tile: K block [Cq][HD + PAD], V^T [HD][Cq + PAD], per request
+// the query row offset (int64), position (int64) and slot (int32), then per
+// wave the 16 partial rows of its current unit [16][HD + 16 B] (PartialT).
 struct TileLds {
-  int Cq, ldk, ldv;
-  size_t k_off, v_off, q_off, pos_off, slot_off, bytes;
+  int Cq, ldk, ldv, ldo;
+  size_t k_off, v_off, q_off, pos_off, slot_off, o_off, bytes;
 };
 
 template <typename T, int HD>
-__host__ __device__ inline TileLds tile_lds(int C, int tile) {
+__host__ __device__ inline TileLds tile_lds(int C, int tile, int waves) {
   typedef QkShape<T, HD> S;
+  typedef typename PartialT<T>::type PT;
   TileLds L;
   L.Cq = (C + S::KQ - 1) / S::KQ * S::KQ;
   L.ldk = HD + S::PAD;
   L.ldv = L.Cq + S::PAD;
+  L.ldo = HD + 16 / (int)sizeof(PT);
   size_t off = 0;
   L.k_off = off;
   off += (size_t)L.Cq * L.ldk * sizeof(T);
@@ -359,6 +362,9 @@ __host__ __device__ inline TileLds tile_lds(int C, int tile) {
   off += (size_t)tile * 8;
   L.slot_off = off;
   off += (size_t)tile * 4;
+  off = (off + 15) / 16 * 16;
+  L.o_off = off;
+  off += (size_t)waves * 16 * L.ldo * sizeof(PT);
   L.bytes = (off + 15) / 16 * 16;
   return L;
 }
@@ -487,7 +493,8 @@ __device__ __forceinline__ typename MfmaOp<T, E>::frag load_vt(const T* vrow, in
 template <typename T, int HD, int NTM>
 __device__ void fwd_tile_units(const AttnArgs& a, const TileLds& L, const T* ks, const T* vt,
                                const int64_t* mq, const int64_t* mpos, const int32_t* mslot,
-                               int nreq, int64_t blk, int rows, int wave, int nwaves, int lane) {
+                               int nreq, int64_t blk, int rows, int wave, int nwaves, int lane,
+                               typename PartialT<T>::type* so) {
   typedef QkShape<T, HD, NTM> S;
   typedef typename S::Op Op;
   typedef typename S::frag frag;
@@ -605,17 +612,34 @@ __device__ void fwd_tile_units(const AttnArgs& a, const TileLds& L, const T* ks,
         }
       }
     }
-    if (valid) {
+    // the partial rows go out through the wave's LDS rows so that each store
+    // instruction writes whole rows (consecutive lanes on consecutive 16 bytes)
+    {
       const float inv = l > 0.f ? 1.f / l : 0.f;
       PT vals[QL];
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) vals[4 * dt + i] = (PT)(o[dt][i] * inv);
-      const int64_t prow = (int64_t)mslot[rq] * a.G + gh;
-      store_vals(static_cast<PT*>(a.part_o) + prow * HD + QL * grp, vals);
-      if (grp == 0) a.part_lse[prow] = m + __logf(l);
+      store_vals(so + col * L.ldo + QL * grp, vals);
+      if (valid && grp == 0) a.part_lse[(int64_t)mslot[rq] * a.G + gh] = m + __logf(l);
     }
+    wave_lds_sync();
+    {
+      constexpr int CH = HD * (int)sizeof(PT) / 16;  // 16-byte chunks per row
+      constexpr int CE = 16 / (int)sizeof(PT);
+#pragma unroll
+      for (int idx = lane; idx < 16 * CH; idx += 64) {
+        const int r = idx / CH, c = idx % CH;
+        const int rho2 = (u << 4) + r, rq2 = rho2 >> gl, gh2 = rho2 & (Gp - 1);
+        if (rq2 < nreq && gh2 < a.G) {
+          const uint4 v = *reinterpret_cast<const uint4*>(so + r * L.ldo + c * CE);
+          *reinterpret_cast<uint4*>(static_cast<PT*>(a.part_o) +
+                                    ((int64_t)mslot[rq2] * a.G + gh2) * HD + c * CE) = v;
+        }
+      }
+    }
+    wave_lds_sync();  // the rows are out; the next unit may overwrite them
   };
   frag qb[DEPTH + 1][DS];
 #pragma unroll
@@ -630,13 +654,15 @@ __device__ void fwd_tile_units(const AttnArgs& a, const TileLds& L, const T* ks,
 template <typename T, int HD, int NTM>
 __global__ void __launch_bounds__(256, PISA_ATTN_WAVES) attn_fwd_tile_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  const TileLds L = tile_lds<T, HD>(a.C, a.tile);
+  const TileLds L = tile_lds<T, HD>(a.C, a.tile, (int)(blockDim.x >> 6));
   T* ks = reinterpret_cast<T*>(smem + L.k_off);
   T* vt = reinterpret_cast<T*>(smem + L.v_off);
   int64_t* mq = reinterpret_cast<int64_t*>(smem + L.q_off);
   int64_t* mpos = reinterpret_cast<int64_t*>(smem + L.pos_off);
   int32_t* mslot = reinterpret_cast<int32_t*>(smem + L.slot_off);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  typedef typename PartialT<T>::type PT;
+  PT* so = reinterpret_cast<PT*>(smem + L.o_off) + wave * 16 * L.ldo;
   const int ntiles = *a.num_tiles;
   for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
     const int g = a.tile_group[tile];
@@ -658,7 +684,7 @@ __global__ void __launch_bounds__(256, PISA_ATTN_WAVES) attn_fwd_tile_kernel(Att
     stage_tile<T, HD>(a, b, h, blk, rows, ks, vt, L, tid, blockDim.x);
     __syncthreads();
     fwd_tile_units<T, HD, NTM>(a, L, ks, vt, mq, mpos, mslot, nreq, blk, rows, wave,
-                               (int)(blockDim.x >> 6), lane);
+                               (int)(blockDim.x >> 6), lane, so);
   }
 }
 
@@ -671,7 +697,7 @@ __global__ void __launch_bounds__(64, 2) attn_fwd_tile_direct_kernel(AttnArgs a,
   const RowInfo ri = row_info(a, slot);
   const int64_t blk = slot_block(a, slot);
   if (!slot_visible(a, blk, ri.pos)) return;
-  const TileLds L = tile_lds<T, HD>(a.C, 1);
+  const TileLds L = tile_lds<T, HD>(a.C, 1, 1);
   T* ks = reinterpret_cast<T*>(smem + L.k_off);
   T* vt = reinterpret_cast<T*>(smem + L.v_off);
   int64_t* mq = reinterpret_cast<int64_t*>(smem + L.q_off);
@@ -685,7 +711,8 @@ __global__ void __launch_bounds__(64, 2) attn_fwd_tile_direct_kernel(AttnArgs a,
   const int rows = (int)min((int64_t)a.C, (int64_t)a.N - blk * a.C);
   stage_tile<T, HD>(a, ri.b, ri.h, blk, rows, ks, vt, L, threadIdx.x, blockDim.x);
   __syncthreads();
-  fwd_tile_units<T, HD, NTM>(a, L, ks, vt, mq, mpos, mslot, 1, blk, rows, 0, 1, threadIdx.x & 63);
+  fwd_tile_units<T, HD, NTM>(a, L, ks, vt, mq, mpos, mslot, 1, blk, rows, 0, 1, threadIdx.x & 63,
+                             reinterpret_cast<typename PartialT<T>::type*>(smem + L.o_off));
 }
 
 // Merge the K partials of each (batch, token, query head) in slot order with
@@ -1717,11 +1744,11 @@ static int grid_size() {
 template <typename T, int HD, int NTM>
 static void launch_fwd_tile_n(const AttnArgs& a, bool grouped, int64_t slots, hipStream_t stream) {
   if (grouped) {
-    const size_t lds = tile_lds<T, HD>(a.C, a.tile).bytes;
+    const size_t lds = tile_lds<T, HD>(a.C, a.tile, 4).bytes;
     allow_lds((const void*)attn_fwd_tile_kernel<T, HD, NTM>, lds);
     PISA_TIMED("attn_fwd", stream, hipLaunchKernelGGL((attn_fwd_tile_kernel<T, HD, NTM>), dim3(grid_size()), dim3(256), lds, stream, a));
   } else if (slots > 0) {
-    const size_t lds = tile_lds<T, HD>(a.C, 1).bytes;
+    const size_t lds = tile_lds<T, HD>(a.C, 1, 1).bytes;
     allow_lds((const void*)attn_fwd_tile_direct_kernel<T, HD, NTM>, lds);
     PISA_TIMED("attn_fwd_direct", stream, hipLaunchKernelGGL((attn_fwd_tile_direct_kernel<T, HD, NTM>), dim3(slots), dim3(64), lds, stream, a, slots));
   }
@@ -1729,7 +1756,7 @@ static void launch_fwd_tile_n(const AttnArgs& a, bool grouped, int64_t slots, hi
 
 template <typename T, int HD>
 static void launch_fwd_tile(const AttnArgs& a, bool grouped, int64_t slots, hipStream_t stream) {
-  const int nt = tile_lds<T, HD>(a.C, 1).Cq / 16;
+  const int nt = tile_lds<T, HD>(a.C, 1, 1).Cq / 16;
   if (nt <= 2) launch_fwd_tile_n<T, HD, 2>(a, grouped, slots, stream);
   else if (nt <= 4) launch_fwd_tile_n<T, HD, 4>(a, grouped, slots, stream);
   else launch_fwd_tile_n<T, HD, 8>(a, grouped, slots, stream);
