@@ -157,3 +157,70 @@ def test_int32_indices_and_determinism(P):
     a = P.sparse_attention(qg, kg, vg, torch.from_numpy(idx).cuda(), 64)
     b = P.sparse_attention(qg, kg, vg, torch.from_numpy(idx).int().cuda(), 64)
     assert torch.equal(a, b)
+
+
+def _packed_indices(seed, bounds, kh, topk, block):
+    """Document-local ids for a packed prefill (every document's query rows)."""
+    parts = []
+    for d, (s, e) in enumerate(zip(bounds[:-1], bounds[1:])):
+        parts.append(_indices(seed + d, 1, e - s, kh, topk, e - s, block, empty_rows=False))
+    return np.concatenate(parts, 1)
+
+
+def test_packed_documents_forward_backward(P):
+    """cu_seqlens (``sparse_attn.py:29-54``): each document attends its own keys with
+    document-local ids and positions; O, LSE and dQ/dK/dV equal the per-document oracle."""
+    bounds = [0, 700, 1500, 1536, 2300]
+    n, qh, kh, dim, block, topk, dtype = bounds[-1], 8, 2, 128, 64, 6, "bf16"
+    print("attention packed documents", flush=True)
+    q, k, v = structured_qkv(31, 1, n, qh, kh, dim, dtype)
+    idx = _packed_indices(40, bounds, kh, topk, block)
+    dout = O.round_storage(np.random.default_rng(6).standard_normal((1, n, qh, dim)).astype(np.float32), dtype)
+    qg, kg, vg = (to_gpu(x, dtype).requires_grad_(True) for x in (q, k, v))
+    cu = torch.tensor(bounds, dtype=torch.int32, device="cuda")
+    out, lse = P.sparse_attention_with_lse(qg, kg, vg, torch.from_numpy(idx).cuda(), block, cu_seqlens=cu)
+    out.backward(to_gpu(dout, dtype))
+    ref_o, ref_lse, grads = [], [], [[], [], []]
+    for s, e in zip(bounds[:-1], bounds[1:]):
+        sl = slice(s, e)
+        o_, l_ = O.sparse_attention(q[:, sl], k[:, sl], v[:, sl], idx[:, sl], block)
+        g_ = O.sparse_attention_backward(q[:, sl], k[:, sl], v[:, sl], idx[:, sl], dout[:, sl], block)
+        ref_o.append(o_)
+        ref_lse.append(l_)
+        for j in range(3):
+            grads[j].append(g_[j])
+    assert excess_error(out.detach().float().cpu().numpy(), np.concatenate(ref_o, 1), dtype) <= TOL[dtype]
+    mine_lse, ref_lse = lse.cpu().numpy(), np.concatenate(ref_lse, 1)
+    fin = np.isfinite(ref_lse)
+    assert np.array_equal(np.isneginf(mine_lse), ~fin)
+    assert np.abs(mine_lse[fin] - ref_lse[fin]).max() <= TOL[dtype]
+    for name_, mine, ref in zip(("dq", "dk", "dv"), (qg.grad, kg.grad, vg.grad), grads):
+        err = excess_error(mine.float().cpu().numpy(), np.concatenate(ref, 1), dtype)
+        print(f"packed {name_} excess max-abs error {err:.3e}")
+        assert err <= TOL[dtype], f"packed {name_} max-abs error {err}"
+
+
+def test_packed_decode(P):
+    """One decode query per document (``validation.py:72-79``): local position = document
+    length - 1 unless an offset per document is given."""
+    bounds = [0, 900, 2000, 4096]
+    kh, qh, dim, block, topk = 2, 8, 64, 64, 5
+    print("attention packed decode", flush=True)
+    _, k, v = structured_qkv(32, 1, bounds[-1], qh, kh, dim, "bf16")
+    q = O.round_storage(np.random.default_rng(7).standard_normal((1, 3, qh, dim)).astype(np.float32), "bf16")
+    rng = np.random.default_rng(8)
+    idx = np.full((1, 3, kh, topk), -1, dtype=np.int64)
+    for d, (s, e) in enumerate(zip(bounds[:-1], bounds[1:])):
+        blocks = -(-(e - s) // block)
+        for h in range(kh):
+            pick = rng.permutation(blocks)[:topk]
+            idx[0, d, h, :len(pick)] = pick
+    cu = torch.tensor(bounds, dtype=torch.int64, device="cuda")
+    out, lse = P.sparse_attention_with_lse(to_gpu(q, "bf16"), to_gpu(k, "bf16"), to_gpu(v, "bf16"),
+                                           torch.from_numpy(idx).cuda(), block, cu_seqlens=cu)
+    for d, (s, e) in enumerate(zip(bounds[:-1], bounds[1:])):
+        pos = np.array([[e - s - 1]])
+        ref_o, ref_lse = O.sparse_attention(q[:, d:d + 1], k[:, s:e], v[:, s:e], idx[:, d:d + 1], block,
+                                            positions=pos)
+        assert excess_error(out[:, d:d + 1].float().cpu().numpy(), ref_o, "bf16") <= 2e-2
+        assert np.abs(lse[:, d:d + 1].cpu().numpy() - ref_lse).max() <= 2e-2
