@@ -29,12 +29,6 @@
 
 namespace pisa {
 
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-}
-
 template <typename I>
 __device__ __forceinline__ int64_t load_index(const void* p, int64_t i) {
   return (int64_t) static_cast<const I*>(p)[i];
@@ -612,8 +606,8 @@ __device__ void fwd_tile_units(const AttnArgs& a, const TileLds& L, const T* ks,
         }
       }
     }
-    // the partial rows go out through the wave's LDS rows so that each store
-    // instruction writes whole rows (consecutive lanes on consecutive 16 bytes)
+    // the partial rows go out through the wave's LDS rows (when it has them) so
+    // that each store instruction writes whole rows
     {
       const float inv = l > 0.f ? 1.f / l : 0.f;
       PT vals[QL];
@@ -621,11 +615,15 @@ __device__ void fwd_tile_units(const AttnArgs& a, const TileLds& L, const T* ks,
       for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) vals[4 * dt + i] = (PT)(o[dt][i] * inv);
-      store_vals(so + col * L.ldo + QL * grp, vals);
+      if (so) {
+        store_vals(so + col * L.ldo + QL * grp, vals);
+      } else if (valid) {
+        store_vals(static_cast<PT*>(a.part_o) + ((int64_t)mslot[rq] * a.G + gh) * HD + QL * grp, vals);
+      }
       if (valid && grp == 0) a.part_lse[(int64_t)mslot[rq] * a.G + gh] = m + __logf(l);
     }
-    wave_lds_sync();
-    {
+    if (so) {
+      wave_lds_sync();
       constexpr int CH = HD * (int)sizeof(PT) / 16;  // 16-byte chunks per row
       constexpr int CE = 16 / (int)sizeof(PT);
 #pragma unroll
@@ -638,8 +636,8 @@ __device__ void fwd_tile_units(const AttnArgs& a, const TileLds& L, const T* ks,
                                     ((int64_t)mslot[rq2] * a.G + gh2) * HD + c * CE) = v;
         }
       }
+      wave_lds_sync();  // the rows are out; the next unit may overwrite them
     }
-    wave_lds_sync();  // the rows are out; the next unit may overwrite them
   };
   frag qb[DEPTH + 1][DS];
 #pragma unroll
@@ -654,7 +652,9 @@ __device__ void fwd_tile_units(const AttnArgs& a, const TileLds& L, const T* ks,
 template <typename T, int HD, int NTM>
 __global__ void __launch_bounds__(256, PISA_ATTN_WAVES) attn_fwd_tile_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  const TileLds L = tile_lds<T, HD>(a.C, a.tile, (int)(blockDim.x >> 6));
+  // partial rows staged per wave only where the staging keeps two workgroups per CU
+  constexpr bool STAGE = NTM <= 4;
+  const TileLds L = tile_lds<T, HD>(a.C, a.tile, STAGE ? (int)(blockDim.x >> 6) : 0);
   T* ks = reinterpret_cast<T*>(smem + L.k_off);
   T* vt = reinterpret_cast<T*>(smem + L.v_off);
   int64_t* mq = reinterpret_cast<int64_t*>(smem + L.q_off);
@@ -662,7 +662,7 @@ __global__ void __launch_bounds__(256, PISA_ATTN_WAVES) attn_fwd_tile_kernel(Att
   int32_t* mslot = reinterpret_cast<int32_t*>(smem + L.slot_off);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   typedef typename PartialT<T>::type PT;
-  PT* so = reinterpret_cast<PT*>(smem + L.o_off) + wave * 16 * L.ldo;
+  PT* so = STAGE ? reinterpret_cast<PT*>(smem + L.o_off) + wave * 16 * L.ldo : nullptr;
   const int ntiles = *a.num_tiles;
   for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
     const int g = a.tile_group[tile];
@@ -1461,7 +1461,7 @@ __host__ __device__ inline size_t bwd_share_lds(int NT, int tile) {
 }
 
 template <typename T, int HD, int NT>
-__global__ void __launch_bounds__(256, 2) attn_bwd_share_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(256, NT <= 4 ? 2 : 1) attn_bwd_share_kernel(AttnArgs a) {
   typedef QkShape<T, HD> Sh;
   typedef typename Sh::Op Op;     // 16x16x32
   typedef typename Sh::frag frag;
@@ -1744,7 +1744,7 @@ static int grid_size() {
 template <typename T, int HD, int NTM>
 static void launch_fwd_tile_n(const AttnArgs& a, bool grouped, int64_t slots, hipStream_t stream) {
   if (grouped) {
-    const size_t lds = tile_lds<T, HD>(a.C, a.tile, 4).bytes;
+    const size_t lds = tile_lds<T, HD>(a.C, a.tile, NTM <= 4 ? 4 : 0).bytes;
     allow_lds((const void*)attn_fwd_tile_kernel<T, HD, NTM>, lds);
     PISA_TIMED("attn_fwd", stream, hipLaunchKernelGGL((attn_fwd_tile_kernel<T, HD, NTM>), dim3(grid_size()), dim3(256), lds, stream, a));
   } else if (slots > 0) {
@@ -1818,8 +1818,8 @@ template <typename T, int HD, int NT>
 static void launch_bwd_share(const AttnArgs& a, hipStream_t stream) {
   const size_t lds = bwd_share_lds<T, HD>(NT, a.tile);
   allow_lds((const void*)attn_bwd_share_kernel<T, HD, NT>, lds);
-  // two workgroups per CU, all resident
-  PISA_TIMED("attn_bwd", stream, hipLaunchKernelGGL((attn_bwd_share_kernel<T, HD, NT>), dim3(2 * device_cus()), dim3(256), lds, stream, a));
+  // all resident: two workgroups per CU (one at 128-key blocks)
+  PISA_TIMED("attn_bwd", stream, hipLaunchKernelGGL((attn_bwd_share_kernel<T, HD, NT>), dim3((NT <= 4 ? 2 : 1) * device_cus()), dim3(256), lds, stream, a));
 }
 
 template <typename T, int HD, int NT>
@@ -1841,10 +1841,14 @@ static bool launch_bwd_tiles(const AttnArgs& a, hipStream_t stream) {
     const int nt = (a.C + 31) / 32 * 2;
     if (bwd_tile_lds<T, HD>(nt, a.tile).bytes > (size_t)device_lds_limit()) return false;
     if constexpr (HD == 128) {
-      // shared P/dS when two workgroups fit a CU
+      // shared P/dS: two workgroups per CU up to 64-key blocks, one at 128 keys
       if (PISA_BWD_SHARE && nt <= 4 && 2 * bwd_share_lds<T, HD>(nt, a.tile) <= (size_t)device_lds_limit()) {
         if (nt == 2) launch_bwd_share<T, HD, 2>(a, stream);
         else launch_bwd_share<T, HD, 4>(a, stream);
+        return true;
+      }
+      if (PISA_BWD_SHARE && nt == 8 && bwd_share_lds<T, HD>(nt, a.tile) <= (size_t)device_lds_limit()) {
+        launch_bwd_share<T, HD, 8>(a, stream);
         return true;
       }
     }

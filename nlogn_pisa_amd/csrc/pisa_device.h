@@ -428,6 +428,14 @@ __device__ __forceinline__ void load_row_frags(const T* p, F (&f)[N]) {
   }
 }
 
+// LDS written by some lanes of a wave becomes visible to the wave's other
+// lanes (only LDS counters are waited for).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
 template <typename F, int N>
 __device__ __forceinline__ void zero_frags(F (&f)[N]) {
   __builtin_memset(f, 0, sizeof(f));

@@ -23,6 +23,11 @@ namespace pisa {
 
 constexpr int kMaxWidth = 512;
 
+// Support tiles of the MFMA routing in flight ahead of the one being scored.
+#ifndef PISA_ROUTE_DEPTH
+#define PISA_ROUTE_DEPTH 2
+#endif
+
 
 __device__ __forceinline__ int64_t ipow(int64_t b, int e) {
   int64_t r = 1;
@@ -273,10 +278,15 @@ struct SupportAcc {
   int n;
 };
 
-__device__ __forceinline__ SupportAcc support_acc(const float* v, int count, int n, bool lse,
-                                                  float scale) {
-  SupportAcc r{lse ? -INFINITY : 0.f, 0.f, 0};
-  if (lse) {
+// Scoring modes of the MFMA routing (block_scores, top_k_pyramid_torch.py:62-79
+// and :158-160): the node's own summary (pisa1), LogSumExp (pisa), the binary
+// pisa2 form (pisa2 at b = 2), mean + variance moments (pisa2 at b > 2).
+enum RouteMode { kModeOwn = 0, kModeLse = 1, kModeMoments = 2, kModeBinary = 3 };
+
+template <bool LSE>
+__device__ __forceinline__ SupportAcc support_acc(const float* v, int count, int n, float scale) {
+  SupportAcc r{LSE ? -INFINITY : 0.f, 0.f, 0};
+  if constexpr (LSE) {
     for (int i = 0; i < count; ++i)
       if (i < n) r.a0 = fmaxf(r.a0, v[i] * scale);
     for (int i = 0; i < count; ++i)
@@ -292,72 +302,92 @@ __device__ __forceinline__ SupportAcc support_acc(const float* v, int count, int
   return r;
 }
 
-__device__ __forceinline__ SupportAcc support_join(SupportAcc x, SupportAcc y, bool lse) {
-  if (!lse) return SupportAcc{x.a0 + y.a0, x.a1 + y.a1, x.n + y.n};
-  const float m = fmaxf(x.a0, y.a0);
-  if (m == -INFINITY) return x;
-  return SupportAcc{m, x.a1 * __expf(x.a0 - m) + y.a1 * __expf(y.a0 - m), x.n + y.n};
+template <bool LSE>
+__device__ __forceinline__ SupportAcc support_join(SupportAcc x, SupportAcc y) {
+  if constexpr (!LSE) {
+    return SupportAcc{x.a0 + y.a0, x.a1 + y.a1, x.n + y.n};
+  } else {
+    const float m = fmaxf(x.a0, y.a0);
+    if (m == -INFINITY) return x;
+    return SupportAcc{m, x.a1 * __expf(x.a0 - m) + y.a1 * __expf(y.a0 - m), x.n + y.n};
+  }
 }
 
-__device__ __forceinline__ float support_final(SupportAcc r, const float* v, bool lse, bool binary,
-                                               float scale) {
-  if (lse) return r.a0 + __logf(r.a1);
-  if (binary) {
+template <int MODE>
+__device__ __forceinline__ float support_final(SupportAcc r, const float* v, float scale) {
+  if constexpr (MODE == kModeLse) {
+    return r.a0 + __logf(r.a1);
+  } else if constexpr (MODE == kModeBinary) {
     const float z0 = v[0] * scale, z1 = v[1] * scale;
     const float d = z0 - z1;
     return r.n == 2 ? 0.5f * (z0 + z1) + 0.125f * d * d : z0;
+  } else {
+    const float count = (float)max(r.n, 1);
+    const float mean = r.a0 / count;
+    const float var = fmaxf(r.a1 / count - mean * mean, 0.f);
+    return scale * mean + (float)(0.5 * (double)scale * (double)scale) * var;
   }
-  const float count = (float)max(r.n, 1);
-  const float mean = r.a0 / count;
-  const float var = fmaxf(r.a1 / count - mean * mean, 0.f);
-  return scale * mean + (float)(0.5 * (double)scale * (double)scale) * var;
+}
+
+// Candidates of a 16-row support tile seen by one lane, RR rows each: their
+// valid support counts and the score slots (-1: none).  Lane group grp holds
+// rows 4 grp .. 4 grp + 3, i.e. candidates 4 grp / RR + j (RR <= 4) or half of
+// candidate grp / 2 (RR = 8).
+template <int RR>
+struct TileMeta {
+  static constexpr int NJ = RR <= 4 ? 4 / RR : 1;
+  int n[NJ], dst[NJ];
+};
+
+template <int RR, bool OWN>
+__device__ __forceinline__ void tile_meta(TileMeta<RR>& m, int mt, const int* ids_s,
+                                          const int* list_s, int nlist, int len, int grp) {
+  constexpr int cpt = 16 / RR;
+#pragma unroll
+  for (int j = 0; j < TileMeta<RR>::NJ; ++j) {
+    const int ci = RR <= 4 ? mt * cpt + (4 * grp) / RR + j : mt * cpt + (grp >> 1);
+    const bool ok = ci < nlist;
+    const int e = ok ? list_s[ci] : 0;
+    m.dst[j] = ok && (RR <= 4 || (grp & 1) == 0) ? e : -1;
+    m.n[j] = !ok ? 0 : OWN ? 1 : len - ids_s[e] * RR - (RR > 4 ? 4 * (grp & 1) : 0);
+  }
 }
 
 // Scores of the candidates of one 16-row support tile (RR rows per candidate):
 // lane (grp, col) holds head col's dots with rows 4 grp + i in sv.
-template <int RR>
-__device__ __forceinline__ void tile_scores(const f4& sv, int mt, const RouteArgs& a,
-                                            const int* ids_s, const int* list_s, float* sc_s,
-                                            int nlist, int len, bool own, bool lse, bool binary,
-                                            int col, int grp) {
+template <int RR, int MODE>
+__device__ __forceinline__ void tile_scores(const f4& sv, const TileMeta<RR>& m, float scale, int G,
+                                            float* sc_s, int col, int grp) {
+  constexpr bool LSE = MODE == kModeLse;
   const float v[4] = {sv[0], sv[1], sv[2], sv[3]};
-  constexpr int cpt = 16 / RR;
   if constexpr (RR <= 4) {
-    // candidates (4 grp) / RR + j of this tile, rows j RR .. j RR + RR - 1
 #pragma unroll
     for (int j = 0; j < 4 / RR; ++j) {
-      const int ci = mt * cpt + (4 * grp) / RR + j;
-      int n = 0;
-      if (ci < nlist) n = own ? 1 : len - ids_s[list_s[ci]] * RR;
       float head;
-      if (own) {
+      if constexpr (MODE == kModeOwn) {
         head = v[j];
       } else {
-        const SupportAcc acc = support_acc(v + j * RR, RR, n, lse, a.scale);
-        head = support_final(acc, v + j * RR, lse, binary, a.scale);
+        const SupportAcc acc = support_acc<LSE>(v + j * RR, RR, m.n[j], scale);
+        head = support_final<MODE>(acc, v + j * RR, scale);
       }
-      const float tot = row_sum16(col < a.G ? head : 0.f);
-      if (col == 0 && ci < nlist) sc_s[list_s[ci]] = tot;
+      const float tot = row_sum16(col < G ? head : 0.f);
+      if (col == 0 && m.dst[j] >= 0) sc_s[m.dst[j]] = tot;
     }
   } else {
-    // RR = 8: candidate grp / 2 of this tile over lane groups 2c (children 0-3)
-    // and 2c + 1 (children 4-7)
-    const int ci = mt * cpt + (grp >> 1);
-    int n = 0;
-    if (ci < nlist) n = len - ids_s[list_s[ci]] * RR - 4 * (grp & 1);
-    SupportAcc acc = support_acc(v, 4, n, lse, a.scale);
+    // RR = 8: lane groups 2c (children 0-3) and 2c + 1 (children 4-7) of candidate c
+    SupportAcc acc = support_acc<LSE>(v, 4, m.n[0], scale);
     SupportAcc other;
     other.a0 = __shfl_xor(acc.a0, 16);
     other.a1 = __shfl_xor(acc.a1, 16);
     other.n = __shfl_xor(acc.n, 16);
-    acc = (grp & 1) ? support_join(other, acc, lse) : support_join(acc, other, lse);
-    const float head = support_final(acc, v, lse, false, a.scale);
-    const float tot = row_sum16(col < a.G ? head : 0.f);
-    if (col == 0 && (grp & 1) == 0 && ci < nlist) sc_s[list_s[ci]] = tot;
+    acc = (grp & 1) ? support_join<LSE>(other, acc) : support_join<LSE>(acc, other);
+    const float head = support_final<MODE == kModeBinary ? kModeMoments : MODE>(acc, v, scale);
+    const float tot = row_sum16(col < G ? head : 0.f);
+    if (col == 0 && m.dst[0] >= 0) sc_s[m.dst[0]] = tot;
   }
 }
 
-template <typename T, int HD>
+template <typename T, int HD, int RR, int MODE>
 __global__ void __launch_bounds__(64) route_grouped_kernel(RouteArgs a) {
   typedef QkShape<T, HD> S;
   typedef typename S::Op Op;
@@ -379,11 +409,9 @@ __global__ void __launch_bounds__(64) route_grouped_kernel(RouteArgs a) {
   const int col = lane & 15, grp = lane >> 4;
   const int K = a.topk;
   const int levels_traced = a.top + 1;
-  const bool own = a.method == PISA_METHOD_PISA1;  // support = the node's own summary
-  const bool lse = a.method == PISA_METHOD_LSE;
-  const bool binary = !lse && !own && a.branching == 2;
-  const int R = own ? 1 : a.branching;             // support rows per candidate (<= 8)
-  const int cpt = 16 / R;                          // candidates per 16 support rows
+  constexpr bool own = MODE == kModeOwn;  // support = the node's own summary
+  constexpr int R = RR;                    // support rows per candidate (<= 8)
+  constexpr int cpt = 16 / R;              // candidates per 16 support rows
 
   // Q^T: lane (grp, col) holds head col's dimensions 4 E s + E grp + e of step s
   frag qb[DS];
@@ -440,32 +468,34 @@ __global__ void __launch_bounds__(64) route_grouped_kernel(RouteArgs a) {
     // exist (past the list, or past the level's tail) read row 0 of the level
     // instead and are masked out of the support scores, so no load sits behind
     // a branch and the compiler keeps the next tile's loads in flight.
-    auto fetch = [&](int mt, frag (&f)[DS]) {
+    // (the candidate counts and score slots of the tile come with its rows)
+    auto fetch = [&](int mt, frag (&f)[DS], TileMeta<R>& m) {
       const int ci = mt * cpt + col / R, child = col % R;  // ci < nlist implies mt < ntile
       const int id = ci < nlist ? ids_s[list_s[ci]] : 0;
       const int64_t r = (int64_t)id * R + child;
       const bool ok = ci < nlist && r < len;
       load_row_frags<E>(base + (ok ? r : 0) * rstride + E * grp, f);
+      tile_meta<R, own>(m, mt, ids_s, list_s, nlist, len, grp);
     };
-    // tile mt: scored from `xf`, loads tile mt + 1 into `xn`; the two buffers
-    // alternate by unrolling, never by copies
-    auto tile = [&](int mt, frag (&xf)[DS], frag (&xn)[DS]) {
-      fetch(mt + 1, xn);
+    // tile mt: scored from `xf`, loads tile mt + DEPTH into `xn` (the buffer the
+    // previous tile used); the buffers rotate by unrolling, never by copies
+    constexpr int DEPTH = PISA_ROUTE_DEPTH;
+    auto tile = [&](int mt, frag (&xf)[DS], frag (&xn)[DS], const TileMeta<R>& mf, TileMeta<R>& mn) {
+      fetch(mt + DEPTH, xn, mn);
       f4 sv = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int d = 0; d < DS; ++d) sv = Op::mma(xf[d], qb[d], sv);
-      switch (R) {
-        case 1: tile_scores<1>(sv, mt, a, ids_s, list_s, sc_s, nlist, len, own, lse, binary, col, grp); break;
-        case 2: tile_scores<2>(sv, mt, a, ids_s, list_s, sc_s, nlist, len, own, lse, binary, col, grp); break;
-        case 4: tile_scores<4>(sv, mt, a, ids_s, list_s, sc_s, nlist, len, own, lse, binary, col, grp); break;
-        default: tile_scores<8>(sv, mt, a, ids_s, list_s, sc_s, nlist, len, own, lse, binary, col, grp); break;
-      }
+      tile_scores<R, MODE>(sv, mf, a.scale, a.G, sc_s, col, grp);
     };
-    frag xb[2][DS];
-    fetch(0, xb[0]);
-    for (int mt = 0; mt < ntile; mt += 2) {
-      tile(mt, xb[0], xb[1]);
-      if (mt + 1 < ntile) tile(mt + 1, xb[1], xb[0]);
+    frag xb[DEPTH + 1][DS];
+    TileMeta<R> mb[DEPTH + 1];
+#pragma unroll
+    for (int p = 0; p < DEPTH; ++p) fetch(p, xb[p], mb[p]);
+    for (int mt0 = 0; mt0 < ntile; mt0 += DEPTH + 1) {
+#pragma unroll
+      for (int p = 0; p <= DEPTH; ++p)
+        if (mt0 + p < ntile)
+          tile(mt0 + p, xb[p], xb[(p + DEPTH) % (DEPTH + 1)], mb[p], mb[(p + DEPTH) % (DEPTH + 1)]);
     }
     __syncthreads();
 
@@ -598,13 +628,39 @@ static int launch_route_t(const RouteArgs& a, int64_t items, int threads, hipStr
   }
 }
 
+template <typename T, int HD, int RR, int MODE>
+static void launch_route_rm(const RouteArgs& a, int64_t items, hipStream_t stream) {
+  PISA_TIMED("route", stream, hipLaunchKernelGGL((route_grouped_kernel<T, HD, RR, MODE>), dim3(items), dim3(64), 0, stream, a));
+}
+
+// One kernel per (support rows per candidate, scoring mode).
+template <typename T, int HD>
+static void launch_route_hd(const RouteArgs& a, int64_t items, hipStream_t stream) {
+  if (a.method == PISA_METHOD_PISA1) return launch_route_rm<T, HD, 1, kModeOwn>(a, items, stream);
+  const bool lse = a.method == PISA_METHOD_LSE;
+  switch (a.branching) {
+    case 2:
+      if (lse) launch_route_rm<T, HD, 2, kModeLse>(a, items, stream);
+      else launch_route_rm<T, HD, 2, kModeBinary>(a, items, stream);
+      break;
+    case 4:
+      if (lse) launch_route_rm<T, HD, 4, kModeLse>(a, items, stream);
+      else launch_route_rm<T, HD, 4, kModeMoments>(a, items, stream);
+      break;
+    default:
+      if (lse) launch_route_rm<T, HD, 8, kModeLse>(a, items, stream);
+      else launch_route_rm<T, HD, 8, kModeMoments>(a, items, stream);
+      break;
+  }
+}
+
 template <typename T>
 static int launch_route_grouped(const RouteArgs& a, int64_t items, hipStream_t stream) {
   switch (a.D) {
-    case 16: PISA_TIMED("route", stream, hipLaunchKernelGGL((route_grouped_kernel<T, 16>), dim3(items), dim3(64), 0, stream, a)); break;
-    case 32: PISA_TIMED("route", stream, hipLaunchKernelGGL((route_grouped_kernel<T, 32>), dim3(items), dim3(64), 0, stream, a)); break;
-    case 64: PISA_TIMED("route", stream, hipLaunchKernelGGL((route_grouped_kernel<T, 64>), dim3(items), dim3(64), 0, stream, a)); break;
-    default: PISA_TIMED("route", stream, hipLaunchKernelGGL((route_grouped_kernel<T, 128>), dim3(items), dim3(64), 0, stream, a)); break;
+    case 16: launch_route_hd<T, 16>(a, items, stream); break;
+    case 32: launch_route_hd<T, 32>(a, items, stream); break;
+    case 64: launch_route_hd<T, 64>(a, items, stream); break;
+    default: launch_route_hd<T, 128>(a, items, stream); break;
   }
   return check_launch("route");
 }
