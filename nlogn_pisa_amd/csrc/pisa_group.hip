@@ -196,6 +196,75 @@ __global__ void __launch_bounds__(1024) bucket_scan_kernel(const int32_t* counts
   if (tid == 1023) *num_tiles = (int32_t)part[1023];
 }
 
+// The same exclusive scan of tiles per group for many groups, in three passes:
+// per block of kScanGroups groups the local offsets and the block's total,
+// the scan of the block totals (and the tile count), then the block bases added.
+constexpr int kScanGroups = 4096;  // 256 threads x 16 consecutive groups
+
+__global__ void __launch_bounds__(256) scan_local_kernel(const int32_t* counts, int64_t groups,
+                                                         int tile, int32_t* tile_off,
+                                                         int32_t* block_sum) {
+  __shared__ int part[256];
+  const int tid = threadIdx.x;
+  const int64_t begin = (int64_t)blockIdx.x * kScanGroups + tid * 16;
+  int t[16];
+  int sum = 0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t g = begin + i;
+    t[i] = g < groups ? (counts[g] + tile - 1) / tile : 0;
+    sum += t[i];
+  }
+  part[tid] = sum;
+  __syncthreads();
+  for (int off = 1; off < 256; off <<= 1) {
+    const int v = tid >= off ? part[tid - off] : 0;
+    __syncthreads();
+    part[tid] += v;
+    __syncthreads();
+  }
+  int run = part[tid] - sum;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t g = begin + i;
+    if (g < groups) tile_off[g] = run;
+    run += t[i];
+  }
+  if (tid == 255) block_sum[blockIdx.x] = part[255];
+}
+
+__global__ void __launch_bounds__(1024) scan_blocks_kernel(int32_t* block_sum, int64_t blocks,
+                                                           int32_t* num_tiles) {
+  __shared__ int part[1024];
+  const int tid = threadIdx.x;
+  int64_t carry = 0;
+  for (int64_t b0 = 0; b0 < blocks; b0 += 1024) {
+    const int64_t b = b0 + tid;
+    const int v = b < blocks ? block_sum[b] : 0;
+    part[tid] = v;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {
+      const int x = tid >= off ? part[tid - off] : 0;
+      __syncthreads();
+      part[tid] += x;
+      __syncthreads();
+    }
+    if (b < blocks) block_sum[b] = (int32_t)(carry + part[tid] - v);  // exclusive base
+    carry += part[1023];
+    __syncthreads();
+  }
+  if (tid == 0) *num_tiles = (int32_t)carry;
+}
+
+__global__ void __launch_bounds__(256) scan_add_kernel(int32_t* tile_off, int64_t groups,
+                                                       const int32_t* block_base) {
+  const int64_t g = (int64_t)blockIdx.x * kScanGroups + threadIdx.x;
+  const int32_t base = block_base[blockIdx.x];
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    if (g + 256 * i < groups) tile_off[g + 256 * i] += base;
+}
+
 template <typename Src>
 __global__ void __launch_bounds__(kBucketThreads) bucket_scatter_kernel(
     Src src, int64_t slot_begin, int64_t slot_end, int64_t chunk,
@@ -225,6 +294,7 @@ void carve_buckets(Carve& c, Buckets& b, int64_t slots, int64_t groups, int tile
   b.tile_group = c.take<int32_t>(b.max_tiles);
   b.tile_req = c.take<int32_t>(b.max_tiles * tile);
   b.hist = groups <= kLdsGroups ? c.take<int32_t>(kMaxBucketGroups * groups) : nullptr;
+  b.block_sum = groups > kLdsGroups ? c.take<int32_t>((groups + kScanGroups - 1) / kScanGroups) : nullptr;
 }
 
 static void fill_i32(int32_t* p, int64_t n, int32_t v, hipStream_t stream) {
@@ -277,8 +347,15 @@ static int run_buckets(const Src& src, int64_t slot_begin, int64_t slot_end, Buc
   const int64_t grid = (range + chunk - 1) / chunk;
   PISA_TIMED("bucket_count", stream, hipLaunchKernelGGL((bucket_count_kernel<Src>), dim3(grid), dim3(kBucketThreads), 0, stream,
                      src, slot_begin, slot_end, chunk, b.counts));
-  PISA_TIMED("bucket_scan", stream, hipLaunchKernelGGL(bucket_scan_kernel, dim3(1), dim3(1024), 0, stream, b.counts, b.groups,
-                     b.tile, b.tile_off, b.num_tiles));
+  {
+    const int64_t nb = (b.groups + kScanGroups - 1) / kScanGroups;
+    PISA_TIMED("bucket_scan", stream, hipLaunchKernelGGL(scan_local_kernel, dim3(nb), dim3(256), 0, stream, b.counts, b.groups,
+                       b.tile, b.tile_off, b.block_sum));
+    PISA_TIMED("bucket_scan", stream, hipLaunchKernelGGL(scan_blocks_kernel, dim3(1), dim3(1024), 0, stream, b.block_sum, nb,
+                       b.num_tiles));
+    PISA_TIMED("bucket_scan", stream, hipLaunchKernelGGL(scan_add_kernel, dim3(nb), dim3(256), 0, stream, b.tile_off, b.groups,
+                       b.block_sum));
+  }
   PISA_TIMED("bucket_scatter", stream, hipLaunchKernelGGL((bucket_scatter_kernel<Src>), dim3(grid), dim3(kBucketThreads), 0, stream,
                      src, slot_begin, slot_end, chunk, b.tile_off, b.cursors, b.tile, b.tile_group,
                      b.tile_req));

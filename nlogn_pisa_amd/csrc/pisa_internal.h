@@ -60,6 +60,7 @@ struct Buckets {
   int32_t* tile_req;    // [max_tiles * tile]
   int32_t* num_tiles;   // [1]
   int32_t* hist;        // [kMaxBucketGroups rows][groups]: per-workgroup histograms, then offsets
+  int32_t* block_sum;   // [groups / 4096]: block totals of the many-group scan, then bases
   int64_t groups;
   int64_t max_tiles;
   int tile;
