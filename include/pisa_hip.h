@@ -132,6 +132,17 @@ int pisa_pyramid_append(const void* keys, int64_t k_stride_batch, int64_t k_stri
                         const int32_t* starts, void* storage, int64_t storage_stride_batch,
                         int32_t dtype, void* stream);
 
+/* Split-half rotary encoding (pisa/pisa/ops/lrpe/rotary.py:9-16, the eager
+ * float32 formula of rotary_torch.py:5-10): y[..., f] = x_f cos - x_{f+D/2} sin,
+ * y[..., f + D/2] = x_f sin + x_{f+D/2} cos with angle = positions[b, t] *
+ * frequency[f] in float32 (frequency: D/2 floats); inverse != 0 turns by the
+ * negative angle (the gradient).  x and y are [B,T,H,D] with contiguous
+ * [H,D] rows; y may alias x. */
+int pisa_rotary(const void* x, int64_t x_stride_batch, int64_t x_stride_token, void* y,
+                int64_t y_stride_batch, int64_t y_stride_token, int32_t batch, int32_t tokens,
+                int32_t heads, int32_t dim, const float* frequency, const int64_t* positions,
+                int64_t positions_stride_batch, int32_t inverse, int32_t dtype, void* stream);
+
 /* Workspace bytes for pisa_select / pisa_leaf_scores. */
 size_t pisa_select_workspace_size(const pisa_qk_desc* qk, const pisa_select_params* p);
 

@@ -27,7 +27,7 @@ MAX_LEVELS = 32
 # Every exported entry point of include/pisa_hip.h.
 EXPORTS = (
     "pisa_last_error", "pisa_abi_version", "pisa_routing_geometry", "pisa_pyramid_layout",
-    "pisa_mean_pool", "pisa_build_pyramid", "pisa_pyramid_append", "pisa_select_workspace_size", "pisa_select",
+    "pisa_mean_pool", "pisa_build_pyramid", "pisa_pyramid_append", "pisa_rotary", "pisa_select_workspace_size", "pisa_select",
     "pisa_leaf_workspace_size", "pisa_leaf_scores", "pisa_attention_workspace_size", "pisa_sparse_attention_fwd",
     "pisa_sparse_attention_bwd", "pisa_profile_begin", "pisa_profile_end",
 )
@@ -101,6 +101,7 @@ def _declare(lib):
         "pisa_build_pyramid": (I32, [P, I64, I64, I32, I32, I32, I32, I32, I32, I32, P, I64, I32, P]),
         "pisa_pyramid_append": (I32, [P, I64, I64, I32, I32, I32, I32, I32, I32, I32, I32,
                                       ctypes.POINTER(I32), P, I64, I32, P]),
+        "pisa_rotary": (I32, [P, I64, I64, P, I64, I64, I32, I32, I32, I32, P, P, I64, I32, I32, P]),
         "pisa_select_workspace_size": (SZ, [ctypes.POINTER(QkDesc), ctypes.POINTER(SelectParams)]),
         "pisa_select": (I32, [ctypes.POINTER(QkDesc), ctypes.POINTER(SelectParams), P, P,
                               ctypes.POINTER(PyramidDesc), P, I64, P, P, P, SZ, P]),

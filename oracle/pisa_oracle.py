@@ -28,7 +28,8 @@ __all__ = [
     "round_storage", "mean_pool", "build_pyramid", "routing_geometry", "force_mask",
     "routing_masks", "block_scores", "network_topk", "pyramid_select", "query_positions",
     "sparse_attention", "sparse_attention_dense", "sparse_attention_backward",
-    "leaf_scores", "flops_visible", "SENTINEL_FORCED", "SENTINEL_INVALID",
+    "leaf_scores", "flops_visible", "rotary", "rotary_frequency", "SENTINEL_FORCED",
+    "SENTINEL_INVALID",
 ]
 
 SENTINEL_FORCED = np.float32(1.0e9)
@@ -522,4 +523,31 @@ def flops_visible(indices, block_size, n, positions, causal=True):
     """Number of (row, key) pairs attended per KV head row: sum of visible keys."""
     _, valid = _gather_tokens(np.asarray(indices), block_size, n, positions, causal)
     return int(valid.sum())
+
+
+# --------------------------------------------------------------------------- rotary encoding
+
+
+def rotary_frequency(head_dim, base, fraction):
+    """Frequencies of ``xmixers/xmixers/modules/pes/lrpe.py:20-28`` (type 3): the float32
+    values base^(-2 i / head_dim) for i < head_dim // 2 * fraction, zero after."""
+    exponent = np.float32(-2.0 / head_dim) * np.arange(head_dim // 2, dtype=np.float32)
+    theta = np.power(np.float32(base), exponent, dtype=np.float32)
+    theta[int(head_dim // 2 * fraction):] = 0
+    return theta
+
+
+def rotary(x, frequency, positions):
+    """Split-half rotary encoding (``pisa/pisa/ops/lrpe/rotary_torch.py:5-10``).
+
+    The angle is the reference's float32 product position x frequency; the turn
+    itself is evaluated in float64 (callers round to the storage dtype).
+    ``positions`` is ``[B or 1, T]``.
+    """
+    x = np.asarray(x, dtype=np.float64)
+    angles = (np.asarray(positions, dtype=np.float32)[..., None, None]
+              * np.asarray(frequency, dtype=np.float32).reshape(-1)).astype(np.float64)
+    first, second = np.split(x, 2, axis=-1)
+    cos, sin = np.cos(angles), np.sin(angles)
+    return np.concatenate((first * cos - second * sin, first * sin + second * cos), -1)
 

@@ -16,6 +16,9 @@ scores                 closed forms: LSE, mean+var/2, binary pisa2 == general fo
                        one valid child -> z
 sparse_attention       dense textbook attention (union mask), torch fp64 autograd,
                        finite differences for the gradients, LSE closed form
+rotary_frequency       closed form base^(-2i/d) within float32 rounding, zero tail count
+rotary                 invariants: pair norms kept, identity at position 0, turns compose
+                       (p1 then p2 == p1 + p2), negated frequencies undo the turn
 =====================  ==========================================================
 """
 
@@ -349,3 +352,34 @@ def test_attention_lse_closed_form():
     keys = sorted({j for i in idx[0, t, h] if i >= 0 for j in range(i * 16, i * 16 + 16) if j <= t})
     z = k[0, keys, h] @ q[0, t, hq] * 16 ** -0.5
     assert abs(lse[0, t, hq] - np.log(np.exp(z).sum())) < 1e-12
+
+
+# ----------------------------------------------------------------- rotary encoding
+
+@pytest.mark.parametrize("dim,fraction", [(64, 0.5), (128, 1.0), (32, 0.25)])
+def test_rotary_frequency_closed_form(dim, fraction):
+    theta = O.rotary_frequency(dim, 10000.0, fraction)
+    count = int(dim // 2 * fraction)
+    exact = 10000.0 ** (-2.0 * np.arange(dim // 2) / dim)
+    assert theta.dtype == np.float32 and theta.shape == (dim // 2,)
+    np.testing.assert_allclose(theta[:count], exact[:count], rtol=2e-6)
+    assert not theta[count:].any()
+
+
+def test_rotary_invariants():
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((2, 40, 3, 64))
+    freq = O.rotary_frequency(64, 10000.0, 1.0)
+    pos = np.stack([np.arange(40), np.arange(40) + 977])
+    y = O.rotary(x, freq, pos)
+    half = 32
+    norm = lambda a: a[..., :half] ** 2 + a[..., half:] ** 2
+    np.testing.assert_allclose(norm(y), norm(x), rtol=1e-12)
+    np.testing.assert_allclose(O.rotary(x, freq, np.zeros((1, 40)))[0], x[0], rtol=0, atol=0)
+    # turns compose: p1 then p2 equals p1 + p2 (small integer positions: exact float32 angles)
+    p1, p2 = np.full((1, 40), 3), np.full((1, 40), 5)
+    np.testing.assert_allclose(O.rotary(O.rotary(x, freq, p1), freq, p2), O.rotary(x, freq, p1 + p2),
+                               atol=1e-6)
+    # negated frequencies undo the turn
+    np.testing.assert_allclose(O.rotary(y, -freq, pos), x, atol=1e-9)
+
