@@ -132,6 +132,144 @@ __device__ float score_node(const RouteArgs& a, const float (&qr)[MAXG][CH], int
   return row_sum16(sub < G ? head : 0.f);
 }
 
+// Leaf score of candidate block `id` for the fused schedule, one wave on the
+// matrix cores (the leaf_tile_kernel formulation for a single request):
+// S^T = K Q^T per 16 keys (A = the block's key rows gathered from memory in the
+// natural k order, B = the item's query heads as columns), then per head the
+// LogSumExp of s * S (pisa) or s * mean + s^2 / 2 * var of S (pisa2) over the
+// block's valid keys, summed over the G heads (block_scores,
+// top_k_pyramid_torch.py:62-80).  Every lane returns the score.
+template <typename T, int HD, int NTM>
+struct LeafBlock {
+  typename QkShape<T, HD>::frag k[NTM][QkShape<T, HD>::DS];
+  int rows;
+};
+
+// the key rows of candidate block `id` (rows past the block's end repeat its last)
+template <typename T, int HD, int NTM>
+__device__ __forceinline__ void leaf_fetch(const RouteArgs& a, int b, int h, int id, int lane,
+                                           LeafBlock<T, HD, NTM>& kb) {
+  typedef QkShape<T, HD> S;
+  const int col = lane & 15, grp = lane >> 4;
+  kb.rows = (int)min((int64_t)a.C, (int64_t)a.N - (int64_t)id * a.C);  // >= 1
+  const int NT = (a.C + 15) / 16;
+  const T* base = static_cast<const T*>(a.key) + b * a.key_batch + (int64_t)id * a.C * a.key_token +
+                  (int64_t)h * HD;
+#pragma unroll
+  for (int mt = 0; mt < NTM; ++mt) {
+    const int row = mt < NT ? min(16 * mt + col, kb.rows - 1) : 0;
+    load_row_frags<S::E>(base + (int64_t)row * a.key_token + S::E * grp, kb.k[mt]);
+  }
+}
+
+// Per-head LogSumExp of s * S (pisa) or s * mean + s^2 / 2 * var of S (pisa2)
+// over the block's valid keys, summed over the G heads; sv holds S^T tiles
+// (lane (grp, col): head col, keys 16 mt + 4 grp + i).  Every lane returns it.
+template <int NTM>
+__device__ __forceinline__ float leaf_head_sum(const RouteArgs& a, const f4 (&sv)[NTM], int rows,
+                                               int lane) {
+  const int col = lane & 15, grp = lane >> 4;
+  const int NT = (a.C + 15) / 16;
+  const float scale = a.scale;
+  float head;
+  if (a.method == PISA_METHOD_LSE) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int mt = 0; mt < NTM; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (mt < NT && 16 * mt + 4 * grp + i < rows) m = fmaxf(m, sv[mt][i] * scale);
+    m = xor32_max(xor16_max(m));
+    float l = 0.f;
+#pragma unroll
+    for (int mt = 0; mt < NTM; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (mt < NT && 16 * mt + 4 * grp + i < rows) l += __expf(sv[mt][i] * scale - m);
+    l = xor32_sum(xor16_sum(l));
+    head = m + __logf(l);
+  } else {
+    float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int mt = 0; mt < NTM; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (mt < NT && 16 * mt + 4 * grp + i < rows) {
+          s1 += sv[mt][i];
+          s2 = fmaf(sv[mt][i], sv[mt][i], s2);
+        }
+    s1 = xor32_sum(xor16_sum(s1));
+    s2 = xor32_sum(xor16_sum(s2));
+    const float count = (float)rows;
+    const float mean = s1 / count;
+    const float var = fmaxf(s2 / count - mean * mean, 0.f);
+    head = scale * mean + (float)(0.5 * (double)scale * (double)scale) * var;
+  }
+  return row_sum16(col < a.G ? head : 0.f);
+}
+
+template <typename T, int HD, int NTM>
+__device__ float leaf_score_mfma(const RouteArgs& a, const typename QkShape<T, HD>::frag (&qb)[QkShape<T, HD>::DS],
+                                 const LeafBlock<T, HD, NTM>& kb, int lane) {
+  typedef QkShape<T, HD> S;
+  f4 sv[NTM];
+#pragma unroll
+  for (int mt = 0; mt < NTM; ++mt) {
+    sv[mt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int d = 0; d < S::DS; ++d) sv[mt] = S::Op::mma(kb.k[mt][d], qb[d], sv[mt]);
+  }
+  return leaf_head_sum<NTM>(a, sv, kb.rows, lane);
+}
+
+// Candidates wave, wave + nwaves, ... of the scoreable list; with PREFETCH each
+// wave loads the next candidate's key block while it scores the current one
+// (the two blocks alternate by unrolling).
+template <typename T, int HD, int NTM, bool PREFETCH>
+__device__ void leaf_scores_mfma(const RouteArgs& a, const typename QkShape<T, HD>::frag (&qb)[QkShape<T, HD>::DS],
+                                 int b, int h, const int* ids_s, const int* list_s, float* sc_s,
+                                 int nlist, int wave, int nwaves, int lane) {
+  auto id_of = [&](int i) { return i < nlist ? ids_s[list_s[i]] : ids_s[list_s[0]]; };
+  if constexpr (!PREFETCH) {
+    // one key tile's rows in registers at a time
+    typedef QkShape<T, HD> S;
+    for (int i = wave; i < nlist; i += nwaves) {
+      const int id = id_of(i);
+      LeafBlock<T, HD, 1> kt;
+      const int rows = (int)min((int64_t)a.C, (int64_t)a.N - (int64_t)id * a.C);
+      const int NT = (a.C + 15) / 16;
+      const T* base = static_cast<const T*>(a.key) + b * a.key_batch +
+                      (int64_t)id * a.C * a.key_token + (int64_t)h * HD;
+      f4 sv[NTM];
+#pragma unroll
+      for (int mt = 0; mt < NTM; ++mt) {
+        sv[mt] = f4{0.f, 0.f, 0.f, 0.f};
+        if (mt < NT) {
+          const int row = min(16 * mt + (lane & 15), rows - 1);
+          load_row_frags<S::E>(base + (int64_t)row * a.key_token + S::E * (lane >> 4), kt.k[0]);
+#pragma unroll
+          for (int d = 0; d < S::DS; ++d) sv[mt] = S::Op::mma(kt.k[0][d], qb[d], sv[mt]);
+        }
+      }
+      const float s = leaf_head_sum<NTM>(a, sv, rows, lane);
+      if (lane == 0) sc_s[list_s[i]] = s;
+    }
+    return;
+  }
+  LeafBlock<T, HD, NTM> kb[2];
+  if (wave < nlist) leaf_fetch<T, HD, NTM>(a, b, h, id_of(wave), lane, kb[0]);
+  for (int i = wave; i < nlist; i += 2 * nwaves) {
+    leaf_fetch<T, HD, NTM>(a, b, h, id_of(i + nwaves), lane, kb[1]);
+    float s = leaf_score_mfma<T, HD, NTM>(a, qb, kb[0], lane);
+    if (lane == 0) sc_s[list_s[i]] = s;
+    if (i + nwaves < nlist) {
+      leaf_fetch<T, HD, NTM>(a, b, h, id_of(i + 2 * nwaves), lane, kb[0]);
+      s = leaf_score_mfma<T, HD, NTM>(a, qb, kb[1], lane);
+      if (lane == 0) sc_s[list_s[i + nwaves]] = s;
+    }
+  }
+}
+
 template <typename T, int CH, int MAXG>
 __global__ void __launch_bounds__(512) route_kernel(RouteArgs a) {
   __shared__ int ids_s[kMaxWidth];
@@ -203,10 +341,31 @@ __global__ void __launch_bounds__(512) route_kernel(RouteArgs a) {
     if (grouped_leaf) return;
 
     const int nlist = cnt_s[1];
-    for (int i = rgrp; i < nlist; i += nrgrp) {
-      const int e = list_s[i];
-      const float s = score_node<T, CH, MAXG>(a, qr, b, h, ids_s[e], level, sub);
-      if (sub == 0) sc_s[e] = s;
+    // the leaf level of pisa / pisa2 on the matrix cores: a wave per candidate
+    constexpr int HD = 16 * CH;
+    constexpr bool kMfmaLeaf = sizeof(T) == 2 && HD >= 32 && MAXG <= 16;
+    if (kMfmaLeaf && level == 0 && a.method != PISA_METHOD_PISA1) {
+      typedef QkShape<T, HD> Sh;
+      typename Sh::frag qb[Sh::DS];
+      const int col = lane & 15, grp = lane >> 4;
+      if (col < a.G)
+        load_row_frags<Sh::E>(static_cast<const T*>(a.q) + b * a.q_batch + t * a.q_token +
+                                  ((int64_t)h * a.G + col) * HD + Sh::E * grp,
+                              qb);
+      else
+        zero_frags(qb);
+      const int nwaves = nthr >> 6;
+      // two blocks in flight when the registers allow it (up to 64 keys, 4 heads per kv head)
+      if (a.C <= 64)
+        leaf_scores_mfma<T, HD, 4, (MAXG <= 4)>(a, qb, b, h, ids_s, list_s, sc_s, nlist, wave, nwaves, lane);
+      else
+        leaf_scores_mfma<T, HD, 8, false>(a, qb, b, h, ids_s, list_s, sc_s, nlist, wave, nwaves, lane);
+    } else {
+      for (int i = rgrp; i < nlist; i += nrgrp) {
+        const int e = list_s[i];
+        const float s = score_node<T, CH, MAXG>(a, qr, b, h, ids_s[e], level, sub);
+        if (sub == 0) sc_s[e] = s;
+      }
     }
     __syncthreads();
 
