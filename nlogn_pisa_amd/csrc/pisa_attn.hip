@@ -336,7 +336,7 @@ struct TileLds {
 };
 
 template <typename T, int HD>
-__host__ __device__ inline TileLds tile_lds(int C, int tile, int waves) {
+__host__ __device__ inline TileLds tile_lds(int C, int tile, int waves, bool with_k = true) {
   typedef QkShape<T, HD> S;
   typedef typename PartialT<T>::type PT;
   TileLds L;
@@ -346,7 +346,7 @@ __host__ __device__ inline TileLds tile_lds(int C, int tile, int waves) {
   L.ldo = HD + 16 / (int)sizeof(PT);
   size_t off = 0;
   L.k_off = off;
-  off += (size_t)L.Cq * L.ldk * sizeof(T);
+  if (with_k) off += (size_t)L.Cq * L.ldk * sizeof(T);
   L.v_off = off;
   off += (size_t)HD * L.ldv * sizeof(T);
   off = (off + 15) / 16 * 16;
@@ -488,7 +488,8 @@ template <typename T, int HD, int NTM>
 __device__ void fwd_tile_units(const AttnArgs& a, const TileLds& L, const T* ks, const T* vt,
                                const int64_t* mq, const int64_t* mpos, const int32_t* mslot,
                                int nreq, int64_t blk, int rows, int wave, int nwaves, int lane,
-                               typename PartialT<T>::type* so) {
+                               typename PartialT<T>::type* so, const T* kg = nullptr,
+                               int64_t kg_stride = 0) {
   typedef QkShape<T, HD, NTM> S;
   typedef typename S::Op Op;
   typedef typename S::frag frag;
@@ -540,7 +541,10 @@ __device__ void fwd_tile_units(const AttnArgs& a, const TileLds& L, const T* ks,
           for (int d = 0; d < DS; ++d) s[mt] = Op::mma(kreg[mt][d], qf[d], s[mt]);
         } else {
           frag kf[DS];
-          load_row_frags<E>(ks + (mt * 16 + col) * L.ldk + E * grp, kf);
+          if (kg)  // key rows straight from memory (rows past the block repeat its last)
+            load_row_frags<E>(kg + (int64_t)min(mt * 16 + col, rows - 1) * kg_stride + E * grp, kf);
+          else
+            load_row_frags<E>(ks + (mt * 16 + col) * L.ldk + E * grp, kf);
 #pragma unroll
           for (int d = 0; d < DS; ++d) s[mt] = Op::mma(kf[d], qf[d], s[mt]);
         }
@@ -688,7 +692,9 @@ __global__ void __launch_bounds__(256, PISA_ATTN_WAVES) attn_fwd_tile_kernel(Att
   }
 }
 
-// One request (slot) per workgroup of one wave (decode and other short queries).
+// One request (slot) per workgroup of one wave (decode and other short queries):
+// the key rows are read straight from memory as MFMA operands and the partial
+// rows stored directly, so only V^T takes LDS and more workgroups fit a CU.
 template <typename T, int HD, int NTM>
 __global__ void __launch_bounds__(64, 2) attn_fwd_tile_direct_kernel(AttnArgs a, int64_t slots) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -697,8 +703,7 @@ __global__ void __launch_bounds__(64, 2) attn_fwd_tile_direct_kernel(AttnArgs a,
   const RowInfo ri = row_info(a, slot);
   const int64_t blk = slot_block(a, slot);
   if (!slot_visible(a, blk, ri.pos)) return;
-  const TileLds L = tile_lds<T, HD>(a.C, 1, 1);
-  T* ks = reinterpret_cast<T*>(smem + L.k_off);
+  const TileLds L = tile_lds<T, HD>(a.C, 1, 0, false);
   T* vt = reinterpret_cast<T*>(smem + L.v_off);
   int64_t* mq = reinterpret_cast<int64_t*>(smem + L.q_off);
   int64_t* mpos = reinterpret_cast<int64_t*>(smem + L.pos_off);
@@ -709,10 +714,15 @@ __global__ void __launch_bounds__(64, 2) attn_fwd_tile_direct_kernel(AttnArgs a,
     mslot[0] = (int32_t)slot;
   }
   const int rows = (int)min((int64_t)a.C, (int64_t)a.N - blk * a.C);
-  stage_tile<T, HD>(a, ri.b, ri.h, blk, rows, ks, vt, L, threadIdx.x, blockDim.x);
+  const T* kb = static_cast<const T*>(a.k) + (int64_t)ri.b * a.k_batch + blk * a.C * a.k_token +
+                (int64_t)ri.h * HD;
+  const T* vb = static_cast<const T*>(a.v) + (int64_t)ri.b * a.v_batch + blk * a.C * a.v_token +
+                (int64_t)ri.h * HD;
+  stage_transposed<T, HD>(vb, a.v_token, rows, L.Cq, vt, L.ldv, threadIdx.x, blockDim.x);
   __syncthreads();
-  fwd_tile_units<T, HD, NTM>(a, L, ks, vt, mq, mpos, mslot, 1, blk, rows, 0, 1, threadIdx.x & 63,
-                             reinterpret_cast<typename PartialT<T>::type*>(smem + L.o_off));
+  // (the LDS key tile argument is unused when the key rows come from memory)
+  fwd_tile_units<T, HD, NTM>(a, L, vt, vt, mq, mpos, mslot, 1, blk, rows, 0, 1, threadIdx.x & 63,
+                             nullptr, kb, a.k_token);
 }
 
 // Merge the K partials of each (batch, token, query head) in slot order with
@@ -1748,7 +1758,7 @@ static void launch_fwd_tile_n(const AttnArgs& a, bool grouped, int64_t slots, hi
     allow_lds((const void*)attn_fwd_tile_kernel<T, HD, NTM>, lds);
     PISA_TIMED("attn_fwd", stream, hipLaunchKernelGGL((attn_fwd_tile_kernel<T, HD, NTM>), dim3(grid_size()), dim3(256), lds, stream, a));
   } else if (slots > 0) {
-    const size_t lds = tile_lds<T, HD>(a.C, 1, 1).bytes;
+    const size_t lds = tile_lds<T, HD>(a.C, 1, 0, false).bytes;
     allow_lds((const void*)attn_fwd_tile_direct_kernel<T, HD, NTM>, lds);
     PISA_TIMED("attn_fwd_direct", stream, hipLaunchKernelGGL((attn_fwd_tile_direct_kernel<T, HD, NTM>), dim3(slots), dim3(64), lds, stream, a, slots));
   }
