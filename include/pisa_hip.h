@@ -169,6 +169,21 @@ int pisa_leaf_scores(const pisa_qk_desc* qk, const pisa_select_params* p, const 
                      int64_t positions_stride_batch, float* scores, void* workspace,
                      size_t workspace_bytes, void* stream);
 
+/* Workspace bytes for pisa_bsa_select: the block means [B, ceil(N / C), Hkv, D]. */
+size_t pisa_bsa_workspace_size(const pisa_qk_desc* qk, int32_t block_size);
+
+/* Flat BSA block selection, the reference's benchmark baseline: int64
+ * [B, Tq, Hkv, topk] ids in the streaming network's rank order, -1 padded.
+ * Replaces select_bsa, ops/flash_sparse_attn/bsa/bsa_triton.py:87-114 (kernel
+ * :13-84; equations bsa_select, bsa_torch.py:61-106, network streaming_topk
+ * :28-58).  block_size <= 128, topk <= 64, head_dim in {16, 32, 64, 128}, at
+ * most 32 query heads per kv head; block_size < 2 topk widens the comparison
+ * tile as the Torch path does. */
+int pisa_bsa_select(const pisa_qk_desc* qk, int32_t block_size, int32_t topk, int32_t force_first,
+                    int32_t force_recent, const void* q, const void* k, const int64_t* positions,
+                    int64_t positions_stride_batch, int64_t* out, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
 /* Workspace bytes for the attention entry points. */
 size_t pisa_attention_workspace_size(const pisa_attn_desc* a, int32_t backward);
 

@@ -62,8 +62,9 @@ def select_blocks(q, k, method="pisa", block_size=64, topk=8, cu_seqlens=None, q
     if method != "bsa" and force_recent == 0:
         raise ValueError("causal pyramid routing requires force_recent >= 1")
     if method == "bsa":
-        raise ValueError("method 'bsa' (flat block-sparse routing baseline) is not provided by "
-                         "nlogn_pisa_amd")
+        from .bsa import bsa_fn
+        return bsa_fn(q, k, block_size, topk, cu_seqlens=cu_seqlens, query_offset=query_offset,
+                      force_first=force_first, force_recent=force_recent, backend=backend)
     if branching < 2 or branching & (branching - 1):
         raise ValueError("branching must be a power of two >= 2")
     if routing_schedule == "auto":

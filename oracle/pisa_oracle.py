@@ -28,7 +28,8 @@ __all__ = [
     "round_storage", "mean_pool", "build_pyramid", "routing_geometry", "force_mask",
     "routing_masks", "block_scores", "network_topk", "pyramid_select", "query_positions",
     "sparse_attention", "sparse_attention_dense", "sparse_attention_backward",
-    "leaf_scores", "flops_visible", "rotary", "rotary_frequency", "SENTINEL_FORCED",
+    "leaf_scores", "flops_visible", "rotary", "rotary_frequency", "bitonic_merge",
+    "streaming_topk", "bsa_tile_width", "bsa_scores", "bsa_select", "SENTINEL_FORCED",
     "SENTINEL_INVALID",
 ]
 
@@ -551,3 +552,130 @@ def rotary(x, frequency, positions):
     cos, sin = np.cos(angles), np.sin(angles)
     return np.concatenate((first * cos - second * sin, first * sin + second * cos), -1)
 
+
+
+# --------------------------------------------------------------------------- flat BSA routing
+
+
+def bitonic_merge(scores, ids, stage, descending):
+    """One merge of the streaming network (``ops/flash_sparse_attn/bsa/bsa_torch.py:8-25``).
+
+    Lanes pair at distances 2**(stage-1) .. 1; a pair exchanges iff
+    ``(lower > upper) != descending`` where ``descending`` is the lane's bit
+    ``stage`` (``None``, alternating runs) or the given constant.  ids ride along.
+    """
+    width = scores.shape[-1]
+    lanes = np.arange(width)
+    direction = ((lanes & (1 << stage)) != 0) if descending is None else np.full(width, descending)
+    for exponent in range(stage - 1, -1, -1):
+        distance = 1 << exponent
+        partner = lanes ^ distance
+        lower = lanes & ~distance
+        upper = lower | distance
+        exchange = (scores[..., lower] > scores[..., upper]) != direction
+        scores = np.where(exchange, scores[..., partner], scores)
+        ids = np.where(exchange, ids[..., partner], ids)
+    return scores, ids
+
+
+def streaming_topk(scores, ids, topk, tile_size):
+    """Top-``topk`` ids in network rank order over tiles of ``tile_size`` lanes
+    (``bsa_torch.py:28-58``): each tile is sorted into alternating runs, its best half
+    merged with the retained best half of the tiles before; tiles holding no id >= 0
+    are skipped; the tail tile pads with score 0 and id -1."""
+    if topk < 1 or tile_size < 2 * topk or tile_size & (tile_size - 1):
+        raise ValueError("tile_size must be a power of two and at least 2 * topk")
+    scores = np.asarray(scores)
+    ids = np.asarray(ids)
+    if scores.shape != ids.shape or scores.shape[-1] < 1:
+        raise ValueError("scores and ids must have the same nonempty shape")
+    stages = tile_size.bit_length() - 1
+    lead = scores.shape[:-1]
+    retained_scores = np.full(lead + (tile_size,), -1, dtype=scores.dtype)
+    retained_ids = np.zeros(lead + (tile_size,), dtype=ids.dtype)
+    half = tile_size // 2
+    for start in range(0, scores.shape[-1], tile_size):
+        values = scores[..., start:start + tile_size]
+        indices = ids[..., start:start + tile_size]
+        active = (indices >= 0).any(-1, keepdims=True)
+        padding = tile_size - values.shape[-1]
+        pad = [(0, 0)] * len(lead) + [(0, padding)]
+        values = np.pad(values, pad, constant_values=0)
+        indices = np.pad(indices, pad, constant_values=-1)
+        for stage in range(1, stages):
+            values, indices = bitonic_merge(values, indices, stage, None)
+        if start:
+            values, indices = bitonic_merge(values, indices, stages, False)
+            values = np.concatenate((retained_scores[..., :half], values[..., half:]), -1)
+            indices = np.concatenate((retained_ids[..., :half], indices[..., half:]), -1)
+        values, indices = bitonic_merge(values, indices, stages, True)
+        retained_scores = np.where(active, values, retained_scores)
+        retained_ids = np.where(active, indices, retained_ids)
+    return retained_ids[..., :topk]
+
+
+def bsa_tile_width(block_size, topk):
+    """Comparison tile of flat routing: the power of two >= max(block_size, 2 topk)
+    (``bsa_torch.py:74``)."""
+    return 1 << (max(block_size, 2 * topk) - 1).bit_length()
+
+
+def bsa_scores(q, k, block_size, positions, force_first, force_recent, dtype="fp32"):
+    """Per-block routing scores [B, Tq, Hkv, M] and ids (-1 beyond the current block).
+
+    Restates ``bsa_torch.py:61-103``: summaries are the block means of k
+    (``mean_pool``), queries are scaled by D^-1/2 in float32 and rounded to the
+    storage dtype, each head's logits are normalised by the log-sum-exp over the
+    complete blocks (0 when none is complete), a block's score is the sum over the
+    group's heads of exp(logit - normaliser) for blocks before the current one, the
+    number of heads for forced blocks (block 0 with ``force_first``, the current
+    block and the ``force_recent - 1`` before it), and 0 otherwise.  Raises the
+    reference's ValueError when a token has more distinct forced blocks than
+    ``topk`` would hold (checked by the caller, ``bsa_select``).
+    """
+    compute = np.float64 if dtype == "fp64" else np.float32
+    q = np.asarray(q)
+    batch, length, heads_q, dim = q.shape
+    heads = k.shape[2]
+    groups = heads_q // heads
+    summaries = mean_pool(k, block_size, dtype).astype(compute)
+    blocks = np.arange(summaries.shape[1])
+    scale = compute(dim ** -0.5)
+    query = round_storage(np.asarray(q, dtype=compute) * scale, dtype).astype(compute)
+    query = query.reshape(batch, length, heads, groups, dim)
+    logits = np.einsum("bthgd,bmhd->bthgm", query, summaries).astype(compute)
+    position = np.asarray(positions, dtype=np.int64)
+    position = np.broadcast_to(position, (batch, length))[:, :, None, None]
+    current = position // block_size
+    complete = (position + 1) // block_size
+    visible = blocks < complete[..., None]
+    masked = np.where(visible, logits, -np.inf)
+    peak = masked.max(-1, keepdims=True)
+    safe = np.where(np.isfinite(peak), peak, 0)
+    with np.errstate(divide="ignore"):
+        normalizer = np.log(np.exp(masked - safe).sum(-1, keepdims=True)) + safe
+    normalizer = np.where(complete[..., None] > 0, normalizer, 0).astype(compute)
+    forced = np.zeros(current.shape[:2] + (1, blocks.size), dtype=bool)
+    if force_first:
+        forced |= blocks == 0
+    for recent in range(force_recent):
+        forced |= (current >= recent) & (blocks == current - recent)
+    valid = blocks <= current
+    candidate = np.where((blocks < current)[..., None, :], logits, -np.inf)
+    probabilities = np.exp(candidate - normalizer).astype(compute)
+    probabilities = np.where(forced[..., None, :], compute(1), probabilities)
+    scores = probabilities.sum(-2, dtype=compute)
+    ids = np.where(valid, blocks, -1)
+    ids = np.broadcast_to(ids, scores.shape).astype(np.int64)
+    required = (forced & valid).sum(-1)
+    return scores, ids, required
+
+
+def bsa_select(q, k, block_size, topk, positions, force_first, force_recent, dtype="fp32"):
+    """Flat BSA block selection (``bsa_torch.py:61-106``): ids [B, Tq, Hkv, topk] in
+    network rank order, -1 padded."""
+    scores, ids, required = bsa_scores(q, k, block_size, positions, force_first,
+                                       force_recent, dtype)
+    if (required > topk).any():
+        raise ValueError("topk is smaller than the number of required distinct blocks")
+    return streaming_topk(scores, ids, topk, bsa_tile_width(block_size, topk))

@@ -103,3 +103,34 @@ def adjudicate(gpu_ids, gpu_trace, oracle_ids, oracle_trace, tol=1e-4):
         else:
             failures.append((int(r), int(h), verdict[1]))
     return rows, len(bad), exempt, failures
+
+
+def adjudicate_flat(got, want, scores, ids, tol=1e-4):
+    """Flat (BSA) selections: (rows that differ, exempt rows, failing rows).
+
+    ``scores``/``ids`` are the oracle's per-block scores and ids [..., M] of each
+    row (``oracle.bsa_scores``).  A differing row is exempt when, slot by slot,
+    the oracle scores of the two ids (0 for the -1 padding, as the network pads)
+    are closer than ``tol`` times the row's largest score: the two selections
+    then differ only by near-tied blocks trading places.
+    """
+    got = np.asarray(got).reshape(-1, got.shape[-1])
+    want = np.asarray(want).reshape(-1, want.shape[-1])
+    scores = np.asarray(scores).reshape(-1, scores.shape[-1])
+    ids = np.asarray(ids).reshape(-1, ids.shape[-1])
+    bad = np.flatnonzero((got != want).any(-1))
+    exempt, failures = 0, []
+    for r in bad:
+        lookup = {-1: 0.0}
+        for i, s in zip(ids[r].tolist(), scores[r].tolist()):
+            if i >= 0:
+                lookup[i] = s
+        scale = float(np.abs(scores[r]).max())
+        ok = scale > 0 and all(
+            a in lookup and b in lookup and abs(lookup[a] - lookup[b]) < tol * scale
+            for a, b in zip(got[r].tolist(), want[r].tolist()))
+        if ok:
+            exempt += 1
+        else:
+            failures.append(int(r))
+    return len(bad), exempt, failures
