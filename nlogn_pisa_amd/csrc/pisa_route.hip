@@ -23,6 +23,10 @@ namespace pisa {
 
 constexpr int kMaxWidth = 512;
 
+// Fused-schedule launches with at least this many items (batch x tokens x kv
+// heads) run one wave per item.
+constexpr int64_t kFusedWaveItems = 8192;
+
 // Support tiles of the MFMA routing in flight ahead of the one being scored.
 #ifndef PISA_ROUTE_DEPTH
 #define PISA_ROUTE_DEPTH 2
@@ -546,7 +550,7 @@ __device__ __forceinline__ void tile_scores(const f4& sv, const TileMeta<RR>& m,
   }
 }
 
-template <typename T, int HD, int RR, int MODE>
+template <typename T, int HD, int RR, int MODE, bool FUSED>
 __global__ void __launch_bounds__(64) route_grouped_kernel(RouteArgs a) {
   typedef QkShape<T, HD> S;
   typedef typename S::Op Op;
@@ -605,7 +609,7 @@ __global__ void __launch_bounds__(64) route_grouped_kernel(RouteArgs a) {
       const bool forced = valid && is_forced(id, leaf, span_blocks, a.force_first, a.force_recent);
       const bool scoreable = valid && !forced && !identity;
       sc_s[e] = valid ? (forced ? kForced : 0.f) : kInvalid;
-      if (level == 0) {
+      if (level == 0 && !FUSED) {
         a.cand[(int64_t)item * width + e] = id;
         a.scoreable[(int64_t)item * width + e] = scoreable ? 1 : 0;
       } else if (scoreable) {
@@ -613,10 +617,20 @@ __global__ void __launch_bounds__(64) route_grouped_kernel(RouteArgs a) {
       }
     }
     __syncthreads();
-    if (level == 0) return;
+    if (level == 0 && !FUSED) return;
 
-    // score the scoreable candidates, 16 support rows at a time
     const int nlist = cnt_s[1];
+    if (FUSED && level == 0 && !own) {
+      // fused schedule: this wave scores the leaf candidates' key blocks on the
+      // matrix cores, the next block loading while one is scored
+      if constexpr (sizeof(T) == 2 && HD >= 32) {
+        if (a.C <= 64)
+          leaf_scores_mfma<T, HD, 4, true>(a, qb, b, h, ids_s, list_s, sc_s, nlist, 0, 1, lane);
+        else
+          leaf_scores_mfma<T, HD, 8, false>(a, qb, b, h, ids_s, list_s, sc_s, nlist, 0, 1, lane);
+      }
+    } else {
+    // score the scoreable candidates, 16 support rows at a time
     const int src_level = own ? level : level - 1;
     const T* base = static_cast<const T*>(a.summary) + b * a.sum_batch +
                     ((int64_t)a.offsets[src_level] * a.Hkv + h) * HD;
@@ -656,6 +670,7 @@ __global__ void __launch_bounds__(64) route_grouped_kernel(RouteArgs a) {
         if (mt0 + p < ntile)
           tile(mt0 + p, xb[p], xb[(p + DEPTH) % (DEPTH + 1)], mb[p], mb[(p + DEPTH) % (DEPTH + 1)]);
     }
+    }
     __syncthreads();
 
     const int net = next_pow2(width);
@@ -688,6 +703,10 @@ __global__ void __launch_bounds__(64) route_grouped_kernel(RouteArgs a) {
     const int sel = idv[0];
     if (a.trace && lane < K)
       a.trace[((int64_t)item * levels_traced + (a.top - level)) * K + lane] = sel;
+    if (level == 0) {  // fused schedule: the final ids (top_k_pyramid_torch.py:176)
+      if (lane < K) a.out[(int64_t)item * K + lane] = (sel < 0 || (int64_t)sel * a.C > pos) ? -1 : sel;
+      return;
+    }
     __syncthreads();
     if (lane < K)
       for (int c = 0; c < a.branching; ++c)
@@ -787,59 +806,77 @@ static int launch_route_t(const RouteArgs& a, int64_t items, int threads, hipStr
   }
 }
 
-template <typename T, int HD, int RR, int MODE>
+template <typename T, int HD, int RR, int MODE, bool FUSED>
 static void launch_route_rm(const RouteArgs& a, int64_t items, hipStream_t stream) {
-  PISA_TIMED("route", stream, hipLaunchKernelGGL((route_grouped_kernel<T, HD, RR, MODE>), dim3(items), dim3(64), 0, stream, a));
+  PISA_TIMED("route", stream, hipLaunchKernelGGL((route_grouped_kernel<T, HD, RR, MODE, FUSED>), dim3(items), dim3(64), 0, stream, a));
 }
 
-// One kernel per (support rows per candidate, scoring mode).
-template <typename T, int HD>
+// One kernel per (support rows per candidate, scoring mode); the fused
+// schedule's raw-key leaf exists for 16-bit keys with D >= 32 only.
+template <typename T, int HD, bool FUSED>
 static void launch_route_hd(const RouteArgs& a, int64_t items, hipStream_t stream) {
-  if (a.method == PISA_METHOD_PISA1) return launch_route_rm<T, HD, 1, kModeOwn>(a, items, stream);
-  const bool lse = a.method == PISA_METHOD_LSE;
-  switch (a.branching) {
-    case 2:
-      if (lse) launch_route_rm<T, HD, 2, kModeLse>(a, items, stream);
-      else launch_route_rm<T, HD, 2, kModeBinary>(a, items, stream);
-      break;
-    case 4:
-      if (lse) launch_route_rm<T, HD, 4, kModeLse>(a, items, stream);
-      else launch_route_rm<T, HD, 4, kModeMoments>(a, items, stream);
-      break;
-    default:
-      if (lse) launch_route_rm<T, HD, 8, kModeLse>(a, items, stream);
-      else launch_route_rm<T, HD, 8, kModeMoments>(a, items, stream);
-      break;
+  if (a.method == PISA_METHOD_PISA1) return launch_route_rm<T, HD, 1, kModeOwn, FUSED>(a, items, stream);
+  if constexpr (!FUSED || (sizeof(T) == 2 && HD >= 32)) {
+    const bool lse = a.method == PISA_METHOD_LSE;
+    switch (a.branching) {
+      case 2:
+        if (lse) launch_route_rm<T, HD, 2, kModeLse, FUSED>(a, items, stream);
+        else launch_route_rm<T, HD, 2, kModeBinary, FUSED>(a, items, stream);
+        break;
+      case 4:
+        if (lse) launch_route_rm<T, HD, 4, kModeLse, FUSED>(a, items, stream);
+        else launch_route_rm<T, HD, 4, kModeMoments, FUSED>(a, items, stream);
+        break;
+      default:
+        if (lse) launch_route_rm<T, HD, 8, kModeLse, FUSED>(a, items, stream);
+        else launch_route_rm<T, HD, 8, kModeMoments, FUSED>(a, items, stream);
+        break;
+    }
   }
 }
 
-template <typename T>
+template <typename T, bool FUSED>
 static int launch_route_grouped(const RouteArgs& a, int64_t items, hipStream_t stream) {
   switch (a.D) {
-    case 16: launch_route_hd<T, 16>(a, items, stream); break;
-    case 32: launch_route_hd<T, 32>(a, items, stream); break;
-    case 64: launch_route_hd<T, 64>(a, items, stream); break;
-    default: launch_route_hd<T, 128>(a, items, stream); break;
+    case 16: launch_route_hd<T, 16, FUSED>(a, items, stream); break;
+    case 32: launch_route_hd<T, 32, FUSED>(a, items, stream); break;
+    case 64: launch_route_hd<T, 64, FUSED>(a, items, stream); break;
+    default: launch_route_hd<T, 128, FUSED>(a, items, stream); break;
   }
   return check_launch("route");
 }
 
-// The MFMA routing serves the grouped schedule (level 0 left to the leaf kernel)
-// for D in {16, 32, 64, 128}, G <= 16, b <= 8 and 16-byte aligned rows.
-static bool route_mfma_path(const RouteArgs& a, int es) {
+// The one-wave MFMA routing serves the grouped schedule (level 0 left to the
+// leaf kernel) for D in {16, 32, 64, 128}, G <= 16, b <= 8 and 16-byte aligned
+// rows, and the fused schedule of many items (prefill): its wave then scores the
+// leaf too (16-bit keys with D >= 32, or the leaf means for pisa1).  The fused
+// schedule of few items (decode) spreads each item over several waves instead.
+static bool route_mfma_path(const RouteArgs& a, int64_t items, int es) {
   const bool dim = a.D == 16 || a.D == 32 || a.D == 64 || a.D == 128;
   const bool ptrs = (((uintptr_t)a.q | (uintptr_t)a.summary) & 15) == 0;
   const bool strides = ((a.q_batch | a.q_token | a.sum_batch) * es) % 16 == 0;
-  return !a.fused && dim && a.G <= 16 && a.branching <= 8 && ptrs && strides;
+  const bool base = dim && a.G <= 16 && a.branching <= 8 && ptrs && strides;
+  if (!a.fused) return base;
+  const bool keys = ((uintptr_t)a.key & 15) == 0 && ((a.key_batch | a.key_token) * es) % 16 == 0;
+  const bool leaf = a.method == PISA_METHOD_PISA1 || (es == 2 && a.D >= 32 && keys);
+  return base && leaf && items >= kFusedWaveItems;
 }
 
 int launch_route(int dtype, const RouteArgs& a, int64_t items, int threads, hipStream_t stream) {
   if (items == 0) return PISA_OK;
-  if (route_mfma_path(a, dtype_size(dtype))) {
+  if (route_mfma_path(a, items, dtype_size(dtype))) {
+    if (a.fused) {
+      switch (dtype) {
+        case PISA_F32: return launch_route_grouped<float, true>(a, items, stream);
+        case PISA_F16: return launch_route_grouped<f16_t, true>(a, items, stream);
+        case PISA_BF16: return launch_route_grouped<bf16_t, true>(a, items, stream);
+        default: return fail(PISA_ERR_INVALID, "unknown dtype %d", dtype);
+      }
+    }
     switch (dtype) {
-      case PISA_F32: return launch_route_grouped<float>(a, items, stream);
-      case PISA_F16: return launch_route_grouped<f16_t>(a, items, stream);
-      case PISA_BF16: return launch_route_grouped<bf16_t>(a, items, stream);
+      case PISA_F32: return launch_route_grouped<float, false>(a, items, stream);
+      case PISA_F16: return launch_route_grouped<f16_t, false>(a, items, stream);
+      case PISA_BF16: return launch_route_grouped<bf16_t, false>(a, items, stream);
       default: return fail(PISA_ERR_INVALID, "unknown dtype %d", dtype);
     }
   }
