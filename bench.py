@@ -65,7 +65,7 @@ def copy_probe():
 def query_window(tokens, row_bytes):
     """Query tokens per bucketing window (mirrors query_window in csrc/pisa_capi.hip)."""
     w = 256
-    while w * 2 * max(row_bytes, 1) <= (8 << 20):
+    while w * 2 * max(row_bytes, 1) <= (128 << 20):
         w *= 2
     return max(1, min(w, tokens))
 
@@ -75,8 +75,7 @@ def tile_count(w, valid, ids, elem):
     window of query tokens over the flattened (batch, token) axis."""
     import torch
     blocks = math.ceil(w.keys / w.block_size)
-    G = w.query_heads // w.key_heads
-    window = query_window(w.batch * w.tokens, G * w.head_dim * elem)
+    window = query_window(w.batch * w.tokens, w.query_heads * w.head_dim * elem)
     windows = math.ceil(w.batch * w.tokens / window)
     dev = ids.device
     b = torch.arange(w.batch, device=dev)[:, None, None, None]

@@ -26,9 +26,9 @@ int padded_group(int g) { return next_pow2(g); }
 
 namespace pisa {
 
-// Window budget: q bytes of one kv head per window (0: a single window).
+// Window budget: q bytes of all heads per window (0: a single window).
 #ifndef PISA_WINDOW_BYTES
-#define PISA_WINDOW_BYTES (8 << 20)
+#define PISA_WINDOW_BYTES (128 << 20)
 #endif
 
 int query_window(int64_t tokens, int64_t row_bytes) {
@@ -96,7 +96,7 @@ int plan_select(const pisa_qk_desc* qk, const pisa_select_params* p, SelectPlan&
   pl.slots = pl.items * pl.W;
   pl.groups = (int64_t)qk->batch * qk->key_heads * pl.M0;
   const int64_t flat = (int64_t)qk->batch * qk->query_tokens;
-  pl.window = query_window(flat, (int64_t)G * D * dtype_size(qk->dtype));
+  pl.window = query_window(flat, (int64_t)qk->query_heads * D * dtype_size(qk->dtype));
   pl.window_slots = (int64_t)pl.window * qk->key_heads * pl.W;
   return PISA_OK;
 }
@@ -264,7 +264,7 @@ namespace {
 
 int leaf_window(const pisa_qk_desc* qk) {
   return query_window((int64_t)qk->batch * qk->query_tokens,
-                      (int64_t)(qk->query_heads / qk->key_heads) * qk->head_dim * dtype_size(qk->dtype));
+                      (int64_t)qk->query_heads * qk->head_dim * dtype_size(qk->dtype));
 }
 
 void carve_leaf(const pisa_qk_desc* qk, int block_size, int width, Carve& c, uint8_t** mask,
@@ -390,7 +390,7 @@ int plan_attn(const pisa_attn_desc* d, AttnPlan& pl) {
   pl.groups = (int64_t)d->batch * d->key_heads * pl.M0;
   pl.Cp = (d->block_size + 15) / 16 * 16;
   pl.grouped = pl.slots >= 4 * pl.groups;
-  pl.window = query_window((int64_t)d->batch * d->query_tokens, (int64_t)pl.G * d->head_dim * es);
+  pl.window = query_window((int64_t)d->batch * d->query_tokens, (int64_t)d->query_heads * d->head_dim * es);
   pl.window_slots = (int64_t)pl.window * d->key_heads * d->topk;
   return PISA_OK;
 }
