@@ -11,7 +11,6 @@ using namespace pisa;
 
 namespace {
 
-constexpr int kLeafTile = 256;  // requests per leaf tile (one key-block load each)
 constexpr int kAttnTile = 256;  // requests per attention tile
 
 bool pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
@@ -66,7 +65,9 @@ struct SelectPlan {
   int M0;
   int G;
   int window;            // query tokens bucketed and scored per leaf pass
-  int64_t window_slots;  // slots of one window
+  int64_t window_slots;  // leaf requests of one window
+  int span;              // sibling candidates (consecutive blocks) per leaf request
+  int spans;             // request groups per (batch, kv head)
 };
 
 int plan_select(const pisa_qk_desc* qk, const pisa_select_params* p, SelectPlan& pl) {
@@ -94,10 +95,18 @@ int plan_select(const pisa_qk_desc* qk, const pisa_select_params* p, SelectPlan&
   pl.W = p->top == 0 ? p->first_width : p->branching * p->topk;
   pl.grouped = p->schedule == PISA_SCHEDULE_GROUPED && p->method != PISA_METHOD_PISA1;
   pl.slots = pl.items * pl.W;
-  pl.groups = (int64_t)qk->batch * qk->key_heads * pl.M0;
+  // The routing writes each parent's children side by side, so a leaf request
+  // can take a span of sibling blocks and read its query rows once for all of
+  // them (tile kernel layouts: 16-byte aligned query and key rows).
+  const int es = dtype_size(qk->dtype);
+  const bool aligned = ((qk->q_stride_batch | qk->q_stride_token | qk->k_stride_batch |
+                         qk->k_stride_token) * es) % 16 == 0;
+  pl.span = pl.grouped && aligned ? leaf_span(qk->dtype, D, p->block_size, p->branching, G) : 1;
+  pl.spans = (pl.M0 + pl.span - 1) / pl.span;
+  pl.groups = (int64_t)qk->batch * qk->key_heads * pl.spans;
   const int64_t flat = (int64_t)qk->batch * qk->query_tokens;
-  pl.window = query_window(flat, (int64_t)qk->query_heads * D * dtype_size(qk->dtype));
-  pl.window_slots = (int64_t)pl.window * qk->key_heads * pl.W;
+  pl.window = query_window(flat, (int64_t)qk->query_heads * D * es);
+  pl.window_slots = (int64_t)pl.window * qk->key_heads * pl.W / pl.span;
   return PISA_OK;
 }
 
@@ -135,6 +144,9 @@ LeafArgs leaf_args(const pisa_qk_desc* qk, int method, int block_size, int W, in
   a.W = W;
   a.M0 = M0;
   a.method = method;
+  a.span = 1;
+  a.spans = M0;
+  a.scoreable = nullptr;
   a.scale = (float)(1.0 / sqrt((double)qk->head_dim));
   a.tile_group = b.tile_group;
   a.tile_req = b.tile_req;
@@ -226,12 +238,15 @@ extern "C" int pisa_select(const pisa_qk_desc* qk, const pisa_select_params* p, 
   if (rc || !pl.grouped) return rc;
 
   // leaf scoring one window of query tokens at a time (flattened batch x token)
-  LeafRequests req{sb.cand, sb.scoreable, pl.W, qk->key_heads, qk->query_tokens, pl.M0};
+  LeafRequests req{sb.cand, sb.scoreable, pl.W, qk->key_heads, qk->query_tokens, pl.spans, pl.span};
   LeafArgs la = leaf_args(qk, p->method, p->block_size, pl.W, pl.M0, pl.G, q, k,
                           qk->k_stride_batch, qk->k_stride_token, qk->key_tokens, p->block_size,
                           sb.buckets, sb.scores);
+  la.span = pl.span;
+  la.spans = pl.spans;
+  la.scoreable = sb.scoreable;
   const int64_t flat = (int64_t)qk->batch * qk->query_tokens;
-  const int64_t per_token = (int64_t)qk->key_heads * pl.W;
+  const int64_t per_token = (int64_t)qk->key_heads * pl.W / pl.span;  // leaf requests per token
   for (int64_t u0 = 0; u0 < flat; u0 += pl.window) {
     const int64_t u1 = std::min<int64_t>(flat, u0 + pl.window);
     rc = bucket_leaf(req, u0 * per_token, u1 * per_token, sb.buckets, st);
@@ -335,7 +350,7 @@ extern "C" int pisa_leaf_scores(const pisa_qk_desc* qk, const pisa_select_params
   m.scoreable = mask;
   rc = launch_scoreable(m, st);
   if (rc) return rc;
-  LeafRequests req{candidates, mask, width, qk->key_heads, qk->query_tokens, M0};
+  LeafRequests req{candidates, mask, width, qk->key_heads, qk->query_tokens, M0, 1};
   const bool pisa1 = p->method == PISA_METHOD_PISA1;
   const int64_t row = (int64_t)qk->key_heads * qk->head_dim;
   LeafArgs la = leaf_args(qk, p->method, p->block_size, width, M0, G, q, pisa1 ? leaf_means : k,

@@ -39,13 +39,16 @@ constexpr int64_t kMinChunk = 2048;      // fewest slots per counting-sort workg
 
 struct LeafSrc {
   LeafRequests r;
-  __device__ __forceinline__ bool get(int64_t slot, int& group) const {
-    if (!r.scoreable[slot]) return false;
-    const int blk = r.cand[slot];
+  __device__ __forceinline__ bool get(int64_t req, int& group) const {
+    const int64_t slot = req * r.span;
+    int blk = -1;
+    for (int c = 0; c < r.span; ++c)
+      if (blk < 0 && r.scoreable[slot + c]) blk = r.cand[slot + c];
+    if (blk < 0) return false;
     const int64_t item = slot / r.width;
     const int h = (int)(item % r.heads);
     const int64_t b = item / ((int64_t)r.heads * r.tokens);
-    group = (int)((b * r.heads + h) * r.blocks + blk);
+    group = (int)((b * r.heads + h) * r.blocks + blk / r.span);
     return true;
   }
 };

@@ -85,10 +85,15 @@ __device__ __forceinline__ XcdTiles xcd_tiles(int ntiles) {
 }
 
 // Sources of bucketed requests.
+// Leaf requests: request i is the `span` consecutive slots i*span .. i*span+span-1
+// of one item, whose candidates are consecutive blocks (siblings under one
+// parent: the routing writes each parent's children side by side); it exists
+// when one of them is scoreable and belongs to group (batch, kv head,
+// block / span), `blocks` being the number of such spans per (batch, kv head).
 struct LeafRequests {
   const int32_t* cand;      // [B,T,Hkv,W]
   const uint8_t* scoreable; // [B,T,Hkv,W]
-  int32_t width, heads, tokens, blocks;
+  int32_t width, heads, tokens, blocks, span;
 };
 
 struct AttnRequests {
@@ -170,6 +175,8 @@ struct LeafArgs {
   const void* src;           // raw keys, or leaf means for PISA1
   int64_t src_batch, src_row;
   int T, Hkv, G, Gp, D, src_rows, C, W, M0, method;
+  int span, spans;           // sibling blocks per request, spans per (batch, kv head)
+  const uint8_t* scoreable;  // [B,T,Hkv,W] (read when span > 1)
   float scale;
   const int32_t* tile_group;
   const int32_t* tile_req;
@@ -222,6 +229,10 @@ int launch_route(int dtype, const RouteArgs& a, int64_t items, int threads, hipS
 int launch_final(const FinalArgs& a, hipStream_t stream);
 int launch_scoreable(const MaskArgs& a, hipStream_t stream);
 int launch_leaf(int dtype, const LeafArgs& a, hipStream_t stream);
+// Leaf requests per tile (one key-span load each).
+constexpr int kLeafTile = 256;
+// Sibling blocks per leaf request for the grouped schedule (1: one block each).
+int leaf_span(int dtype, int head_dim, int block_size, int branching, int group);
 int attn_check(const AttnArgs& a, int dtype, bool backward);
 // Forward partials (grouped tiles or one workgroup per slot), then the combine.
 int launch_attn_partials(int dtype, const AttnArgs& a, bool grouped, int64_t slots, hipStream_t stream);

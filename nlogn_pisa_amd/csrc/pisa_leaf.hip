@@ -172,22 +172,27 @@ __global__ void __launch_bounds__(256) leaf_kernel(LeafArgs a) {
 
 struct LeafLds {
   int Cq, ldk;
-  size_t k_off, q_off, slot_off, bytes;
+  size_t k_off, q_off, slot_off, mask_off, bytes;
 };
 
+// LDS of one tile: `span` key blocks of Cq rows (C padded to the MFMA key
+// granularity), then per request its query-row offset, first slot and the
+// scoreable mask of its span.
 template <typename T, int HD>
-__host__ __device__ inline LeafLds leaf_lds(int C, int tile) {
+__host__ __device__ inline LeafLds leaf_lds(int C, int tile, int span = 1) {
   typedef QkShape<T, HD> S;
   LeafLds L;
   L.Cq = (C + S::KQ - 1) / S::KQ * S::KQ;
   L.ldk = HD + S::PAD;
   size_t off = 0;
   L.k_off = off;
-  off += (size_t)L.Cq * L.ldk * sizeof(T);
+  off += (size_t)span * L.Cq * L.ldk * sizeof(T);
   off = (off + 15) / 16 * 16;
   L.q_off = off;
   off += (size_t)tile * 8;
   L.slot_off = off;
+  off += (size_t)tile * 4;
+  L.mask_off = off;
   off += (size_t)tile * 4;
   L.bytes = (off + 15) / 16 * 16;
   return L;
@@ -206,8 +211,14 @@ __host__ __device__ inline LeafLds leaf_lds(int C, int tile) {
 #define PISA_LEAF_WAVES 3
 #endif
 
-template <typename T, int HD, int NTM>
-__global__ void __launch_bounds__(256, (NTM <= 4 ? PISA_LEAF_WAVES : 2)) leaf_tile_kernel(LeafArgs a) {
+// Sibling blocks scored per request at most (a power of two).
+constexpr int kMaxSpan = 4;
+
+// SPAN: the most sibling blocks a request of this instance scores (1, or
+// kMaxSpan with the span read from the arguments).
+template <typename T, int HD, int NTM, int SPAN>
+__global__ void __launch_bounds__(SPAN > 1 ? 512 : 256, (NTM <= 4 ? PISA_LEAF_WAVES : 2))
+leaf_tile_kernel(LeafArgs a) {
   typedef QkShape<T, HD, NTM> S;
   typedef typename S::Op Op;
   typedef typename S::frag frag;
@@ -217,10 +228,12 @@ __global__ void __launch_bounds__(256, (NTM <= 4 ? PISA_LEAF_WAVES : 2)) leaf_ti
   constexpr bool KREG = PISA_LEAF_KREG && NTM <= 4 && NTM * QL * sizeof(T) <= 256;
   constexpr int KR = KREG ? NTM : 1;
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  const LeafLds L = leaf_lds<T, HD>(a.C, a.tile);
+  const int span = SPAN > 1 ? a.span : 1;
+  const LeafLds L = leaf_lds<T, HD>(a.C, a.tile, span);
   T* ks = reinterpret_cast<T*>(smem + L.k_off);
   int64_t* mq = reinterpret_cast<int64_t*>(smem + L.q_off);
   int32_t* mslot = reinterpret_cast<int32_t*>(smem + L.slot_off);
+  int32_t* mmask = reinterpret_cast<int32_t*>(smem + L.mask_off);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nwaves = (int)(blockDim.x >> 6);
   const int col = lane & 15, grp = lane >> 4;
@@ -242,29 +255,44 @@ __global__ void __launch_bounds__(256, (NTM <= 4 ? PISA_LEAF_WAVES : 2)) leaf_ti
   const XcdTiles walk = xcd_tiles(ntiles);
   for (int tile = walk.begin; tile < walk.end; tile += walk.step) {
     const int g = a.tile_group[tile];
-    const int blk = g % a.M0;
-    const int bh = g / a.M0;
+    const int blk0 = (g % a.spans) * span;  // first block of the tile's span
+    const int bh = g / a.spans;
     const int h = bh % a.Hkv;
     const int b = bh / a.Hkv;
     const int start = (tile - a.tile_off[g]) * a.tile;
     const int nreq = min(a.tile, a.counts[g] - start);
-    const int rows_valid = min(a.C, a.src_rows - blk * a.C);
+    // valid keys of each block of the span (0 past the last block)
+    int rows_valid[SPAN];
+#pragma unroll
+    for (int c = 0; c < SPAN; ++c)
+      rows_valid[c] = c < span ? max(0, min(a.C, a.src_rows - (blk0 + c) * a.C)) : 0;
     const int32_t* reqs = a.tile_req + (int64_t)tile * a.tile;
 
     __syncthreads();
     for (int i = tid; i < nreq; i += blockDim.x) {
-      const int slot = reqs[i];
+      const int64_t slot = (int64_t)reqs[i] * span;
       const int64_t item = slot / a.W;
       const int t = (int)((item / a.Hkv) % a.T);
       mq[i] = (int64_t)b * a.q_batch + (int64_t)t * a.q_token + (int64_t)h * a.G * HD;
-      mslot[i] = slot;
+      mslot[i] = (int32_t)slot;
+      int mask = 1;
+      if (SPAN > 1 && span > 1) {
+        mask = 0;
+        for (int c = 0; c < span; ++c) mask |= a.scoreable[slot + c] ? 1 << c : 0;
+      }
+      mmask[i] = mask;
     }
-    const T* kb = static_cast<const T*>(a.src) + b * a.src_batch + (int64_t)blk * a.C * a.src_row +
+    const T* kb = static_cast<const T*>(a.src) + b * a.src_batch + (int64_t)blk0 * a.C * a.src_row +
                   (int64_t)h * HD;
-    for (int idx = tid; idx < L.Cq * vpr; idx += blockDim.x) {
+    for (int idx = tid; idx < span * L.Cq * vpr; idx += blockDim.x) {
       const int r = idx / vpr, c = (idx % vpr) * vec;
+      const int child = r / L.Cq, rr = r - child * L.Cq;
+      int valid = rows_valid[0];
+#pragma unroll
+      for (int c = 1; c < SPAN; ++c) valid = child == c ? rows_valid[c] : valid;
       uint4 v = make_uint4(0, 0, 0, 0);
-      if (r < rows_valid) v = *reinterpret_cast<const uint4*>(kb + (int64_t)r * a.src_row + c);
+      if (rr < valid)
+        v = *reinterpret_cast<const uint4*>(kb + ((int64_t)child * a.C + rr) * a.src_row + c);
       *reinterpret_cast<uint4*>(ks + r * L.ldk + c) = v;
     }
     __syncthreads();
@@ -295,85 +323,99 @@ __global__ void __launch_bounds__(256, (NTM <= 4 ? PISA_LEAF_WAVES : 2)) leaf_ti
     auto fetch_k = [&](int k, frag (&f)[DS]) {
       fetch(k < nunits ? wave + nwaves * (k >> nsl) : items, k & (nsub - 1), f);
     };
-    const int lim = rows_valid - 4 * grp;  // this lane's keys 16 mt + i are valid below lim
-    float total = 0.f;  // this lane's row: head scores summed over the item's units
-    // unit k: scored from `cur`, loads unit k + DEPTH into `into` (the buffer
-    // unit k - 1 used); buffers rotate by unrolling, never by copies, so the
-    // loads in flight are not waited for early.  FULL: every key of the block
-    // is valid (no masks).
+    // this lane's row: head scores of each block of the span, summed over the item's units
+    float total[SPAN];
+#pragma unroll
+    for (int c = 0; c < SPAN; ++c) total[c] = 0.f;
+    // unit k: scored from `cur` against every block of the span, loads unit
+    // k + DEPTH into `into` (the buffer unit k - 1 used); buffers rotate by
+    // unrolling, never by copies, so the loads in flight are not waited for
+    // early.  FULL: every key of every block of the span is valid (no masks).
     auto unit = [&](auto full_tag, int k, frag (&cur)[DS], frag (&into)[DS]) {
       constexpr bool FULL = decltype(full_tag)::value;
       fetch_k(k + DEPTH, into);
       const int r = wave + nwaves * (k >> nsl), j = k & (nsub - 1);
-      f4 s[NTM];
-#pragma unroll
-      for (int mt = 0; mt < NTM; ++mt) {
-        s[mt] = f4{0.f, 0.f, 0.f, 0.f};
-        if (mt < NT) {
-          if constexpr (KREG) {
-#pragma unroll
-            for (int d = 0; d < DS; ++d) s[mt] = Op::mma(kreg[mt][d], cur[d], s[mt]);
-          } else {
-            frag kf[DS];
-            load_row_frags<E>(ks + (mt * 16 + col) * L.ldk + E * grp, kf);
-#pragma unroll
-            for (int d = 0; d < DS; ++d) s[mt] = Op::mma(kf[d], cur[d], s[mt]);
-          }
-        }
-      }
-      auto valid = [&](int mt, int i) { return mt < NT && (FULL || mt * 16 + i < lim); };
-      float head;
-      if (lse) {
-        float m = -INFINITY;
-#pragma unroll
-        for (int mt = 0; mt < NTM; ++mt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (valid(mt, i)) m = fmaxf(m, s[mt][i] * a.scale);
-        m = xor32_max(xor16_max(m));
-        float e = 0.f;
-#pragma unroll
-        for (int mt = 0; mt < NTM; ++mt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (valid(mt, i)) e += __expf(s[mt][i] * a.scale - m);
-        e = xor32_sum(xor16_sum(e));
-        head = m + __logf(e);
-      } else {
-        float s1 = 0.f, s2 = 0.f;
-#pragma unroll
-        for (int mt = 0; mt < NTM; ++mt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (valid(mt, i)) {
-              s1 += s[mt][i];
-              s2 = fmaf(s[mt][i], s[mt][i], s2);
-            }
-        s1 = xor32_sum(xor16_sum(s1));
-        s2 = xor32_sum(xor16_sum(s2));
-        if (pisa1) {
-          head = s1;  // one support row: the leaf mean, scale 1
-        } else {
-          const float cnt = (float)rows_valid;
-          const float mean = s1 / cnt;
-          const float var = fmaxf(s2 / cnt - mean * mean, 0.f);
-          head = a.scale * mean + half_scale2 * var;
-        }
-      }
       const int rho = (((r << nsl) + j) << 4) + col;
       const bool real = (rho >> gl) < nreq && (rho & (Gp - 1)) < a.G;
-      total += real ? head : 0.f;
-      if (j + 1 < nsub) return;
-      // item done: sum the head rows of each request (aligned lanes of a 16-lane row)
-      if (Gp >= 16) {
-        const float v = group_sum(total, 16);
-        if (lane == 0 && r < nreq) a.scores[mslot[r]] = v;
-      } else {
-        const float v = group_sum(total, Gp);
-        const int rq = ((r << 4) + col) >> gl;
-        if (grp == 0 && (col & (Gp - 1)) == 0 && rq < nreq) a.scores[mslot[rq]] = v;
+#pragma unroll
+      for (int c = 0; c < SPAN; ++c) {
+        if (c >= span || rows_valid[c] == 0) continue;
+        const T* kc = ks + c * L.Cq * L.ldk;
+        f4 s[NTM];
+#pragma unroll
+        for (int mt = 0; mt < NTM; ++mt) {
+          s[mt] = f4{0.f, 0.f, 0.f, 0.f};
+          if (mt < NT) {
+            if (KREG && SPAN == 1) {
+#pragma unroll
+              for (int d = 0; d < DS; ++d) s[mt] = Op::mma(kreg[mt][d], cur[d], s[mt]);
+            } else {
+              frag kf[DS];
+              load_row_frags<E>(kc + (mt * 16 + col) * L.ldk + E * grp, kf);
+#pragma unroll
+              for (int d = 0; d < DS; ++d) s[mt] = Op::mma(kf[d], cur[d], s[mt]);
+            }
+          }
+        }
+        const int lim = rows_valid[c] - 4 * grp;  // this lane's keys 16 mt + i are valid below lim
+        auto valid = [&](int mt, int i) { return mt < NT && (FULL || mt * 16 + i < lim); };
+        float head;
+        if (lse) {
+          float m = -INFINITY;
+#pragma unroll
+          for (int mt = 0; mt < NTM; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (valid(mt, i)) m = fmaxf(m, s[mt][i] * a.scale);
+          m = xor32_max(xor16_max(m));
+          float e = 0.f;
+#pragma unroll
+          for (int mt = 0; mt < NTM; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (valid(mt, i)) e += __expf(s[mt][i] * a.scale - m);
+          e = xor32_sum(xor16_sum(e));
+          head = m + __logf(e);
+        } else {
+          float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+          for (int mt = 0; mt < NTM; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (valid(mt, i)) {
+                s1 += s[mt][i];
+                s2 = fmaf(s[mt][i], s[mt][i], s2);
+              }
+          s1 = xor32_sum(xor16_sum(s1));
+          s2 = xor32_sum(xor16_sum(s2));
+          if (pisa1) {
+            head = s1;  // one support row: the leaf mean, scale 1
+          } else {
+            const float cnt = (float)rows_valid[c];
+            const float mean = s1 / cnt;
+            const float var = fmaxf(s2 / cnt - mean * mean, 0.f);
+            head = a.scale * mean + half_scale2 * var;
+          }
+        }
+        total[c] += real ? head : 0.f;
       }
-      total = 0.f;
+      if (j + 1 < nsub) return;
+      // item done: sum the head rows of each request (aligned lanes of a 16-lane
+      // row) and write the scores of its scoreable blocks
+#pragma unroll
+      for (int c = 0; c < SPAN; ++c) {
+        if (c >= span) continue;
+        if (Gp >= 16) {
+          const float v = group_sum(total[c], 16);
+          if (lane == 0 && r < nreq && ((mmask[r] >> c) & 1)) a.scores[mslot[r] + c] = v;
+        } else {
+          const float v = group_sum(total[c], Gp);
+          const int rq = ((r << 4) + col) >> gl;
+          if (grp == 0 && (col & (Gp - 1)) == 0 && rq < nreq && ((mmask[rq] >> c) & 1))
+            a.scores[mslot[rq] + c] = v;
+        }
+        total[c] = 0.f;
+      }
     };
     auto run = [&](auto full_tag) {
       frag qb[DEPTH + 1][DS];
@@ -385,34 +427,76 @@ __global__ void __launch_bounds__(256, (NTM <= 4 ? PISA_LEAF_WAVES : 2)) leaf_ti
           if (k0 + p < nunits) unit(full_tag, k0 + p, qb[p], qb[(p + DEPTH) % (DEPTH + 1)]);
       }
     };
-    if (rows_valid == NT * 16) run(std::true_type{});
+    bool full = NT * 16 == a.C;
+#pragma unroll
+    for (int c = 0; c < SPAN; ++c) full = full && (c >= span || rows_valid[c] == a.C);
+    if (full) run(std::true_type{});
     else run(std::false_type{});
   }
 }
 
+// Workgroups of a tile span's LDS above this many bytes hold eight waves (two
+// workgroups per CU still fit), smaller ones four.
+constexpr size_t kLeafWideLds = 48 << 10;
+
 template <typename T, int HD>
-static void launch_leaf_tile(const LeafArgs& a, int grid, hipStream_t stream) {
-  const LeafLds L = leaf_lds<T, HD>(a.C, a.tile);
+static void launch_leaf_tile(const LeafArgs& a, int cus, hipStream_t stream) {
+  const LeafLds L = leaf_lds<T, HD>(a.C, a.tile, a.span);
   const int nt = L.Cq / 16;
-  if (nt <= 2) {
-    allow_lds((const void*)leaf_tile_kernel<T, HD, 2>, L.bytes);
-    PISA_TIMED("leaf", stream, hipLaunchKernelGGL((leaf_tile_kernel<T, HD, 2>), dim3(grid), dim3(256), L.bytes, stream, a));
+  const bool wide = a.span > 1 && L.bytes > kLeafWideLds;  // 512-thread instances only
+  const dim3 block(wide ? 512 : 256);
+  const dim3 grid(cus * (wide ? 4 : 8));
+  if (a.span > 1) {  // spans need blocks of at most 64 keys (leaf_span)
+    if (nt <= 2) {
+      allow_lds((const void*)leaf_tile_kernel<T, HD, 2, kMaxSpan>, L.bytes);
+      PISA_TIMED("leaf", stream, hipLaunchKernelGGL((leaf_tile_kernel<T, HD, 2, kMaxSpan>), grid, block, L.bytes, stream, a));
+    } else {
+      allow_lds((const void*)leaf_tile_kernel<T, HD, 4, kMaxSpan>, L.bytes);
+      PISA_TIMED("leaf", stream, hipLaunchKernelGGL((leaf_tile_kernel<T, HD, 4, kMaxSpan>), grid, block, L.bytes, stream, a));
+    }
+  } else if (nt <= 2) {
+    allow_lds((const void*)leaf_tile_kernel<T, HD, 2, 1>, L.bytes);
+    PISA_TIMED("leaf", stream, hipLaunchKernelGGL((leaf_tile_kernel<T, HD, 2, 1>), grid, block, L.bytes, stream, a));
   } else if (nt <= 4) {
-    allow_lds((const void*)leaf_tile_kernel<T, HD, 4>, L.bytes);
-    PISA_TIMED("leaf", stream, hipLaunchKernelGGL((leaf_tile_kernel<T, HD, 4>), dim3(grid), dim3(256), L.bytes, stream, a));
+    allow_lds((const void*)leaf_tile_kernel<T, HD, 4, 1>, L.bytes);
+    PISA_TIMED("leaf", stream, hipLaunchKernelGGL((leaf_tile_kernel<T, HD, 4, 1>), grid, block, L.bytes, stream, a));
   } else {
-    allow_lds((const void*)leaf_tile_kernel<T, HD, 8>, L.bytes);
-    PISA_TIMED("leaf", stream, hipLaunchKernelGGL((leaf_tile_kernel<T, HD, 8>), dim3(grid), dim3(256), L.bytes, stream, a));
+    allow_lds((const void*)leaf_tile_kernel<T, HD, 8, 1>, L.bytes);
+    PISA_TIMED("leaf", stream, hipLaunchKernelGGL((leaf_tile_kernel<T, HD, 8, 1>), grid, block, L.bytes, stream, a));
   }
 }
 
+// Sibling blocks per request: the largest power of two <= branching (and
+// kMaxSpan) whose blocks take at most 256 key rows and, with the request
+// bookkeeping, 80 KB of LDS.  Spans serve head groups of up to four heads and
+// blocks of up to 64 keys: there the query rows dominate a tile's traffic and
+// the kernel keeps four waves per SIMD (measured: larger groups or 128-key
+// blocks ran slower).
+#ifndef PISA_LEAF_MAX_SPAN
+#define PISA_LEAF_MAX_SPAN kMaxSpan
+#endif
+int leaf_span(int dtype, int head_dim, int block_size, int branching, int group) {
+  const int es = dtype_size(dtype);
+  if (!es || (head_dim != 16 && head_dim != 32 && head_dim != 64 && head_dim != 128)) return 1;
+  if (group > 4 || block_size > 64) return 1;
+  const int E = es == 4 ? 1 : ((head_dim / 4) % 8 == 0 ? 8 : 4);
+  const int KQ = E == 8 ? 32 : 16;
+  const int cq = (block_size + KQ - 1) / KQ * KQ;
+  const int ldk = head_dim + 16 / es;
+  int span = 1;
+  while (span * 2 <= branching && span * 2 <= PISA_LEAF_MAX_SPAN && span * 2 * cq <= 256 &&
+         (size_t)span * 2 * cq * ldk * es + (size_t)kLeafTile * 16 <= (80u << 10))
+    span *= 2;
+  return span;
+}
+
 template <typename T>
-static void launch_leaf_tile_t(const LeafArgs& a, int grid, hipStream_t stream) {
+static void launch_leaf_tile_t(const LeafArgs& a, int cus, hipStream_t stream) {
   switch (a.D) {
-    case 16: launch_leaf_tile<T, 16>(a, grid, stream); break;
-    case 32: launch_leaf_tile<T, 32>(a, grid, stream); break;
-    case 64: launch_leaf_tile<T, 64>(a, grid, stream); break;
-    default: launch_leaf_tile<T, 128>(a, grid, stream); break;
+    case 16: launch_leaf_tile<T, 16>(a, cus, stream); break;
+    case 32: launch_leaf_tile<T, 32>(a, cus, stream); break;
+    case 64: launch_leaf_tile<T, 64>(a, cus, stream); break;
+    default: launch_leaf_tile<T, 128>(a, cus, stream); break;
   }
 }
 
@@ -437,13 +521,14 @@ int launch_leaf(int dtype, const LeafArgs& a, hipStream_t stream) {
   const int grid = cus * 8;
   if (leaf_tile_path(a, es)) {
     switch (dtype) {
-      case PISA_F32: launch_leaf_tile_t<float>(a, grid, stream); break;
-      case PISA_F16: launch_leaf_tile_t<f16_t>(a, grid, stream); break;
-      case PISA_BF16: launch_leaf_tile_t<bf16_t>(a, grid, stream); break;
+      case PISA_F32: launch_leaf_tile_t<float>(a, cus, stream); break;
+      case PISA_F16: launch_leaf_tile_t<f16_t>(a, cus, stream); break;
+      case PISA_BF16: launch_leaf_tile_t<bf16_t>(a, cus, stream); break;
       default: return fail(PISA_ERR_INVALID, "unknown dtype %d", dtype);
     }
     return check_launch("leaf");
   }
+  if (a.span != 1) return fail(PISA_ERR_UNSUPPORTED, "sibling leaf requests need the tile kernel");
   switch (dtype) {
     case PISA_F32:
       allow_lds((const void*)leaf_kernel<float>, lds);
