@@ -70,11 +70,30 @@ def query_window(tokens, row_bytes):
     return max(1, min(w, tokens))
 
 
-def tile_count(w, valid, ids, elem):
+def leaf_span(w, elem):
+    """Sibling blocks per grouped leaf request (mirrors leaf_span in csrc/pisa_leaf.hip):
+    head groups of up to 4 and blocks of up to 64 keys take the largest power of two
+    <= min(branching, 4) whose blocks fit 256 LDS rows and 80 KB."""
+    G = w.query_heads // w.key_heads
+    D = w.head_dim
+    if w.method == "pisa1" or G > 4 or w.block_size > 64 or D not in (16, 32, 64, 128):
+        return 1
+    E = 1 if elem == 4 else (8 if (D // 4) % 8 == 0 else 4)
+    kq = 32 if E == 8 else 16
+    cq = -(-w.block_size // kq) * kq
+    ldk = D + 16 // elem
+    span = 1
+    while (span * 2 <= min(w.branching, 4) and span * 2 * cq <= 256
+           and span * 2 * cq * ldk * elem + TILE * 16 <= 80 << 10):
+        span *= 2
+    return span
+
+
+def tile_count(w, valid, ids, elem, blocks=None):
     """Tiles of <= TILE requests per (batch, kv head, block) group, bucketed per
     window of query tokens over the flattened (batch, token) axis."""
     import torch
-    blocks = math.ceil(w.keys / w.block_size)
+    blocks = math.ceil(w.keys / w.block_size) if blocks is None else blocks
     window = query_window(w.batch * w.tokens, w.query_heads * w.head_dim * elem)
     windows = math.ceil(w.batch * w.tokens / window)
     dev = ids.device
@@ -145,7 +164,16 @@ def selection_counts(P, w, q, k, positions):
             scoreable &= (valid.sum(-1, keepdim=True) > w.topk)
         counts[level] = int(scoreable.sum())
         if level == 0 and w.method != "pisa1":
-            tiles = tile_count(w, scoreable, cand, q.element_size())
+            # requests: spans of sibling slots with a scoreable block, grouped by block // span
+            span = leaf_span(w, q.element_size())
+            shape = scoreable.shape[:-1] + (scoreable.shape[-1] // span, span)
+            sc, cd = scoreable.reshape(shape), cand.reshape(shape)
+            first_blk = torch.where(sc, cd, torch.iinfo(cd.dtype).max).min(-1).values
+            live = sc.any(-1)
+            counts["leaf_requests"] = int(live.sum())
+            counts["leaf_span"] = span
+            tiles = tile_count(w, live, torch.where(live, first_blk // span, 0),
+                               q.element_size(), blocks=-(-math.ceil(w.keys / w.block_size) // span))
     return ids, counts, tiles, top, first
 
 
@@ -325,14 +353,17 @@ def main():
     items = w.batch * w.tokens * w.key_heads
     width = first if top == 0 else w.branching * w.topk
     r_leaf = counts.get(0, 0)
-    r_int = sum(v for lvl, v in counts.items() if lvl > 0)
+    r_int = sum(v for lvl, v in counts.items() if isinstance(lvl, int) and lvl > 0)
+    span = counts.get("leaf_span", 1)
+    r_span = counts.get("leaf_requests", r_leaf)
     # algorithmic bytes / flops per launch of each hot kernel
     algo = {
         "route": {"bound": "hbm",
                   "bytes": w.batch * w.tokens * w.query_heads * D * e + r_int * w.branching * D * e
                   + items * width * 5},
-        "leaf": {"bound": "hbm",
-                 "bytes": leaf_tiles * w.block_size * D * e + r_leaf * (G * D * e + 8),
+        "leaf": {"bound": "hbm",   # key spans per tile, q rows once per span request, scores
+                 "bytes": leaf_tiles * span * w.block_size * D * e + r_span * (G * D * e + 4)
+                 + r_leaf * 4,
                  "flops": 2 * r_leaf * w.block_size * D * G},
         "final": {"bound": "hbm", "bytes": items * (width * 9 + w.topk * 8)},
         "attn_fwd": {"bound": "hbm",
@@ -400,7 +431,8 @@ def main():
         "sparse_attn_gather_tbps": round(gather_bytes / (att_ms * 1e-3) / 1e12, 2),
         "kernel_ms_per_step": {n: round(t, 4) for n, t in sorted(per_step.items(),
                                                                   key=lambda x: -x[1])},
-        "work": {"route_requests": r_int, "leaf_requests": r_leaf, "leaf_tiles": leaf_tiles,
+        "work": {"route_requests": r_int, "leaf_requests": r_leaf, "leaf_span": span,
+                 "leaf_span_requests": r_span, "leaf_tiles": leaf_tiles,
                  "attn_requests": requests, "attn_tiles": attn_tiles, "attn_pairs": pairs,
                  "attn_flops": attn_flops, "top": top, "first_width": first},
         "roofline": roofline,
