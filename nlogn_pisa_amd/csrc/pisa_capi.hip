@@ -68,6 +68,7 @@ struct SelectPlan {
   int64_t window_slots;  // leaf requests of one window
   int span;              // sibling candidates (consecutive blocks) per leaf request
   int spans;             // request groups per (batch, kv head)
+  int dense_nodes[PISA_MAX_LEVELS];  // nodes of each densely scored routing level (0: gathered)
 };
 
 int plan_select(const pisa_qk_desc* qk, const pisa_select_params* p, SelectPlan& pl) {
@@ -107,6 +108,17 @@ int plan_select(const pisa_qk_desc* qk, const pisa_select_params* p, SelectPlan&
   const int64_t flat = (int64_t)qk->batch * qk->query_tokens;
   pl.window = query_window(flat, (int64_t)qk->query_heads * D * es);
   pl.window_slots = (int64_t)pl.window * qk->key_heads * pl.W / pl.span;
+  // routing levels scored densely (every node for every item) before the route
+  for (int l = 0; l < PISA_MAX_LEVELS; ++l) pl.dense_nodes[l] = 0;
+  if (pl.grouped && p->top >= 1) {
+    int levels, offsets[PISA_MAX_LEVELS], lengths[PISA_MAX_LEVELS];
+    rc = pisa_pyramid_layout(qk->key_tokens, p->block_size, p->branching, p->top, &levels,
+                             offsets, lengths);
+    if (rc) return rc;
+    for (int l = 1; l <= p->top && l < levels; ++l)
+      if (route_level_dense(G, l, p->top, p->first_width, p->branching, p->topk, lengths[l]))
+        pl.dense_nodes[l] = lengths[l];
+  }
   return PISA_OK;
 }
 
@@ -115,6 +127,7 @@ struct SelectBuffers {
   uint8_t* scoreable;
   float* scores;
   Buckets buckets;
+  float* dense[PISA_MAX_LEVELS];
 };
 
 void carve_select(const SelectPlan& pl, Carve& c, SelectBuffers& sb) {
@@ -122,6 +135,9 @@ void carve_select(const SelectPlan& pl, Carve& c, SelectBuffers& sb) {
   sb.scoreable = c.take<uint8_t>(pl.slots);
   sb.scores = c.take<float>(pl.slots);
   carve_buckets(c, sb.buckets, pl.window_slots, pl.groups, kLeafTile);
+  for (int l = 0; l < PISA_MAX_LEVELS; ++l)
+    sb.dense[l] = pl.dense_nodes[l] ? c.take<float>(pl.items * dense_stride(pl.dense_nodes[l]))
+                                    : nullptr;
 }
 
 LeafArgs leaf_args(const pisa_qk_desc* qk, int method, int block_size, int W, int M0, int G,
@@ -230,6 +246,19 @@ extern "C" int pisa_select(const pisa_qk_desc* qk, const pisa_select_params* p, 
   a.scoreable = sb.scoreable;
   a.out = out;
   a.trace = trace;
+  a.batch = qk->batch;
+  a.dense_level = 0;
+  for (int l = 0; l < PISA_MAX_LEVELS; ++l) {
+    // a dense level needs the pyramid's level sizes the plan was made for
+    const bool dense = pl.grouped && sb.dense[l] && l < pyramid->levels &&
+                       pyramid->lengths[l] == pl.dense_nodes[l];
+    a.dense[l] = dense ? sb.dense[l] : nullptr;
+  }
+  for (int l = 1; l <= p->top; ++l) {
+    if (!a.dense[l]) continue;
+    rc = launch_route_dense(qk->dtype, a, l, st);
+    if (rc) return rc;
+  }
   // One wave per item for prefill; the fused leaf of a few long rows (decode)
   // spreads its support rows over eight waves.
   int threads = 64;

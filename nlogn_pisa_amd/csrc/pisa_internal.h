@@ -146,6 +146,11 @@ struct RouteArgs {
   uint8_t* scoreable;
   int64_t* out;
   int32_t* trace;
+  // Dense levels: the score of every node of level l for every item,
+  // [items][lengths[l]] (null: level l gathers its candidates' support rows).
+  float* dense[PISA_MAX_LEVELS];
+  int dense_level;  // the level one route_dense_kernel launch scores
+  int batch;
 };
 
 struct FinalArgs {
@@ -226,6 +231,14 @@ struct AttnArgs {
 };
 
 int launch_route(int dtype, const RouteArgs& a, int64_t items, int threads, hipStream_t stream);
+// Floats per item row of a dense routing level of `nodes` nodes (a multiple of 64).
+__host__ __device__ inline int64_t dense_stride(int nodes) { return (nodes + 63) / 64 * 64; }
+// Whether routing level `level` (>= 1) of the grouped schedule is scored densely
+// (every node for every item, route_dense_kernel) rather than per candidate.
+bool route_level_dense(int G, int level, int top, int first_width, int branching, int topk,
+                       int nodes);
+// Scores every node of dense level `level` for every item into a.dense[level].
+int launch_route_dense(int dtype, const RouteArgs& a, int level, hipStream_t stream);
 int launch_final(const FinalArgs& a, hipStream_t stream);
 int launch_scoreable(const MaskArgs& a, hipStream_t stream);
 int launch_leaf(int dtype, const LeafArgs& a, hipStream_t stream);

@@ -629,6 +629,13 @@ __global__ void __launch_bounds__(64) route_grouped_kernel(RouteArgs a) {
         else
           leaf_scores_mfma<T, HD, 8, false>(a, qb, b, h, ids_s, list_s, sc_s, nlist, 0, 1, lane);
       }
+    } else if (a.dense[level]) {
+      // dense level: every node's score was computed for this item beforehand
+      const float* ds = a.dense[level] + (int64_t)item * dense_stride(a.lengths[level]);
+      for (int i = lane; i < nlist; i += 64) {
+        const int e = list_s[i];
+        sc_s[e] = ds[ids_s[e]];
+      }
     } else {
     // score the scoreable candidates, 16 support rows at a time
     const int src_level = own ? level : level - 1;
@@ -713,6 +720,152 @@ __global__ void __launch_bounds__(64) route_grouped_kernel(RouteArgs a) {
         ids_s[lane * a.branching + c] = sel < 0 ? -1 : sel * a.branching + c;
     __syncthreads();
     width = a.branching * K;
+  }
+}
+
+// ------------------------------------------------------------------ dense routing levels
+//
+// route_dense_kernel: one routing level scored for every node and every item,
+// for levels with few nodes compared with the candidates a row scores there
+// (the top levels of a prefill).  Support scores are the same as
+// route_grouped_kernel's (block_scores, top_k_pyramid_torch.py:48-80) but a
+// wave owns 4 P items of one (batch, kv head) - P = 16 / Gp items of Gp padded
+// heads fill the 16 columns of one query tile, four tiles side by side - and
+// every 16-row tile of the level's support rows, loaded once, is multiplied
+// with all four query tiles.  Lane (grp, col) then holds head col % Gp of item
+// col / Gp against rows 4 grp + i; the per-head support score is computed in
+// the lane, summed over the item's Gp lanes and written to
+// a.dense[level][item][node].  The next support tile loads while one is scored.
+
+// Scores of one wave wait in LDS for 64 nodes of its 16 items, then go out as
+// whole 256-byte pieces of the items' rows (rows padded to 64 nodes).
+constexpr int kDenseChunk = 64;
+
+template <typename T, int HD, int RR, int MODE>
+__global__ void __launch_bounds__(256) route_dense_kernel(RouteArgs a) {
+  __shared__ float stage[4][16][kDenseChunk + 1];
+  typedef QkShape<T, HD> S;
+  typedef typename S::Op Op;
+  typedef typename S::frag frag;
+  constexpr int E = S::E, DS = S::DS;
+  constexpr int NCT = 4;                   // query tiles per wave
+  constexpr bool own = MODE == kModeOwn;   // support = the node's own summary
+  constexpr bool LSE = MODE == kModeLse;
+  constexpr int R = RR;
+  const int level = a.dense_level;
+  const int Gp = next_pow2(a.G);           // <= 16
+  const int P = 16 / Gp;                   // items per query tile
+  const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+  const int per_bh = (a.T + NCT * P - 1) / (NCT * P);
+  const int wid = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (wid >= a.batch * a.Hkv * per_bh) return;
+  const int bh = wid / per_bh;
+  const int t0 = (wid - bh * per_bh) * NCT * P;
+  const int b = bh / a.Hkv, h = bh % a.Hkv;
+  const int hd = col % Gp;
+  // query tiles: column col of tile c is head hd of token t0 + c P + col / Gp
+  frag qb[NCT][DS];
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) {
+    const int t = t0 + c * P + col / Gp;
+    if (t < a.T && hd < a.G)
+      load_row_frags<E>(static_cast<const T*>(a.q) + b * a.q_batch + (int64_t)t * a.q_token +
+                            ((int64_t)h * a.G + hd) * HD + E * grp,
+                        qb[c]);
+    else
+      zero_frags(qb[c]);
+  }
+  const int M = a.lengths[level];
+  const int64_t stride = dense_stride(M);
+  float (*sw)[kDenseChunk + 1] = stage[threadIdx.x >> 6];
+  const int src_level = own ? level : level - 1;
+  const T* base = static_cast<const T*>(a.summary) + b * a.sum_batch +
+                  ((int64_t)a.offsets[src_level] * a.Hkv + h) * HD;
+  const int64_t rstride = (int64_t)a.Hkv * HD;
+  const int len = a.lengths[src_level];
+  const int nrows = own ? M : M * R;
+  const int ntile = (nrows + 15) / 16;
+  float* out = a.dense[level];
+  const int64_t item0 = ((int64_t)b * a.T + t0) * a.Hkv + h;  // item of token t0
+
+  // support rows of tile mt (rows past the level read row 0, masked by the counts)
+  auto fetch = [&](int mt, frag (&f)[DS]) {
+    const int r = mt * 16 + col;
+    const bool ok = r < nrows && (own || r < len);
+    load_row_frags<E>(base + (int64_t)(ok ? r : 0) * rstride + E * grp, f);
+  };
+  // valid support rows of node n (0 past the level)
+  auto count = [&](int n) { return n >= M ? 0 : own ? 1 : max(0, min(R, len - n * R)); };
+  auto store = [&](int c, int n, float head) {
+    const float tot = group_sum(hd < a.G ? head : 0.f, Gp);
+    if (hd == 0) sw[c * P + col / Gp][n % kDenseChunk] = tot;
+  };
+  // the staged nodes [64 k, 64 k + 64) of the wave's items -> their rows
+  auto flush = [&](int k) {
+    wave_lds_sync();
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int il = 4 * u + (lane >> 4), nl = 4 * (lane & 15);
+      const int t = t0 + il;
+      if (il < NCT * P && t < a.T) {
+        const float4 v = make_float4(sw[il][nl], sw[il][nl + 1], sw[il][nl + 2], sw[il][nl + 3]);
+        *reinterpret_cast<float4*>(out + (item0 + (int64_t)il * a.Hkv) * stride +
+                                   k * kDenseChunk + nl) = v;
+      }
+    }
+    wave_lds_sync();
+  };
+  const int tiles_per_chunk = kDenseChunk * (own ? 1 : R) / 16;
+  auto tile = [&](int mt, const frag (&xf)[DS]) {
+#pragma unroll
+    for (int c = 0; c < NCT; ++c) {
+      f4 sv = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int d = 0; d < DS; ++d) sv = Op::mma(xf[d], qb[c][d], sv);
+      const float v[4] = {sv[0], sv[1], sv[2], sv[3]};
+      if constexpr (R <= 4) {
+#pragma unroll
+        for (int j = 0; j < 4 / R; ++j) {
+          const int n = (mt * 16 + 4 * grp) / R + j;
+          float head;
+          if constexpr (own) {
+            head = v[j];
+          } else {
+            const SupportAcc acc = support_acc<LSE>(v + j * R, R, count(n), a.scale);
+            head = support_final<MODE>(acc, v + j * R, a.scale);
+          }
+          store(c, n, head);
+        }
+      } else {
+        // R = 8: lane groups 2k (children 0-3) and 2k + 1 (children 4-7) of node 2 mt + k
+        const int n = mt * 2 + (grp >> 1);
+        const int cnt = count(n) - 4 * (grp & 1);
+        SupportAcc acc = support_acc<LSE>(v, 4, cnt, a.scale);
+        SupportAcc other;
+        other.a0 = __shfl_xor(acc.a0, 16);
+        other.a1 = __shfl_xor(acc.a1, 16);
+        other.n = __shfl_xor(acc.n, 16);
+        acc = (grp & 1) ? support_join<LSE>(other, acc) : support_join<LSE>(acc, other);
+        const float head = support_final<MODE == kModeBinary ? kModeMoments : MODE>(acc, v, a.scale);
+        store(c, n, head);
+      }
+    }
+  };
+  auto done = [&](int mt) {
+    if ((mt + 1) % tiles_per_chunk == 0 || mt + 1 == ntile) flush(mt / tiles_per_chunk);
+  };
+  // two support tiles in flight; the buffers alternate by unrolling
+  frag xa[DS], xb[DS];
+  fetch(0, xa);
+  for (int mt = 0; mt < ntile; mt += 2) {
+    fetch(mt + 1 < ntile ? mt + 1 : mt, xb);
+    tile(mt, xa);
+    done(mt);
+    if (mt + 1 < ntile) {
+      fetch(mt + 2 < ntile ? mt + 2 : mt + 1, xa);
+      tile(mt + 1, xb);
+      done(mt + 1);
+    }
   }
 }
 
@@ -886,6 +1039,72 @@ int launch_route(int dtype, const RouteArgs& a, int64_t items, int threads, hipS
     case PISA_BF16: return launch_route_t<bf16_t>(a, items, threads, stream);
     default: return fail(PISA_ERR_INVALID, "unknown dtype %d", dtype);
   }
+}
+
+// Dense scoring pays where a level's nodes are at most as many as the
+// candidates P items would score there (P = 16 / Gp items per query tile):
+// every node is then scored with no more support-row reads per item and no
+// gathers.  With one item per tile (Gp = 16) the extra pass over the query
+// rows outweighs the saving (measured), so dense levels need P >= 2; a wave's
+// 4 P items fit its 16 staging rows for P <= 4, i.e. Gp in {4, 8}.
+bool route_level_dense(int G, int level, int top, int first_width, int branching, int topk,
+                       int nodes) {
+  const int gp = next_pow2(G);
+  if (level < 1 || level > top || gp < 4 || gp > 8 || branching > 8) return false;
+  const int width = level == top ? first_width : branching * topk;
+  return (int64_t)nodes <= (int64_t)(16 / next_pow2(G)) * width;
+}
+
+template <typename T, int HD, int RR, int MODE>
+static void launch_dense_rm(const RouteArgs& a, int blocks, hipStream_t stream) {
+  PISA_TIMED("route_dense", stream, hipLaunchKernelGGL((route_dense_kernel<T, HD, RR, MODE>), dim3(blocks), dim3(256), 0, stream, a));
+}
+
+template <typename T, int HD>
+static void launch_dense_hd(const RouteArgs& a, int blocks, hipStream_t stream) {
+  if (a.method == PISA_METHOD_PISA1) return launch_dense_rm<T, HD, 1, kModeOwn>(a, blocks, stream);
+  const bool lse = a.method == PISA_METHOD_LSE;
+  switch (a.branching) {
+    case 2:
+      if (lse) launch_dense_rm<T, HD, 2, kModeLse>(a, blocks, stream);
+      else launch_dense_rm<T, HD, 2, kModeBinary>(a, blocks, stream);
+      break;
+    case 4:
+      if (lse) launch_dense_rm<T, HD, 4, kModeLse>(a, blocks, stream);
+      else launch_dense_rm<T, HD, 4, kModeMoments>(a, blocks, stream);
+      break;
+    default:
+      if (lse) launch_dense_rm<T, HD, 8, kModeLse>(a, blocks, stream);
+      else launch_dense_rm<T, HD, 8, kModeMoments>(a, blocks, stream);
+      break;
+  }
+}
+
+template <typename T>
+static void launch_dense_t(const RouteArgs& a, int blocks, hipStream_t stream) {
+  switch (a.D) {
+    case 16: launch_dense_hd<T, 16>(a, blocks, stream); break;
+    case 32: launch_dense_hd<T, 32>(a, blocks, stream); break;
+    case 64: launch_dense_hd<T, 64>(a, blocks, stream); break;
+    default: launch_dense_hd<T, 128>(a, blocks, stream); break;
+  }
+}
+
+int launch_route_dense(int dtype, const RouteArgs& a, int level, hipStream_t stream) {
+  if (!a.dense[level]) return fail(PISA_ERR_INVALID, "dense level %d has no buffer", level);
+  if (a.batch == 0 || a.T == 0) return PISA_OK;
+  RouteArgs d = a;
+  d.dense_level = level;
+  const int P = 16 / next_pow2(a.G);
+  const int64_t waves = (int64_t)a.batch * a.Hkv * ((a.T + 4 * P - 1) / (4 * P));
+  const int blocks = (int)((waves + 3) / 4);
+  switch (dtype) {
+    case PISA_F32: launch_dense_t<float>(d, blocks, stream); break;
+    case PISA_F16: launch_dense_t<f16_t>(d, blocks, stream); break;
+    case PISA_BF16: launch_dense_t<bf16_t>(d, blocks, stream); break;
+    default: return fail(PISA_ERR_INVALID, "unknown dtype %d", dtype);
+  }
+  return check_launch("route_dense");
 }
 
 int launch_final(const FinalArgs& a, hipStream_t stream) {
