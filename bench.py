@@ -89,6 +89,24 @@ def leaf_span(w, elem):
     return span
 
 
+def dense_levels(w, top, first):
+    """Routing levels scored densely, {level: nodes} (mirrors route_level_dense in
+    csrc/pisa_route.hip: padded head groups of 4 or 8, branching <= 8, a level whose
+    nodes are at most (16 / Gp) x its candidate width)."""
+    gp = 1 << (w.query_heads // w.key_heads - 1).bit_length()
+    if not 4 <= gp <= 8 or w.branching > 8 or w.method == "pisa1":   # pisa1 routes fused
+        return {}
+    out, nodes = {}, math.ceil(w.keys / w.block_size)
+    sizes = [nodes]
+    while len(sizes) <= top:
+        sizes.append(math.ceil(sizes[-1] / w.branching))
+    for level in range(1, top + 1):
+        width = first if level == top else w.branching * w.topk
+        if sizes[level] <= (16 // gp) * width:
+            out[level] = sizes[level]
+    return out
+
+
 def tile_count(w, valid, ids, elem, blocks=None):
     """Tiles of <= TILE requests per (batch, kv head, block) group, bucketed per
     window of query tokens over the flattened (batch, token) axis."""
@@ -353,14 +371,25 @@ def main():
     items = w.batch * w.tokens * w.key_heads
     width = first if top == 0 else w.branching * w.topk
     r_leaf = counts.get(0, 0)
-    r_int = sum(v for lvl, v in counts.items() if isinstance(lvl, int) and lvl > 0)
+    dense = dense_levels(w, top, first)
+    # internal requests gathered by the route kernel; dense levels' scores are read
+    r_int = sum(v for lvl, v in counts.items() if isinstance(lvl, int) and lvl > 0
+                and lvl not in dense)
+    r_dense = sum(v for lvl, v in counts.items() if isinstance(lvl, int) and lvl in dense)
     span = counts.get("leaf_span", 1)
     r_span = counts.get("leaf_requests", r_leaf)
     # algorithmic bytes / flops per launch of each hot kernel
     algo = {
         "route": {"bound": "hbm",
                   "bytes": w.batch * w.tokens * w.query_heads * D * e + r_int * w.branching * D * e
-                  + items * width * 5},
+                  + r_dense * 4 + items * width * 5},
+        # per dense level: the query rows, each wave's pass over the level's support
+        # rows (16 items per wave), the score rows written
+        "route_dense": {"bound": "mfma",
+                        "bytes": sum(w.batch * w.tokens * w.query_heads * D * e
+                                     + items / 16 * n * w.branching * D * e
+                                     + items * (-(-n // 64) * 64) * 4 for n in dense.values()),
+                        "flops": sum(2 * items * G * n * w.branching * D for n in dense.values())},
         "leaf": {"bound": "hbm",   # key spans per tile, q rows once per span request, scores
                  "bytes": leaf_tiles * span * w.block_size * D * e + r_span * (G * D * e + 4)
                  + r_leaf * 4,
@@ -398,9 +427,9 @@ def main():
     attn_flops = 4 * D * G * pairs
     attn_kernel_ms = per_step.get("attn_fwd", 0) + per_step.get("attn_combine", 0)
     leaf_ms = per_step.get("leaf", 0)
-    sel_kernels = ["pool", "route", "fill", "bucket_count", "bucket_scan", "bucket_scatter",
-                   "leaf", "final"]
-    sel_bytes = sum(algo[n]["bytes"] for n in ("pool", "route", "leaf", "final"))
+    sel_kernels = ["pool", "route_dense", "route", "fill", "bucket_count", "bucket_scan",
+                   "bucket_scatter", "leaf", "final"]
+    sel_bytes = sum(algo[n]["bytes"] for n in ("pool", "route", "route_dense", "leaf", "final"))
     result = {
         "metric": "selection ms + sparse-attn TFLOP/s at 64K prefill; % HBM / % MFMA peak",
         "value": round(sel_ms, 3),
@@ -431,7 +460,8 @@ def main():
         "sparse_attn_gather_tbps": round(gather_bytes / (att_ms * 1e-3) / 1e12, 2),
         "kernel_ms_per_step": {n: round(t, 4) for n, t in sorted(per_step.items(),
                                                                   key=lambda x: -x[1])},
-        "work": {"route_requests": r_int, "leaf_requests": r_leaf, "leaf_span": span,
+        "work": {"route_requests": r_int, "dense_route_requests": r_dense,
+                 "dense_levels": dense, "leaf_requests": r_leaf, "leaf_span": span,
                  "leaf_span_requests": r_span, "leaf_tiles": leaf_tiles,
                  "attn_requests": requests, "attn_tiles": attn_tiles, "attn_pairs": pairs,
                  "attn_flops": attn_flops, "top": top, "first_width": first},
