@@ -170,6 +170,11 @@ __global__ void __launch_bounds__(256) leaf_kernel(LeafArgs a) {
 // wave is one 16-row unit (Gp <= 16: 16 / Gp requests) or one request of Gp / 16
 // units (Gp > 16).
 
+// Padding of an LDS key row (bytes; a multiple of 8).
+#ifndef PISA_LEAF_PAD_BYTES
+#define PISA_LEAF_PAD_BYTES 16
+#endif
+
 struct LeafLds {
   int Cq, ldk;
   size_t k_off, q_off, slot_off, mask_off, bytes;
@@ -183,7 +188,7 @@ __host__ __device__ inline LeafLds leaf_lds(int C, int tile, int span = 1) {
   typedef QkShape<T, HD> S;
   LeafLds L;
   L.Cq = (C + S::KQ - 1) / S::KQ * S::KQ;
-  L.ldk = HD + S::PAD;
+  L.ldk = HD + PISA_LEAF_PAD_BYTES / (int)sizeof(T);
   size_t off = 0;
   L.k_off = off;
   off += (size_t)span * L.Cq * L.ldk * sizeof(T);
@@ -331,8 +336,70 @@ leaf_tile_kernel(LeafArgs a) {
     // k + DEPTH into `into` (the buffer unit k - 1 used); buffers rotate by
     // unrolling, never by copies, so the loads in flight are not waited for
     // early.  FULL: every key of every block of the span is valid (no masks).
-    auto unit = [&](auto full_tag, int k, frag (&cur)[DS], frag (&into)[DS]) {
+    // head score of this lane's row against block c of the span from S^T tiles s
+    auto head_of = [&](auto full_tag, const f4 (&s)[NTM], int c) {
       constexpr bool FULL = decltype(full_tag)::value;
+      const int lim = rows_valid[c] - 4 * grp;  // this lane's keys 16 mt + i are valid below lim
+      auto valid = [&](int mt, int i) { return mt < NT && (FULL || mt * 16 + i < lim); };
+      float head;
+      if (lse) {
+        float m = -INFINITY;
+#pragma unroll
+        for (int mt = 0; mt < NTM; ++mt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (valid(mt, i)) m = fmaxf(m, s[mt][i] * a.scale);
+        m = xor32_max(xor16_max(m));
+        float e = 0.f;
+#pragma unroll
+        for (int mt = 0; mt < NTM; ++mt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (valid(mt, i)) e += __expf(s[mt][i] * a.scale - m);
+        e = xor32_sum(xor16_sum(e));
+        head = m + __logf(e);
+      } else {
+        float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+        for (int mt = 0; mt < NTM; ++mt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (valid(mt, i)) {
+              s1 += s[mt][i];
+              s2 = fmaf(s[mt][i], s[mt][i], s2);
+            }
+        s1 = xor32_sum(xor16_sum(s1));
+        s2 = xor32_sum(xor16_sum(s2));
+        if (pisa1) {
+          head = s1;  // one support row: the leaf mean, scale 1
+        } else {
+          const float cnt = (float)rows_valid[c];
+          const float mean = s1 / cnt;
+          const float var = fmaxf(s2 / cnt - mean * mean, 0.f);
+          head = a.scale * mean + half_scale2 * var;
+        }
+      }
+      return head;
+    };
+    // item r done: sum the head rows of each request (aligned lanes of a 16-lane
+    // row) and write the scores of its scoreable blocks
+    auto finish = [&](int r, float (&tot)[SPAN]) {
+#pragma unroll
+      for (int c = 0; c < SPAN; ++c) {
+        if (c >= span) continue;
+        if (Gp >= 16) {
+          const float v = group_sum(tot[c], 16);
+          if (lane == 0 && r < nreq && ((mmask[r] >> c) & 1)) a.scores[mslot[r] + c] = v;
+        } else {
+          const float v = group_sum(tot[c], Gp);
+          const int rq = ((r << 4) + col) >> gl;
+          if (grp == 0 && (col & (Gp - 1)) == 0 && rq < nreq && ((mmask[rq] >> c) & 1))
+            a.scores[mslot[rq] + c] = v;
+        }
+        tot[c] = 0.f;
+      }
+    };
+    auto unit = [&](auto full_tag, int k, frag (&cur)[DS], frag (&into)[DS]) {
       fetch_k(k + DEPTH, into);
       const int r = wave + nwaves * (k >> nsl), j = k & (nsub - 1);
       const int rho = (((r << nsl) + j) << 4) + col;
@@ -357,65 +424,10 @@ leaf_tile_kernel(LeafArgs a) {
             }
           }
         }
-        const int lim = rows_valid[c] - 4 * grp;  // this lane's keys 16 mt + i are valid below lim
-        auto valid = [&](int mt, int i) { return mt < NT && (FULL || mt * 16 + i < lim); };
-        float head;
-        if (lse) {
-          float m = -INFINITY;
-#pragma unroll
-          for (int mt = 0; mt < NTM; ++mt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              if (valid(mt, i)) m = fmaxf(m, s[mt][i] * a.scale);
-          m = xor32_max(xor16_max(m));
-          float e = 0.f;
-#pragma unroll
-          for (int mt = 0; mt < NTM; ++mt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              if (valid(mt, i)) e += __expf(s[mt][i] * a.scale - m);
-          e = xor32_sum(xor16_sum(e));
-          head = m + __logf(e);
-        } else {
-          float s1 = 0.f, s2 = 0.f;
-#pragma unroll
-          for (int mt = 0; mt < NTM; ++mt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              if (valid(mt, i)) {
-                s1 += s[mt][i];
-                s2 = fmaf(s[mt][i], s[mt][i], s2);
-              }
-          s1 = xor32_sum(xor16_sum(s1));
-          s2 = xor32_sum(xor16_sum(s2));
-          if (pisa1) {
-            head = s1;  // one support row: the leaf mean, scale 1
-          } else {
-            const float cnt = (float)rows_valid[c];
-            const float mean = s1 / cnt;
-            const float var = fmaxf(s2 / cnt - mean * mean, 0.f);
-            head = a.scale * mean + half_scale2 * var;
-          }
-        }
+        const float head = head_of(full_tag, s, c);
         total[c] += real ? head : 0.f;
       }
-      if (j + 1 < nsub) return;
-      // item done: sum the head rows of each request (aligned lanes of a 16-lane
-      // row) and write the scores of its scoreable blocks
-#pragma unroll
-      for (int c = 0; c < SPAN; ++c) {
-        if (c >= span) continue;
-        if (Gp >= 16) {
-          const float v = group_sum(total[c], 16);
-          if (lane == 0 && r < nreq && ((mmask[r] >> c) & 1)) a.scores[mslot[r] + c] = v;
-        } else {
-          const float v = group_sum(total[c], Gp);
-          const int rq = ((r << 4) + col) >> gl;
-          if (grp == 0 && (col & (Gp - 1)) == 0 && rq < nreq && ((mmask[rq] >> c) & 1))
-            a.scores[mslot[rq] + c] = v;
-        }
-        total[c] = 0.f;
-      }
+      if (j + 1 == nsub) finish(r, total);
     };
     auto run = [&](auto full_tag) {
       frag qb[DEPTH + 1][DS];
@@ -482,7 +494,7 @@ int leaf_span(int dtype, int head_dim, int block_size, int branching, int group)
   const int E = es == 4 ? 1 : ((head_dim / 4) % 8 == 0 ? 8 : 4);
   const int KQ = E == 8 ? 32 : 16;
   const int cq = (block_size + KQ - 1) / KQ * KQ;
-  const int ldk = head_dim + 16 / es;
+  const int ldk = head_dim + PISA_LEAF_PAD_BYTES / es;
   int span = 1;
   while (span * 2 <= branching && span * 2 <= PISA_LEAF_MAX_SPAN && span * 2 * cq <= 256 &&
          (size_t)span * 2 * cq * ldk * es + (size_t)kLeafTile * 16 <= (80u << 10))
