@@ -229,7 +229,7 @@ __device__ void fwd_unit(const AttnArgs& a, ReqFn req_slot, int nreq, int unit, 
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i)
-    if (valid_r[i] && col == 0) a.part_lse[slot_r[i] * a.G + gh_r[i]] = mrow[i] + __logf(lrow[i]);
+    if (valid_r[i] && col == 0) stream_store(a.part_lse + slot_r[i] * a.G + gh_r[i], mrow[i] + __logf(lrow[i]));
   wave_lds_sync();
   // 16-byte stores of whole partial rows (row = request x head)
   constexpr int V = 16 / sizeof(PT);
@@ -240,7 +240,7 @@ __device__ void fwd_unit(const AttnArgs& a, ReqFn req_slot, int nreq, int unit, 
     const int rq_r = rho_r / Gp, g_r = rho_r % Gp;
     if (rq_r < nreq && g_r < a.G) {
       PT* dst = static_cast<PT*>(a.part_o) + (req_slot(rq_r) * a.G + g_r) * a.Dv + c * V;
-      *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(os + r * ldo + c * V);
+      stream_store16(dst, *reinterpret_cast<const uint4*>(os + r * ldo + c * V));
     }
   }
   wave_lds_sync();
@@ -622,9 +622,18 @@ __device__ void fwd_tile_units(const AttnArgs& a, const TileLds& L, const T* ks,
       if (so) {
         store_vals(so + col * L.ldo + QL * grp, vals);
       } else if (valid) {
-        store_vals(static_cast<PT*>(a.part_o) + ((int64_t)mslot[rq] * a.G + gh) * HD + QL * grp, vals);
+        PT* dst = static_cast<PT*>(a.part_o) + ((int64_t)mslot[rq] * a.G + gh) * HD + QL * grp;
+        if constexpr (QL * sizeof(PT) % 16 == 0) {  // whole 16-byte chunks: streaming stores
+          uint4 chunk[QL * sizeof(PT) / 16];
+          __builtin_memcpy(chunk, vals, sizeof(chunk));
+#pragma unroll
+          for (int i = 0; i < (int)(QL * sizeof(PT) / 16); ++i)
+            stream_store16(dst + i * (16 / (int)sizeof(PT)), chunk[i]);
+        } else {
+          store_vals(dst, vals);
+        }
       }
-      if (valid && grp == 0) a.part_lse[(int64_t)mslot[rq] * a.G + gh] = m + __logf(l);
+      if (valid && grp == 0) stream_store(a.part_lse + (int64_t)mslot[rq] * a.G + gh, m + __logf(l));
     }
     if (so) {
       wave_lds_sync();
@@ -636,8 +645,7 @@ __device__ void fwd_tile_units(const AttnArgs& a, const TileLds& L, const T* ks,
         const int rho2 = (u << 4) + r, rq2 = rho2 >> gl, gh2 = rho2 & (Gp - 1);
         if (rq2 < nreq && gh2 < a.G) {
           const uint4 v = *reinterpret_cast<const uint4*>(so + r * L.ldo + c * CE);
-          *reinterpret_cast<uint4*>(static_cast<PT*>(a.part_o) +
-                                    ((int64_t)mslot[rq2] * a.G + gh2) * HD + c * CE) = v;
+          stream_store16(static_cast<PT*>(a.part_o) + ((int64_t)mslot[rq2] * a.G + gh2) * HD + c * CE, v);
         }
       }
       wave_lds_sync();  // the rows are out; the next unit may overwrite them
@@ -766,8 +774,8 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a, int64_t i
 #pragma unroll
         for (int j = 0; j < U; ++j) {
           const int64_t row = (slot0 + s0 + min(s + j, n - 1)) * a.G + g;
-          lse[j] = a.part_lse[row];
-          x[j].u = *reinterpret_cast<const uint4*>(part + row * a.Dv + c * V);
+          lse[j] = stream_load(a.part_lse + row);
+          x[j].u = stream_load16(part + row * a.Dv + c * V);
         }
 #pragma unroll
         for (int j = 0; j < U; ++j) {
@@ -1044,8 +1052,8 @@ __global__ void __launch_bounds__(512) attn_bwd_grouped_kernel(AttnArgs a) {
       const int key_r = kbase + 4 * grp + i;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        part[(int64_t)key_r * (2 * HD) + dt * 16 + col] = dk[dt][i] * a.scale;
-        part[(int64_t)key_r * (2 * HD) + HD + dt * 16 + col] = dv[dt][i];
+        stream_store(part + (int64_t)key_r * (2 * HD) + dt * 16 + col, dk[dt][i] * a.scale);
+        stream_store(part + (int64_t)key_r * (2 * HD) + HD + dt * 16 + col, dv[dt][i]);
       }
     }
   }
@@ -1078,7 +1086,8 @@ __global__ void __launch_bounds__(256) attn_dkv_reduce_kernel(AttnArgs a, int64_
     for (; j + 4 <= n; j += 4) {
       float4 v[4];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) v[k] = src[(int64_t)(j + k) * tile_stride];
+      for (int k = 0; k < 4; ++k)
+        v[k] = stream_load_f4(reinterpret_cast<const float*>(src + (int64_t)(j + k) * tile_stride));
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         acc.x += v[k].x;
@@ -1088,7 +1097,7 @@ __global__ void __launch_bounds__(256) attn_dkv_reduce_kernel(AttnArgs a, int64_
       }
     }
     for (; j < n; ++j) {
-      const float4 v = src[(int64_t)j * tile_stride];
+      const float4 v = stream_load_f4(reinterpret_cast<const float*>(src + (int64_t)j * tile_stride));
       acc.x += v.x;
       acc.y += v.y;
       acc.z += v.z;
@@ -1150,7 +1159,8 @@ __global__ void __launch_bounds__(256) attn_dq_combine_kernel(AttnArgs a, int64_
           for (int j = 0; j < 4; ++j) {
             const int c = c0 + lane + 64 * j;
             v[k][j] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (k < cnt && c < chunks) v[k][j] = part[sidx[k] * chunks + c];
+            if (k < cnt && c < chunks)
+              v[k][j] = stream_load_f4(reinterpret_cast<const float*>(part + sidx[k] * chunks + c));
           }
 #pragma unroll
         for (int k = 0; k < 4; ++k)
@@ -1420,8 +1430,9 @@ __global__ void __launch_bounds__(64 * W, W == 4 ? 2 : 1) attn_bwd_tile_kernel(A
         float* dst = a.part_dq + ((int64_t)mslot[rq] * a.G + gh) * HD + 4 * grp;
 #pragma unroll
         for (int t = 0; t < NQ; ++t)
-          *reinterpret_cast<float4*>(dst + 16 * (w * NQ + t)) =
-              make_float4(dq[t][0] * a.scale, dq[t][1] * a.scale, dq[t][2] * a.scale, dq[t][3] * a.scale);
+          stream_store_f4(dst + 16 * (w * NQ + t),
+                          make_float4(dq[t][0] * a.scale, dq[t][1] * a.scale, dq[t][2] * a.scale,
+                                      dq[t][3] * a.scale));
       }
     };
     Rows buf[2];
@@ -1443,8 +1454,8 @@ __global__ void __launch_bounds__(64 * W, W == 4 ? 2 : 1) attn_bwd_tile_kernel(A
 #pragma unroll
           for (int t = 0; t < NS; ++t) {
             const int d = 32 * (dsb + t) + 16 * hw + col;
-            part[(int64_t)key * (2 * HD) + d] = dk[m][t][i] * a.scale;
-            part[(int64_t)key * (2 * HD) + HD + d] = dv[m][t][i];
+            stream_store(part + (int64_t)key * (2 * HD) + d, dk[m][t][i] * a.scale);
+            stream_store(part + (int64_t)key * (2 * HD) + HD + d, dv[m][t][i]);
           }
         }
       }
@@ -1683,8 +1694,9 @@ __global__ void __launch_bounds__(256, NT <= 4 ? 2 : 1) attn_bwd_share_kernel(At
         float* dst = a.part_dq + ((int64_t)mslot[rq] * a.G + gh) * HD + 4 * grp;
 #pragma unroll
         for (int t = 0; t < NQ; ++t)
-          *reinterpret_cast<float4*>(dst + 16 * (w * NQ + t)) =
-              make_float4(dq[t][0] * a.scale, dq[t][1] * a.scale, dq[t][2] * a.scale, dq[t][3] * a.scale);
+          stream_store_f4(dst + 16 * (w * NQ + t),
+                          make_float4(dq[t][0] * a.scale, dq[t][1] * a.scale, dq[t][2] * a.scale,
+                                      dq[t][3] * a.scale));
       }
       __syncthreads();  // the exchange is free and the next unit's rows are in LDS
     };
@@ -1710,8 +1722,8 @@ __global__ void __launch_bounds__(256, NT <= 4 ? 2 : 1) attn_bwd_share_kernel(At
 #pragma unroll
           for (int t = 0; t < NS; ++t) {
             const int d = 32 * (dsb + t) + 16 * hw + col;
-            part[(int64_t)key * (2 * HD) + d] = dk[m][t][i] * a.scale;
-            part[(int64_t)key * (2 * HD) + HD + d] = dv[m][t][i];
+            stream_store(part + (int64_t)key * (2 * HD) + d, dk[m][t][i] * a.scale);
+            stream_store(part + (int64_t)key * (2 * HD) + HD + d, dv[m][t][i]);
           }
         }
       }

@@ -20,6 +20,30 @@ typedef _Float16 f16_t;
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef short s4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+
+// Streaming (non-temporal) global accesses for data written once by one kernel
+// and read once by the next (attention partial rows, LSEs, dQ and dK/dV
+// partials): they stay out of the way of the reused rows in L2 and the MALL.
+__device__ __forceinline__ void stream_store16(void* p, const uint4& v) {
+  const u32x4v x = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(x, reinterpret_cast<u32x4v*>(p));
+}
+__device__ __forceinline__ uint4 stream_load16(const void* p) {
+  const u32x4v x = __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(p));
+  return make_uint4(x[0], x[1], x[2], x[3]);
+}
+__device__ __forceinline__ void stream_store_f4(float* p, float4 v) {
+  stream_store16(p, make_uint4(__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z),
+                               __float_as_uint(v.w)));
+}
+__device__ __forceinline__ float4 stream_load_f4(const float* p) {
+  const uint4 u = stream_load16(p);
+  return make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z),
+                     __uint_as_float(u.w));
+}
+__device__ __forceinline__ void stream_store(float* p, float v) { __builtin_nontemporal_store(v, p); }
+__device__ __forceinline__ float stream_load(const float* p) { return __builtin_nontemporal_load(p); }
 
 constexpr float kForced = 1.0e9f;    // sentinel of required blocks
 constexpr float kInvalid = -1.0e9f;  // sentinel of invalid / future blocks
