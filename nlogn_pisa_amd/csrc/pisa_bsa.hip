@@ -36,22 +36,6 @@ struct BsaArgs {
   int64_t* out;  // [B, T, Hkv, K]
 };
 
-// Value of lane (lane ^ D) of the same 16-lane row, D in {1, 2, 4, 8}.
-template <int D>
-__device__ __forceinline__ int xor_row(int v) {
-  if constexpr (D == 1) {
-    return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
-  } else if constexpr (D == 2) {
-    return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
-  } else if constexpr (D == 4) {
-    // row_half_mirror (j <- j ^ 7 within 8 lanes), then quad_perm [3,2,1,0] (j <- j ^ 3)
-    const int m = __builtin_amdgcn_update_dpp(0, v, 0x141, 0xf, 0xf, false);
-    return __builtin_amdgcn_update_dpp(0, m, 0x1B, 0xf, 0xf, false);
-  } else {
-    return __builtin_amdgcn_update_dpp(0, v, 0x128, 0xf, 0xf, false);  // row_ror 8
-  }
-}
-
 // Direction of element e in one merge: MODE 0 alternates by bit STAGE of e
 // (descending where it is set), 1 is descending, 2 ascending.
 template <int MODE, int STAGE>

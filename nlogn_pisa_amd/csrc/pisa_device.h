@@ -504,6 +504,41 @@ struct QkShape {
   static constexpr int PAD = 16 / (int)sizeof(T);   // 16-byte LDS row padding
 };
 
+// ------------------------------------------------------------------ lane exchanges
+
+// Value of lane (lane ^ D) of the same 16-lane row, D in {1, 2, 4, 8}, by DPP.
+template <int D>
+__device__ __forceinline__ int xor_row(int v) {
+  if constexpr (D == 1) {
+    return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
+  } else if constexpr (D == 2) {
+    return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
+  } else if constexpr (D == 4) {
+    // row_half_mirror (j <- j ^ 7 within 8 lanes), then quad_perm [3,2,1,0] (j <- j ^ 3)
+    const int m = __builtin_amdgcn_update_dpp(0, v, 0x141, 0xf, 0xf, false);
+    return __builtin_amdgcn_update_dpp(0, m, 0x1B, 0xf, 0xf, false);
+  } else {
+    return __builtin_amdgcn_update_dpp(0, v, 0x128, 0xf, 0xf, false);  // row_ror 8
+  }
+}
+
+// Value of lane (lane ^ D) of the wave, D in {1, 2, ..., 32}: DPP inside a
+// 16-lane row, v_permlane16_swap / v_permlane32_swap across rows.  A lane swap
+// of a register with itself leaves the lane's own value in one result and its
+// partner's in the other; the partner's is the one that differs from the own
+// (or either, when they are equal).
+template <int D>
+__device__ __forceinline__ int xor_lane(int v) {
+  if constexpr (D <= 8) {
+    return xor_row<D>(v);
+  } else {
+    static_assert(D == 16 || D == 32, "lane exchange distance");
+    const auto r = D == 16 ? __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false)
+                           : __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+    return (int)r[0] == v ? (int)r[1] : (int)r[0];
+  }
+}
+
 // ------------------------------------------------------------------ comparison network
 //
 // Element e of a network of width `width` (power of two, <= 64*J) lives in lane
@@ -511,36 +546,107 @@ struct QkShape {
 // group = 2^x (all-descending when group == width) and distance group/2 .. 1,
 // the pair (e, e ^ distance) exchanges iff (left > right) != descending, so
 // equal scores exchange in descending groups and stay in ascending ones.
+// Distances of 64 and more swap registers, smaller ones exchange lanes.
+template <int J, int DIST>
+__device__ __forceinline__ void bitonic_step(float (&s)[J], int (&id)[J], int group, int width,
+                                             int lane) {
+  if constexpr (DIST >= 64) {
+    constexpr int jd = DIST >> 6;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      if ((j & jd) == 0 && (j | jd) < J) {
+        const int j2 = j | jd;
+        const int e = j * 64 + lane;
+        const bool desc = (group == width) || ((e & group) != 0);
+        const float l = s[j], r = s[j2];
+        if ((l > r) != desc) {
+          s[j] = r;
+          s[j2] = l;
+          const int t = id[j];
+          id[j] = id[j2];
+          id[j2] = t;
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const float ps = __int_as_float(xor_lane<DIST>(__float_as_int(s[j])));
+      const int pid = xor_lane<DIST>(id[j]);
+      const int e = j * 64 + lane;
+      const bool left = (e & DIST) == 0;
+      const bool desc = (group == width) || ((e & group) != 0);
+      const float ls = left ? s[j] : ps;
+      const float rs = left ? ps : s[j];
+      if ((ls > rs) != desc) {
+        s[j] = ps;
+        id[j] = pid;
+      }
+    }
+  }
+}
+
+// stage group = 2^X: distances 2^(X-1) .. 1
+template <int J, int X, int Y = X - 1>
+__device__ __forceinline__ void bitonic_stage(float (&s)[J], int (&id)[J], int width, int lane) {
+  if constexpr (Y >= 0) {
+    bitonic_step<J, (1 << Y)>(s, id, 1 << X, width, lane);
+    bitonic_stage<J, X, Y - 1>(s, id, width, lane);
+  }
+}
+
+template <int J, int X = 1>
+__device__ __forceinline__ void bitonic_stages(float (&s)[J], int (&id)[J], int width, int lane) {
+  if constexpr ((1 << X) <= 64 * J) {
+    if ((1 << X) > width) return;
+    bitonic_stage<J, X>(s, id, width, lane);
+    bitonic_stages<J, X + 1>(s, id, width, lane);
+  }
+}
+
+// Networks of up to 128 elements (the routing levels and the leaf) run fully
+// unrolled with register-level lane exchanges; wider ones (up to 512) keep a
+// compact loop with LDS-path shuffles, whose code and registers stay small.
 template <int J>
 __device__ __forceinline__ void bitonic_desc(float (&s)[J], int (&id)[J], int width, int lane) {
-  for (int group = 2; group <= width; group <<= 1) {
-    for (int dist = group >> 1; dist > 0; dist >>= 1) {
-      if (dist >= 64) {
-        const int jd = dist >> 6;
+  if constexpr (J <= 2) {
+    bitonic_stages<J>(s, id, width, lane);
+  } else {
+    for (int group = 2; group <= width; group <<= 1) {
+      for (int dist = group >> 1; dist > 0; dist >>= 1) {
+        if (dist >= 64) {
+          const int jd = dist >> 6;
 #pragma unroll
-        for (int j = 0; j < J; ++j) {
-          if ((j & jd) == 0 && (j | jd) < J) {
-            const int j2 = j | jd;
-            const int e = j * 64 + lane;
-            const bool desc = (group == width) || ((e & group) != 0);
-            const float l = s[j], r = s[j2];
-            if ((l > r) != desc) {
-              s[j] = r; s[j2] = l;
-              const int t = id[j]; id[j] = id[j2]; id[j2] = t;
+          for (int j = 0; j < J; ++j) {
+            if ((j & jd) == 0 && (j | jd) < J) {
+              const int j2 = j | jd;
+              const int e = j * 64 + lane;
+              const bool desc = (group == width) || ((e & group) != 0);
+              const float l = s[j], r = s[j2];
+              if ((l > r) != desc) {
+                s[j] = r;
+                s[j2] = l;
+                const int t = id[j];
+                id[j] = id[j2];
+                id[j2] = t;
+              }
             }
           }
-        }
-      } else {
+        } else {
 #pragma unroll
-        for (int j = 0; j < J; ++j) {
-          const float ps = __shfl_xor(s[j], dist);
-          const int pid = __shfl_xor(id[j], dist);
-          const int e = j * 64 + lane;
-          const bool left = (e & dist) == 0;
-          const bool desc = (group == width) || ((e & group) != 0);
-          const float ls = left ? s[j] : ps;
-          const float rs = left ? ps : s[j];
-          if ((ls > rs) != desc) { s[j] = ps; id[j] = pid; }
+          for (int j = 0; j < J; ++j) {
+            const float ps = __shfl_xor(s[j], dist);
+            const int pid = __shfl_xor(id[j], dist);
+            const int e = j * 64 + lane;
+            const bool left = (e & dist) == 0;
+            const bool desc = (group == width) || ((e & group) != 0);
+            const float ls = left ? s[j] : ps;
+            const float rs = left ? ps : s[j];
+            if ((ls > rs) != desc) {
+              s[j] = ps;
+              id[j] = pid;
+            }
+          }
         }
       }
     }
