@@ -559,7 +559,6 @@ __global__ void __launch_bounds__(64) route_grouped_kernel(RouteArgs a) {
   __shared__ int ids_s[kMaxWidth];
   __shared__ float sc_s[kMaxWidth];
   __shared__ int list_s[kMaxWidth];
-  __shared__ int cnt_s[2];
 
   const int item = blockIdx.x;
   const int h = item % a.Hkv;
@@ -592,34 +591,37 @@ __global__ void __launch_bounds__(64) route_grouped_kernel(RouteArgs a) {
     const int M = a.lengths[level];
     const int64_t span_blocks = ipow(a.branching, level);
     const int64_t span = span_blocks * a.C;
-    if (lane == 0) { cnt_s[0] = 0; cnt_s[1] = 0; }
-    __syncthreads();
+    // counts by wave ballots (one wave per item): valid candidates, then the
+    // scoreable ones listed in slot order
+    const uint64_t below = (1ull << lane) - 1;
     int nvalid = 0;
-    for (int e = lane; e < width; e += 64) {
-      int id = ids_s[e];
-      if (id >= M) { id = -1; ids_s[e] = -1; }
-      nvalid += (id >= 0 && (int64_t)id * span <= pos) ? 1 : 0;
+    for (int e0 = 0; e0 < width; e0 += 64) {
+      const int e = e0 + lane;
+      int id = e < width ? ids_s[e] : -1;
+      if (e < width && id >= M) { id = -1; ids_s[e] = -1; }
+      nvalid += __popcll(__ballot(id >= 0 && (int64_t)id * span <= pos));
     }
-    if (nvalid) atomicAdd(&cnt_s[0], nvalid);
-    __syncthreads();
-    const bool identity = !own && cnt_s[0] <= K;
-    for (int e = lane; e < width; e += 64) {
-      const int id = ids_s[e];
+    const bool identity = !own && nvalid <= K;
+    int nlist = 0;
+    for (int e0 = 0; e0 < width; e0 += 64) {
+      const int e = e0 + lane;
+      const int id = e < width ? ids_s[e] : -1;
       const bool valid = id >= 0 && (int64_t)id * span <= pos;
       const bool forced = valid && is_forced(id, leaf, span_blocks, a.force_first, a.force_recent);
       const bool scoreable = valid && !forced && !identity;
-      sc_s[e] = valid ? (forced ? kForced : 0.f) : kInvalid;
-      if (level == 0 && !FUSED) {
-        a.cand[(int64_t)item * width + e] = id;
-        a.scoreable[(int64_t)item * width + e] = scoreable ? 1 : 0;
-      } else if (scoreable) {
-        list_s[atomicAdd(&cnt_s[1], 1)] = e;
+      if (e < width) {
+        sc_s[e] = valid ? (forced ? kForced : 0.f) : kInvalid;
+        if (level == 0 && !FUSED) {
+          a.cand[(int64_t)item * width + e] = id;
+          a.scoreable[(int64_t)item * width + e] = scoreable ? 1 : 0;
+        }
       }
+      const uint64_t m = __ballot(scoreable);
+      if (scoreable) list_s[nlist + __popcll(m & below)] = e;
+      nlist += __popcll(m);
     }
-    __syncthreads();
     if (level == 0 && !FUSED) return;
-
-    const int nlist = cnt_s[1];
+    __syncthreads();
     if (FUSED && level == 0 && !own) {
       // fused schedule: this wave scores the leaf candidates' key blocks on the
       // matrix cores, the next block loading while one is scored
