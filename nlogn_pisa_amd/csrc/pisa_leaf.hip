@@ -447,12 +447,284 @@ leaf_tile_kernel(LeafArgs a) {
   }
 }
 
+// ------------------------------------------------------------------ split spans
+//
+// Spans of SPAN sibling blocks of at most 64 keys, 16-bit inputs.  Wave c of
+// a SPAN-wave workgroup owns block c of the tile's span: it holds the block's
+// MFMA A fragments (its key rows) in registers for the whole tile, and every
+// wave scores every unit of the tile against its own block.  The tile's query
+// rows pass through LDS once, NU units (16 rows each) at a time and double
+// buffered, so LDS serves 16 query rows per unit and block instead of the span's
+// whole key set per unit.  Loads of the next NU units are in flight while the
+// current ones are scored; one workgroup barrier per NU units.
+
+// LDS of a split-span workgroup: two buffers of NU units of padded query rows,
+// then per request its query-row offset, first slot and scoreable mask.
+template <typename T, int HD>
+__host__ __device__ inline size_t leaf_split_lds(int nu, int tile) {
+  return (size_t)2 * nu * 16 * (HD + 16 / sizeof(T)) * sizeof(T) + (size_t)tile * 16;
+}
+
+// Units per staged batch, batches of query rows in flight (1 or 2), and the
+// minimum waves per SIMD requested from the compiler.
+#ifndef PISA_LEAF_NU
+#define PISA_LEAF_NU 4
+#endif
+#ifndef PISA_LEAF_SPLIT_DEPTH
+#define PISA_LEAF_SPLIT_DEPTH 1
+#endif
+#ifndef PISA_LEAF_SPLIT_WAVES
+#define PISA_LEAF_SPLIT_WAVES 3
+#endif
+
+template <typename T, int HD, int SPAN, int NU>
+__global__ void __launch_bounds__(64 * SPAN, PISA_LEAF_SPLIT_WAVES) leaf_split_kernel(LeafArgs a) {
+  typedef QkShape<T, HD> S;
+  typedef typename S::Op Op;
+  typedef typename S::frag frag;
+  constexpr int E = S::E, DS = S::DS;
+  constexpr int NTM = 4;                      // key tiles of a block (up to 64 keys)
+  constexpr int THREADS = 64 * SPAN;
+  constexpr int vec = 16 / (int)sizeof(T);
+  constexpr int vpr = HD / vec;               // 16-byte chunks of a query row
+  constexpr int LPT = NU * 16 * vpr / THREADS;  // staging loads per thread and batch
+  static_assert(sizeof(T) == 2 && LPT * THREADS == NU * 16 * vpr, "query staging layout");
+  constexpr int LDQ = HD + vec;               // LDS query row, 16 bytes of padding
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  T* qs = reinterpret_cast<T*>(smem);         // [2][NU * 16][LDQ]
+  int64_t* mq = reinterpret_cast<int64_t*>(smem + (size_t)2 * NU * 16 * LDQ * sizeof(T));
+  int32_t* mslot = reinterpret_cast<int32_t*>(mq + a.tile);
+  int32_t* mmask = mslot + a.tile;
+  const int tid = threadIdx.x, lane = tid & 63, c = tid >> 6;  // c: this wave's block
+  const int col = lane & 15, grp = lane >> 4;
+  const int NT = ((a.C + S::KQ - 1) / S::KQ * S::KQ) / 16;
+  const int Gp = a.Gp;                        // a power of two <= 16
+  const int gl = 31 - __clz(Gp);
+  const float half_scale2 = (float)(0.5 * (double)a.scale * (double)a.scale);
+  const bool lse = a.method == PISA_METHOD_LSE;
+  const bool pisa1 = a.method == PISA_METHOD_PISA1;
+  const T* q = static_cast<const T*>(a.q);
+  const int ntiles = *a.num_tiles;
+
+  const XcdTiles walk = xcd_tiles(ntiles);
+  for (int tile = walk.begin; tile < walk.end; tile += walk.step) {
+    const int g = a.tile_group[tile];
+    const int blk0 = (g % a.spans) * SPAN;
+    const int bh = g / a.spans;
+    const int h = bh % a.Hkv;
+    const int b = bh / a.Hkv;
+    const int start = (tile - a.tile_off[g]) * a.tile;
+    const int nreq = min(a.tile, a.counts[g] - start);
+    const int rows_valid = max(0, min(a.C, a.src_rows - (blk0 + c) * a.C));
+    const int32_t* reqs = a.tile_req + (int64_t)tile * a.tile;
+
+    __syncthreads();  // the previous tile's readers of the bookkeeping are done
+    for (int i = tid; i < nreq; i += THREADS) {
+      const int64_t slot = (int64_t)reqs[i] * SPAN;
+      const int64_t item = slot / a.W;
+      const int t = (int)((item / a.Hkv) % a.T);
+      mq[i] = (int64_t)b * a.q_batch + (int64_t)t * a.q_token + (int64_t)h * a.G * HD;
+      mslot[i] = (int32_t)slot;
+      int mask = 0;
+#pragma unroll
+      for (int j = 0; j < SPAN; ++j) mask |= a.scoreable[slot + j] ? 1 << j : 0;
+      mmask[i] = mask;
+    }
+    // this wave's block: A fragments of its key rows (zero past the valid rows)
+    frag kreg[NTM][DS];
+    {
+      const T* kb = static_cast<const T*>(a.src) + b * a.src_batch +
+                    (int64_t)(blk0 + c) * a.C * a.src_row + (int64_t)h * HD;
+#pragma unroll
+      for (int mt = 0; mt < NTM; ++mt) {
+        const int row = mt * 16 + col;
+        if (mt < NT && row < rows_valid) {
+          load_row_frags<E>(kb + (int64_t)row * a.src_row + E * grp, kreg[mt]);
+        } else {
+#pragma unroll
+          for (int d = 0; d < DS; ++d) kreg[mt][d] = frag{};
+        }
+      }
+    }
+    const int nunits = (nreq + (16 >> gl) - 1) >> (4 - gl);
+    const int nb = (nunits + NU - 1) / NU;
+    __syncthreads();  // bookkeeping visible
+
+    // Query rows of batch `batch` into registers.  Rows that do not exist
+    // (padding heads or requests) read request 0's first head instead; their
+    // scores are never used, so no load sits behind a branch.
+    auto fetch = [&](int batch, u32x4v (&st)[LPT]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int j = 0; j < LPT; ++j) {
+        const int idx = j * THREADS + tid;
+        const int rho = batch * NU * 16 + idx / vpr;
+        const int rq = rho >> gl, gh = rho & (Gp - 1);
+        const bool ok = rq < nreq && gh < a.G;
+        st[j] = *reinterpret_cast<const u32x4v*>(q + mq[ok ? rq : 0] + (int64_t)(ok ? gh : 0) * HD +
+                                                (idx % vpr) * vec);
+      }
+    };
+    auto stage = [&](int buf, const u32x4v (&st)[LPT]) __attribute__((always_inline)) {
+      T* dst = qs + (size_t)buf * NU * 16 * LDQ;
+#pragma unroll
+      for (int j = 0; j < LPT; ++j) {
+        const int idx = j * THREADS + tid;
+        *reinterpret_cast<u32x4v*>(dst + (idx / vpr) * LDQ + (idx % vpr) * vec) = st[j];
+      }
+    };
+    // head score of this lane's row (column `col` of S^T) against this wave's block
+    auto head_of = [&](auto full_tag, const f4 (&s)[NTM]) __attribute__((always_inline)) {
+      constexpr bool FULL = decltype(full_tag)::value;
+      const int lim = rows_valid - 4 * grp;  // this lane's keys 16 mt + i are valid below lim
+      auto valid = [&](int mt, int i) { return mt < NT && (FULL || mt * 16 + i < lim); };
+      float head;
+      if (lse) {
+        float m = -INFINITY;
+#pragma unroll
+        for (int mt = 0; mt < NTM; ++mt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (valid(mt, i)) m = fmaxf(m, s[mt][i] * a.scale);
+        m = xor32_max(xor16_max(m));
+        float e = 0.f;
+#pragma unroll
+        for (int mt = 0; mt < NTM; ++mt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (valid(mt, i)) e += __expf(s[mt][i] * a.scale - m);
+        e = xor32_sum(xor16_sum(e));
+        head = m + __logf(e);
+      } else {
+        float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+        for (int mt = 0; mt < NTM; ++mt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (valid(mt, i)) {
+              s1 += s[mt][i];
+              s2 = fmaf(s[mt][i], s[mt][i], s2);
+            }
+        s1 = xor32_sum(xor16_sum(s1));
+        s2 = xor32_sum(xor16_sum(s2));
+        if (pisa1) {
+          head = s1;
+        } else {
+          const float cnt = (float)rows_valid;
+          const float mean = s1 / cnt;
+          const float var = fmaxf(s2 / cnt - mean * mean, 0.f);
+          head = a.scale * mean + half_scale2 * var;
+        }
+      }
+      return head;
+    };
+    auto score_batch = [&](auto full_tag, int batch) __attribute__((always_inline)) {
+      const T* qb = qs + (size_t)(batch & 1) * NU * 16 * LDQ;
+#pragma unroll
+      for (int p = 0; p < NU; ++p) {
+        const int u = batch * NU + p;
+        if (u >= nunits) break;
+        frag qf[DS];
+        load_row_frags<E>(qb + (p * 16 + col) * LDQ + E * grp, qf);
+        f4 s[NTM];
+#pragma unroll
+        for (int mt = 0; mt < NTM; ++mt) {
+          s[mt] = f4{0.f, 0.f, 0.f, 0.f};
+          if (mt < NT) {
+#pragma unroll
+            for (int d = 0; d < DS; ++d) s[mt] = Op::mma(kreg[mt][d], qf[d], s[mt]);
+          }
+        }
+        const float head = head_of(full_tag, s);
+        const int rho = u * 16 + col;
+        const int rq = rho >> gl;
+        const bool real = rq < nreq && (rho & (Gp - 1)) < a.G;
+        const float v = group_sum(real ? head : 0.f, Gp);
+        if (grp == 0 && (col & (Gp - 1)) == 0 && rq < nreq && ((mmask[rq] >> c) & 1))
+          a.scores[mslot[rq] + c] = v;
+      }
+    };
+    // Two register sets: batch i + 2 is loaded while batch i is scored and batch
+    // i + 1 (loaded during batch i - 1) goes to LDS after it; the loop is
+    // unrolled by two so the sets alternate without copies.  nb is uniform over
+    // the workgroup, so every wave meets the same barriers.
+    auto run2 = [&](auto full_tag) __attribute__((always_inline)) {
+      u32x4v sa[LPT], sb[LPT];
+      fetch(0, sa);
+      stage(0, sa);
+      if (1 < nb) fetch(1, sb);
+      __syncthreads();
+      for (int i = 0; i < nb; i += 2) {
+        if (i + 2 < nb) fetch(i + 2, sa);
+        if (rows_valid > 0) score_batch(full_tag, i);
+        if (i + 1 < nb) stage((i + 1) & 1, sb);
+        __syncthreads();
+        if (i + 1 >= nb) break;
+        if (i + 3 < nb) fetch(i + 3, sb);
+        if (rows_valid > 0) score_batch(full_tag, i + 1);
+        if (i + 2 < nb) stage(i & 1, sa);
+        __syncthreads();
+      }
+    };
+    // One register set: batch i + 1 is loaded while batch i is scored.
+    auto run1 = [&](auto full_tag) __attribute__((always_inline)) {
+      u32x4v sa[LPT];
+      fetch(0, sa);
+      stage(0, sa);
+      __syncthreads();
+      for (int i = 0; i < nb; ++i) {
+        if (i + 1 < nb) fetch(i + 1, sa);
+        if (rows_valid > 0) score_batch(full_tag, i);
+        if (i + 1 < nb) stage((i + 1) & 1, sa);
+        __syncthreads();
+      }
+    };
+    auto run = [&](auto full_tag) __attribute__((always_inline)) {
+      if constexpr (PISA_LEAF_SPLIT_DEPTH >= 2) run2(full_tag);
+      else run1(full_tag);
+    };
+    // FULL: every key of every block of the span is valid (uniform over the workgroup)
+    const bool full = NT * 16 == a.C && (blk0 + SPAN) * a.C <= a.src_rows;
+    if (full) run(std::true_type{});
+    else run(std::false_type{});
+  }
+}
+
 // Workgroups of a tile span's LDS above this many bytes hold eight waves (two
 // workgroups per CU still fit), smaller ones four.
 constexpr size_t kLeafWideLds = 48 << 10;
 
+#ifndef PISA_LEAF_SPLIT
+#define PISA_LEAF_SPLIT 1
+#endif
+
+// Split-span kernel of `SPAN` waves; grid = the resident workgroups of the device
+// (a multiple of 8 for the XCD tile walk).
+template <typename T, int HD, int SPAN>
+static void launch_leaf_split(const LeafArgs& a, int cus, hipStream_t stream) {
+  constexpr int vpr = HD * (int)sizeof(T) / 16;
+  // PISA_LEAF_NU units per batch at four waves, in proportion to the waves
+  // otherwise (the same staging loads per thread), and at least one load per thread
+  constexpr int NU0 = PISA_LEAF_NU * SPAN / 4 > 0 ? PISA_LEAF_NU * SPAN / 4 : 1;
+  constexpr int NU = NU0 * 16 * vpr >= 64 * SPAN ? NU0 : 64 * SPAN / (16 * vpr);
+  const void* kernel = (const void*)leaf_split_kernel<T, HD, SPAN, NU>;
+  const size_t lds = leaf_split_lds<T, HD>(NU, a.tile);
+  allow_lds(kernel, lds);
+  static int per_cu = 0;  // per instance
+  if (per_cu == 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, 64 * SPAN, lds) != hipSuccess || n < 1) n = 1;
+    per_cu = n;
+  }
+  const dim3 grid(cus * per_cu / 8 * 8 > 0 ? cus * per_cu / 8 * 8 : 8);
+  PISA_TIMED("leaf", stream, hipLaunchKernelGGL((leaf_split_kernel<T, HD, SPAN, NU>), grid, dim3(64 * SPAN), lds, stream, a));
+}
+
 template <typename T, int HD>
 static void launch_leaf_tile(const LeafArgs& a, int cus, hipStream_t stream) {
+  if constexpr (sizeof(T) == 2) {
+    if (PISA_LEAF_SPLIT && a.span == 4) return launch_leaf_split<T, HD, 4>(a, cus, stream);
+    if (PISA_LEAF_SPLIT && a.span == 2) return launch_leaf_split<T, HD, 2>(a, cus, stream);
+  }
   const LeafLds L = leaf_lds<T, HD>(a.C, a.tile, a.span);
   const int nt = L.Cq / 16;
   const bool wide = a.span > 1 && L.bytes > kLeafWideLds;  // 512-thread instances only

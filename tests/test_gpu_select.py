@@ -116,6 +116,9 @@ CONFIGS = [
     ("suffix", 1, 4096, 8, 2, 64, 64, 4, 8, "pisa", True, 2, "bf16", 0.0, 100),
     ("d32", 1, 2048, 8, 2, 32, 32, 4, 8, "pisa2", True, 1, "bf16", 0.0, None),
     ("d16-fp32", 1, 1024, 4, 2, 16, 16, 2, 8, "pisa", True, 1, "fp32", 0.0, None),
+    # 63 blocks, the last one half full: the last span of four sibling blocks has three
+    ("ragged-span", 2, 4000, 8, 2, 128, 64, 4, 8, "pisa", True, 1, "bf16", 0.0, None),
+    ("ragged-span2", 1, 3000, 4, 2, 64, 64, 2, 8, "pisa2", True, 2, "bf16", 0.02, None),
 ]
 
 
