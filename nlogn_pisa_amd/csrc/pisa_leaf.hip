@@ -477,13 +477,14 @@ __host__ __device__ inline size_t leaf_split_lds(int nu, int tile) {
 #define PISA_LEAF_SPLIT_WAVES 3
 #endif
 
-template <typename T, int HD, int SPAN, int NU>
+// NTM: key tiles of a block (2: up to 32 keys, 4: up to 64); LSE: log-sum-exp
+// support scores, else the moment form (pisa2).
+template <typename T, int HD, int SPAN, int NU, int NTM, bool LSE>
 __global__ void __launch_bounds__(64 * SPAN, PISA_LEAF_SPLIT_WAVES) leaf_split_kernel(LeafArgs a) {
   typedef QkShape<T, HD> S;
   typedef typename S::Op Op;
   typedef typename S::frag frag;
   constexpr int E = S::E, DS = S::DS;
-  constexpr int NTM = 4;                      // key tiles of a block (up to 64 keys)
   constexpr int THREADS = 64 * SPAN;
   constexpr int vec = 16 / (int)sizeof(T);
   constexpr int vpr = HD / vec;               // 16-byte chunks of a query row
@@ -497,12 +498,10 @@ __global__ void __launch_bounds__(64 * SPAN, PISA_LEAF_SPLIT_WAVES) leaf_split_k
   int32_t* mmask = mslot + a.tile;
   const int tid = threadIdx.x, lane = tid & 63, c = tid >> 6;  // c: this wave's block
   const int col = lane & 15, grp = lane >> 4;
-  const int NT = ((a.C + S::KQ - 1) / S::KQ * S::KQ) / 16;
   const int Gp = a.Gp;                        // a power of two <= 16
   const int gl = 31 - __clz(Gp);
   const float half_scale2 = (float)(0.5 * (double)a.scale * (double)a.scale);
-  const bool lse = a.method == PISA_METHOD_LSE;
-  const bool pisa1 = a.method == PISA_METHOD_PISA1;
+  const float scale2 = a.scale * 1.44269504088896340736f;  // scale * log2(e)
   const T* q = static_cast<const T*>(a.q);
   const int ntiles = *a.num_tiles;
 
@@ -516,6 +515,7 @@ __global__ void __launch_bounds__(64 * SPAN, PISA_LEAF_SPLIT_WAVES) leaf_split_k
     const int start = (tile - a.tile_off[g]) * a.tile;
     const int nreq = min(a.tile, a.counts[g] - start);
     const int rows_valid = max(0, min(a.C, a.src_rows - (blk0 + c) * a.C));
+    const float inv_rows = 1.f / (float)max(rows_valid, 1);
     const int32_t* reqs = a.tile_req + (int64_t)tile * a.tile;
 
     __syncthreads();  // the previous tile's readers of the bookkeeping are done
@@ -538,7 +538,7 @@ __global__ void __launch_bounds__(64 * SPAN, PISA_LEAF_SPLIT_WAVES) leaf_split_k
 #pragma unroll
       for (int mt = 0; mt < NTM; ++mt) {
         const int row = mt * 16 + col;
-        if (mt < NT && row < rows_valid) {
+        if (row < rows_valid) {
           load_row_frags<E>(kb + (int64_t)row * a.src_row + E * grp, kreg[mt]);
         } else {
 #pragma unroll
@@ -572,28 +572,30 @@ __global__ void __launch_bounds__(64 * SPAN, PISA_LEAF_SPLIT_WAVES) leaf_split_k
         *reinterpret_cast<u32x4v*>(dst + (idx / vpr) * LDQ + (idx % vpr) * vec) = st[j];
       }
     };
-    // head score of this lane's row (column `col` of S^T) against this wave's block
+    // head score of this lane's row (column `col` of S^T) against this wave's
+    // block.  The log-sum-exp runs in base 2 (scale > 0): with c = scale *
+    // log2(e) and m = c * max S, head = ln 2 * (m + log2 sum 2^(c S - m)); the
+    // sum is at least about 1.
     auto head_of = [&](auto full_tag, const f4 (&s)[NTM]) __attribute__((always_inline)) {
       constexpr bool FULL = decltype(full_tag)::value;
       const int lim = rows_valid - 4 * grp;  // this lane's keys 16 mt + i are valid below lim
-      auto valid = [&](int mt, int i) { return mt < NT && (FULL || mt * 16 + i < lim); };
-      float head;
-      if (lse) {
+      auto valid = [&](int mt, int i) { return FULL || mt * 16 + i < lim; };
+      if constexpr (LSE) {
         float m = -INFINITY;
 #pragma unroll
         for (int mt = 0; mt < NTM; ++mt)
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            if (valid(mt, i)) m = fmaxf(m, s[mt][i] * a.scale);
-        m = xor32_max(xor16_max(m));
+            if (valid(mt, i)) m = fmaxf(m, s[mt][i]);
+        m = xor32_max(xor16_max(m)) * scale2;
         float e = 0.f;
 #pragma unroll
         for (int mt = 0; mt < NTM; ++mt)
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            if (valid(mt, i)) e += __expf(s[mt][i] * a.scale - m);
+            if (valid(mt, i)) e += __builtin_amdgcn_exp2f(fmaf(s[mt][i], scale2, -m));
         e = xor32_sum(xor16_sum(e));
-        head = m + __logf(e);
+        return (m + __builtin_amdgcn_logf(e)) * 0.69314718055994530942f;
       } else {
         float s1 = 0.f, s2 = 0.f;
 #pragma unroll
@@ -606,16 +608,10 @@ __global__ void __launch_bounds__(64 * SPAN, PISA_LEAF_SPLIT_WAVES) leaf_split_k
             }
         s1 = xor32_sum(xor16_sum(s1));
         s2 = xor32_sum(xor16_sum(s2));
-        if (pisa1) {
-          head = s1;
-        } else {
-          const float cnt = (float)rows_valid;
-          const float mean = s1 / cnt;
-          const float var = fmaxf(s2 / cnt - mean * mean, 0.f);
-          head = a.scale * mean + half_scale2 * var;
-        }
+        const float mean = s1 * inv_rows;
+        const float var = fmaxf(s2 * inv_rows - mean * mean, 0.f);
+        return a.scale * mean + half_scale2 * var;
       }
-      return head;
     };
     auto score_batch = [&](auto full_tag, int batch) __attribute__((always_inline)) {
       const T* qb = qs + (size_t)(batch & 1) * NU * 16 * LDQ;
@@ -629,10 +625,8 @@ __global__ void __launch_bounds__(64 * SPAN, PISA_LEAF_SPLIT_WAVES) leaf_split_k
 #pragma unroll
         for (int mt = 0; mt < NTM; ++mt) {
           s[mt] = f4{0.f, 0.f, 0.f, 0.f};
-          if (mt < NT) {
 #pragma unroll
-            for (int d = 0; d < DS; ++d) s[mt] = Op::mma(kreg[mt][d], qf[d], s[mt]);
-          }
+          for (int d = 0; d < DS; ++d) s[mt] = Op::mma(kreg[mt][d], qf[d], s[mt]);
         }
         const float head = head_of(full_tag, s);
         const int rho = u * 16 + col;
@@ -683,7 +677,7 @@ __global__ void __launch_bounds__(64 * SPAN, PISA_LEAF_SPLIT_WAVES) leaf_split_k
       else run1(full_tag);
     };
     // FULL: every key of every block of the span is valid (uniform over the workgroup)
-    const bool full = NT * 16 == a.C && (blk0 + SPAN) * a.C <= a.src_rows;
+    const bool full = NTM * 16 == a.C && (blk0 + SPAN) * a.C <= a.src_rows;
     if (full) run(std::true_type{});
     else run(std::false_type{});
   }
@@ -699,14 +693,14 @@ constexpr size_t kLeafWideLds = 48 << 10;
 
 // Split-span kernel of `SPAN` waves; grid = the resident workgroups of the device
 // (a multiple of 8 for the XCD tile walk).
-template <typename T, int HD, int SPAN>
+template <typename T, int HD, int SPAN, int NTM, bool LSE>
 static void launch_leaf_split(const LeafArgs& a, int cus, hipStream_t stream) {
   constexpr int vpr = HD * (int)sizeof(T) / 16;
   // PISA_LEAF_NU units per batch at four waves, in proportion to the waves
   // otherwise (the same staging loads per thread), and at least one load per thread
   constexpr int NU0 = PISA_LEAF_NU * SPAN / 4 > 0 ? PISA_LEAF_NU * SPAN / 4 : 1;
   constexpr int NU = NU0 * 16 * vpr >= 64 * SPAN ? NU0 : 64 * SPAN / (16 * vpr);
-  const void* kernel = (const void*)leaf_split_kernel<T, HD, SPAN, NU>;
+  const void* kernel = (const void*)leaf_split_kernel<T, HD, SPAN, NU, NTM, LSE>;
   const size_t lds = leaf_split_lds<T, HD>(NU, a.tile);
   allow_lds(kernel, lds);
   static int per_cu = 0;  // per instance
@@ -716,14 +710,34 @@ static void launch_leaf_split(const LeafArgs& a, int cus, hipStream_t stream) {
     per_cu = n;
   }
   const dim3 grid(cus * per_cu / 8 * 8 > 0 ? cus * per_cu / 8 * 8 : 8);
-  PISA_TIMED("leaf", stream, hipLaunchKernelGGL((leaf_split_kernel<T, HD, SPAN, NU>), grid, dim3(64 * SPAN), lds, stream, a));
+  PISA_TIMED("leaf", stream, hipLaunchKernelGGL((leaf_split_kernel<T, HD, SPAN, NU, NTM, LSE>), grid, dim3(64 * SPAN), lds, stream, a));
+}
+
+template <typename T, int HD, int SPAN>
+static void launch_leaf_split_s(const LeafArgs& a, int cus, hipStream_t stream) {
+  typedef QkShape<T, HD> S;
+  const int nt = (a.C + S::KQ - 1) / S::KQ * S::KQ / 16;  // key tiles of a block
+  const bool lse = a.method == PISA_METHOD_LSE;
+  if (nt <= 2) {
+    if (lse) launch_leaf_split<T, HD, SPAN, 2, true>(a, cus, stream);
+    else launch_leaf_split<T, HD, SPAN, 2, false>(a, cus, stream);
+  } else {
+    if (lse) launch_leaf_split<T, HD, SPAN, 4, true>(a, cus, stream);
+    else launch_leaf_split<T, HD, SPAN, 4, false>(a, cus, stream);
+  }
+}
+
+template <typename T, int HD>
+static void launch_leaf_split_t(const LeafArgs& a, int cus, hipStream_t stream) {
+  if (a.span == 4) launch_leaf_split_s<T, HD, 4>(a, cus, stream);
+  else launch_leaf_split_s<T, HD, 2>(a, cus, stream);
 }
 
 template <typename T, int HD>
 static void launch_leaf_tile(const LeafArgs& a, int cus, hipStream_t stream) {
   if constexpr (sizeof(T) == 2) {
-    if (PISA_LEAF_SPLIT && a.span == 4) return launch_leaf_split<T, HD, 4>(a, cus, stream);
-    if (PISA_LEAF_SPLIT && a.span == 2) return launch_leaf_split<T, HD, 2>(a, cus, stream);
+    if (PISA_LEAF_SPLIT && (a.span == 2 || a.span == 4) && a.method != PISA_METHOD_PISA1 && a.scale > 0.f)
+      return launch_leaf_split_t<T, HD>(a, cus, stream);
   }
   const LeafLds L = leaf_lds<T, HD>(a.C, a.tile, a.span);
   const int nt = L.Cq / 16;
