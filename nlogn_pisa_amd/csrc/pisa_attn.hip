@@ -375,6 +375,10 @@ __host__ __device__ inline TileLds tile_lds(int C, int tile, int waves, bool wit
 #ifndef PISA_ATTN_WAVES
 #define PISA_ATTN_WAVES 2
 #endif
+// 1: the forward tile kernel walks its tiles XCD-contiguously (xcd_tiles).
+#ifndef PISA_ATTN_XCD
+#define PISA_ATTN_XCD 0
+#endif
 // 1: every backward takes the LDS-staged kernel (for comparisons).
 #ifndef PISA_BWD_LDS
 #define PISA_BWD_LDS 0
@@ -676,7 +680,12 @@ __global__ void __launch_bounds__(256, PISA_ATTN_WAVES) attn_fwd_tile_kernel(Att
   typedef typename PartialT<T>::type PT;
   PT* so = STAGE ? reinterpret_cast<PT*>(smem + L.o_off) + wave * 16 * L.ldo : nullptr;
   const int ntiles = *a.num_tiles;
-  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+#if PISA_ATTN_XCD
+  const XcdTiles walk = xcd_tiles(ntiles);  // grid_size() is a multiple of 8
+#else
+  const XcdTiles walk{(int)blockIdx.x, ntiles, (int)gridDim.x};
+#endif
+  for (int tile = walk.begin; tile < walk.end; tile += walk.step) {
     const int g = a.tile_group[tile];
     const int64_t blk = g % a.M0;
     const int bh = g / a.M0;

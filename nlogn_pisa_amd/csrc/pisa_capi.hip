@@ -25,15 +25,19 @@ int padded_group(int g) { return next_pow2(g); }
 
 namespace pisa {
 
-// Window budget: q bytes of all heads per window (0: a single window).
+// Window budgets: q bytes of all heads per window of leaf scoring and of the
+// attention forward (0: a single window).
 #ifndef PISA_WINDOW_BYTES
 #define PISA_WINDOW_BYTES (128 << 20)
 #endif
+#ifndef PISA_ATTN_WINDOW_BYTES
+#define PISA_ATTN_WINDOW_BYTES PISA_WINDOW_BYTES
+#endif
 
-int query_window(int64_t tokens, int64_t row_bytes) {
-  if (PISA_WINDOW_BYTES <= 0) return (int)std::max<int64_t>(1, tokens);
+int query_window(int64_t tokens, int64_t row_bytes, int64_t budget) {
+  if (budget <= 0) return (int)std::max<int64_t>(1, tokens);
   int64_t w = 256;
-  while (w * 2 * std::max<int64_t>(row_bytes, 1) <= (int64_t)PISA_WINDOW_BYTES) w *= 2;
+  while (w * 2 * std::max<int64_t>(row_bytes, 1) <= budget) w *= 2;
   return (int)std::max<int64_t>(1, std::min<int64_t>(w, tokens));
 }
 
@@ -106,7 +110,7 @@ int plan_select(const pisa_qk_desc* qk, const pisa_select_params* p, SelectPlan&
   pl.spans = (pl.M0 + pl.span - 1) / pl.span;
   pl.groups = (int64_t)qk->batch * qk->key_heads * pl.spans;
   const int64_t flat = (int64_t)qk->batch * qk->query_tokens;
-  pl.window = query_window(flat, (int64_t)qk->query_heads * D * es);
+  pl.window = query_window(flat, (int64_t)qk->query_heads * D * es, PISA_WINDOW_BYTES);
   pl.window_slots = (int64_t)pl.window * qk->key_heads * pl.W / pl.span;
   // routing levels scored densely (every node for every item) before the route
   for (int l = 0; l < PISA_MAX_LEVELS; ++l) pl.dense_nodes[l] = 0;
@@ -308,7 +312,8 @@ namespace {
 
 int leaf_window(const pisa_qk_desc* qk) {
   return query_window((int64_t)qk->batch * qk->query_tokens,
-                      (int64_t)qk->query_heads * qk->head_dim * dtype_size(qk->dtype));
+                      (int64_t)qk->query_heads * qk->head_dim * dtype_size(qk->dtype),
+                      PISA_WINDOW_BYTES);
 }
 
 void carve_leaf(const pisa_qk_desc* qk, int block_size, int width, Carve& c, uint8_t** mask,
@@ -434,7 +439,8 @@ int plan_attn(const pisa_attn_desc* d, AttnPlan& pl) {
   pl.groups = (int64_t)d->batch * d->key_heads * pl.M0;
   pl.Cp = (d->block_size + 15) / 16 * 16;
   pl.grouped = pl.slots >= 4 * pl.groups;
-  pl.window = query_window((int64_t)d->batch * d->query_tokens, (int64_t)d->query_heads * d->head_dim * es);
+  pl.window = query_window((int64_t)d->batch * d->query_tokens, (int64_t)d->query_heads * d->head_dim * es,
+                           PISA_ATTN_WINDOW_BYTES);
   pl.window_slots = (int64_t)pl.window * d->key_heads * d->topk;
   return PISA_OK;
 }

@@ -111,11 +111,11 @@ int bucket_leaf(const LeafRequests& src, int64_t slot_begin, int64_t slot_end, B
 int bucket_attn(const AttnRequests& src, int64_t slot_begin, int64_t slot_end, Buckets& b,
                 hipStream_t stream);
 
-// Query tokens per bucketing window: the q rows of all heads over a window
-// (row_bytes per token) stay within 128 MiB, so the tiles of a window re-read
-// them from the L2 and the 256 MB MALL instead of HBM.  Windows run over the
-// flattened (batch, token) axis.
-int query_window(int64_t tokens, int64_t row_bytes);
+// Query tokens per bucketing window: the largest power of two (at least 256)
+// whose q rows of all heads (row_bytes per token) stay within `budget` bytes,
+// so the tiles of a window re-read them from the L2 and the 256 MB MALL
+// instead of HBM.  Windows run over the flattened (batch, token) axis.
+int query_window(int64_t tokens, int64_t row_bytes, int64_t budget);
 
 int dtype_size(int dtype);
 // Compute units of the current device (cached per device).

@@ -575,9 +575,13 @@ __global__ void __launch_bounds__(64) route_grouped_kernel(RouteArgs a) {
   constexpr int R = RR;                    // support rows per candidate (<= 8)
   constexpr int cpt = 16 / R;              // candidates per 16 support rows
 
-  // Q^T: lane (grp, col) holds head col's dimensions 4 E s + E grp + e of step s
+  // Q^T: lane (grp, col) holds head col's dimensions 4 E s + E grp + e of step s.
+  // Only levels that gather support rows (and the fused leaf) read it: when
+  // every level above the leaf is dense, the query rows are not loaded at all.
+  bool gathers = FUSED;
+  for (int l = 1; l <= a.top; ++l) gathers = gathers || !a.dense[l];
   frag qb[DS];
-  if (col < a.G)
+  if (gathers && col < a.G)
     load_row_frags<E>(static_cast<const T*>(a.q) + b * a.q_batch + t * a.q_token +
                           ((int64_t)h * a.G + col) * HD + E * grp,
                       qb);
@@ -895,7 +899,10 @@ __global__ void __launch_bounds__(256) final_kernel(FinalArgs a) {
       if (id >= a.M0) id = -1;
       const bool valid = id >= 0 && (int64_t)id * a.C <= pos;
       const bool forced = valid && is_forced(id, leaf, 1, a.force_first, a.force_recent);
-      const float sc = a.scoreable[item * a.W + e] ? a.scores[item * a.W + e] : 0.f;
+      // the score is read whatever the flag says (one round trip, not two);
+      // slots that were not scored hold stale values and are selected away
+      const float raw = a.scores[item * a.W + e];
+      const float sc = a.scoreable[item * a.W + e] ? raw : 0.f;
       s[j] = valid ? (forced ? kForced : sc) : kInvalid;
       idv[j] = id;
     } else {
