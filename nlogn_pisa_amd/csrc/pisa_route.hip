@@ -875,6 +875,187 @@ __global__ void __launch_bounds__(256) route_dense_kernel(RouteArgs a) {
   }
 }
 
+// route_dense_lds_kernel: route_dense_kernel with the support rows shared by
+// the four waves of a workgroup, all of one (batch, kv head): chunks of
+// kDenseCT 16-row support tiles are read from memory once per workgroup into
+// LDS (double buffered, the next chunk's loads in flight while one is scored)
+// and each wave takes its MFMA fragments from there.  The products, their order
+// and the per-node scores are the same as route_dense_kernel's.  16-bit inputs.
+constexpr int kDenseCT = 4;
+
+#ifndef PISA_DENSE_LDS
+#define PISA_DENSE_LDS 1
+#endif
+
+template <typename T, int HD, int RR, int MODE>
+__global__ void __launch_bounds__(256) route_dense_lds_kernel(RouteArgs a) {
+  typedef QkShape<T, HD> S;
+  typedef typename S::Op Op;
+  typedef typename S::frag frag;
+  constexpr int E = S::E, DS = S::DS;
+  constexpr int NCT = 4;                   // query tiles per wave
+  constexpr bool own = MODE == kModeOwn;   // support = the node's own summary
+  constexpr bool LSE = MODE == kModeLse;
+  constexpr int R = RR;
+  constexpr int vec = 16 / (int)sizeof(T);
+  constexpr int vpr = HD / vec;            // 16-byte chunks of a support row
+  constexpr int LDR = HD + vec;            // LDS row: 16 bytes of padding
+  constexpr int CR = kDenseCT * 16;        // support rows per chunk
+  constexpr int LPT = (CR * vpr + 255) / 256;  // staging loads per thread and chunk
+  static_assert(sizeof(T) == 2, "16-bit support rows");
+  __shared__ float stage[4][16][kDenseChunk + 1];
+  __shared__ __attribute__((aligned(16))) T rows_s[2][CR * LDR];
+
+  const int level = a.dense_level;
+  const int Gp = next_pow2(a.G);           // <= 16
+  const int P = 16 / Gp;                   // items per query tile
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int col = lane & 15, grp = lane >> 4;
+  const int per_bh = (a.T + 4 * NCT * P - 1) / (4 * NCT * P);  // workgroups per (batch, kv head)
+  const int bh = blockIdx.x / per_bh;
+  if (bh >= a.batch * a.Hkv) return;       // uniform over the workgroup
+  // waves whose tokens start past T score nothing but join the staging and barriers
+  const int t0 = ((blockIdx.x - bh * per_bh) * 4 + wave) * NCT * P;
+  const int b = bh / a.Hkv, h = bh % a.Hkv;
+  const int hd = col % Gp;
+  // query tiles: column col of tile c is head hd of token t0 + c P + col / Gp
+  frag qb[NCT][DS];
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) {
+    const int t = t0 + c * P + col / Gp;
+    if (t < a.T && hd < a.G)
+      load_row_frags<E>(static_cast<const T*>(a.q) + b * a.q_batch + (int64_t)t * a.q_token +
+                            ((int64_t)h * a.G + hd) * HD + E * grp,
+                        qb[c]);
+    else
+      zero_frags(qb[c]);
+  }
+  const int M = a.lengths[level];
+  const int64_t stride = dense_stride(M);
+  float (*sw)[kDenseChunk + 1] = stage[wave];
+  const int src_level = own ? level : level - 1;
+  const T* base = static_cast<const T*>(a.summary) + b * a.sum_batch +
+                  ((int64_t)a.offsets[src_level] * a.Hkv + h) * HD;
+  const int64_t rstride = (int64_t)a.Hkv * HD;
+  const int len = a.lengths[src_level];
+  const int nrows = own ? M : M * R;
+  const int ntile = (nrows + 15) / 16;
+  const int nchunk = (ntile + kDenseCT - 1) / kDenseCT;
+  float* out = a.dense[level];
+  const int64_t item0 = ((int64_t)b * a.T + t0) * a.Hkv + h;  // item of token t0
+
+  // support rows of chunk ch into registers (rows past the level read row 0,
+  // masked by the counts), then into LDS buffer `buf`
+  static_assert(LPT <= kDenseCT, "one staging load per thread and tile");
+  // piece j of chunk ch: 16 bytes of support row per thread (rows past the
+  // level read row 0, masked by the counts); put() writes it to LDS buffer buf
+  auto piece = [&](int ch, int j) __attribute__((always_inline)) {
+    const int idx = min(j * 256 + tid, CR * vpr - 1);
+    const int r = ch * CR + idx / vpr;
+    const bool ok = r < nrows && (own || r < len);
+    return *reinterpret_cast<const uint4*>(base + (int64_t)(ok ? r : 0) * rstride + (idx % vpr) * vec);
+  };
+  auto put = [&](int buf, int j, const uint4& v) __attribute__((always_inline)) {
+    const int idx = j * 256 + tid;
+    if (CR * vpr % 256 == 0 || idx < CR * vpr)
+      *reinterpret_cast<uint4*>(rows_s[buf] + (idx / vpr) * LDR + (idx % vpr) * vec) = v;
+  };
+  // valid support rows of node n (0 past the level)
+  auto count = [&](int n) __attribute__((always_inline)) { return n >= M ? 0 : own ? 1 : max(0, min(R, len - n * R)); };
+  auto store = [&](int c, int n, float head) __attribute__((always_inline)) {
+    const float tot = group_sum(hd < a.G ? head : 0.f, Gp);
+    if (hd == 0) sw[c * P + col / Gp][n % kDenseChunk] = tot;
+  };
+  // the staged nodes [64 k, 64 k + 64) of the wave's items -> their rows
+  auto flush = [&](int k) __attribute__((always_inline)) {
+    wave_lds_sync();
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int il = 4 * u + (lane >> 4), nl = 4 * (lane & 15);
+      const int t = t0 + il;
+      if (il < NCT * P && t < a.T) {
+        const float4 v = make_float4(sw[il][nl], sw[il][nl + 1], sw[il][nl + 2], sw[il][nl + 3]);
+        *reinterpret_cast<float4*>(out + (item0 + (int64_t)il * a.Hkv) * stride +
+                                   k * kDenseChunk + nl) = v;
+      }
+    }
+    wave_lds_sync();
+  };
+  const int tiles_per_chunk = kDenseChunk * (own ? 1 : R) / 16;
+  auto tile = [&](int mt, const frag (&xf)[DS]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int c = 0; c < NCT; ++c) {
+      f4 sv = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int d = 0; d < DS; ++d) sv = Op::mma(xf[d], qb[c][d], sv);
+      const float v[4] = {sv[0], sv[1], sv[2], sv[3]};
+      if constexpr (R <= 4) {
+#pragma unroll
+        for (int j = 0; j < 4 / R; ++j) {
+          const int n = (mt * 16 + 4 * grp) / R + j;
+          float head;
+          if constexpr (own) {
+            head = v[j];
+          } else {
+            const SupportAcc acc = support_acc<LSE>(v + j * R, R, count(n), a.scale);
+            head = support_final<MODE>(acc, v + j * R, a.scale);
+          }
+          store(c, n, head);
+        }
+      } else {
+        // R = 8: lane groups 2k (children 0-3) and 2k + 1 (children 4-7) of node 2 mt + k
+        const int n = mt * 2 + (grp >> 1);
+        const int cnt = count(n) - 4 * (grp & 1);
+        SupportAcc acc = support_acc<LSE>(v, 4, cnt, a.scale);
+        SupportAcc other;
+        other.a0 = __shfl_xor(acc.a0, 16);
+        other.a1 = __shfl_xor(acc.a1, 16);
+        other.n = __shfl_xor(acc.n, 16);
+        acc = (grp & 1) ? support_join<LSE>(other, acc) : support_join<LSE>(acc, other);
+        const float head = support_final<MODE == kModeBinary ? kModeMoments : MODE>(acc, v, a.scale);
+        store(c, n, head);
+      }
+    }
+  };
+  auto done = [&](int mt) __attribute__((always_inline)) {
+    if ((mt + 1) % tiles_per_chunk == 0 || mt + 1 == ntile) flush(mt / tiles_per_chunk);
+  };
+  // Chunk ch is scored from buffer ch & 1 while chunk ch + 1 goes into the
+  // other buffer, whose readers (chunk ch - 1) passed the previous barrier.
+  // Tile i of a chunk loads piece i of the next chunk and stores piece i - 1,
+  // so each staging load is in flight for one tile and held by no copy.
+  {
+    uint4 st[LPT];
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) st[j] = piece(0, j);
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) put(0, j, st[j]);
+  }
+  __syncthreads();
+  for (int ch = 0; ch < nchunk; ++ch) {
+    // the last chunk reloads itself into the idle buffer (no branch around the
+    // loads, so none of them is waited for early)
+    const int next = min(ch + 1, nchunk - 1);
+    const int nb = (ch + 1) & 1;
+    const T* rows = rows_s[ch & 1];
+    uint4 st[LPT];
+#pragma unroll
+    for (int i = 0; i < kDenseCT; ++i) {
+      if (i < LPT) st[i < LPT ? i : 0] = piece(next, i);
+      if (i >= 1 && i - 1 < LPT) put(nb, i - 1, st[i >= 1 ? i - 1 : 0]);
+      const int mt = ch * kDenseCT + i;
+      if (mt < ntile) {
+        frag xf[DS];
+        load_row_frags<E>(rows + (i * 16 + col) * LDR + E * grp, xf);
+        tile(mt, xf);
+        done(mt);
+      }
+    }
+    if (LPT == kDenseCT) put(nb, kDenseCT - 1, st[LPT - 1]);
+    __syncthreads();
+  }
+}
+
 // Final leaf network of the grouped schedule (final_kernel,
 // top_k_pyramid_triton.py:279-308, with the Torch sentinels :169-171 and
 // output mask :176).  One wave per item, four items per workgroup.
@@ -1066,7 +1247,14 @@ bool route_level_dense(int G, int level, int top, int first_width, int branching
 
 template <typename T, int HD, int RR, int MODE>
 static void launch_dense_rm(const RouteArgs& a, int blocks, hipStream_t stream) {
-  PISA_TIMED("route_dense", stream, hipLaunchKernelGGL((route_dense_kernel<T, HD, RR, MODE>), dim3(blocks), dim3(256), 0, stream, a));
+  if constexpr (sizeof(T) == 2 && PISA_DENSE_LDS) {
+    // four waves of 16 / Gp items x 4 query tiles per workgroup, one (batch, kv head) each
+    const int per = 16 * (16 / next_pow2(a.G));
+    const int64_t groups = (int64_t)a.batch * a.Hkv * ((a.T + per - 1) / per);
+    PISA_TIMED("route_dense", stream, hipLaunchKernelGGL((route_dense_lds_kernel<T, HD, RR, MODE>), dim3(groups), dim3(256), 0, stream, a));
+  } else {
+    PISA_TIMED("route_dense", stream, hipLaunchKernelGGL((route_dense_kernel<T, HD, RR, MODE>), dim3(blocks), dim3(256), 0, stream, a));
+  }
 }
 
 template <typename T, int HD>
