@@ -124,9 +124,11 @@ def tile_count(w, valid, ids, elem, blocks=None):
     return int(((per + TILE - 1) // TILE).sum())
 
 # kernel names of the bench's timing keys in the rocprofv3 summaries under profiles/
-PROFILED = {"attn_fwd": "attn_fwd_tile_kernel", "leaf": "leaf_tile_kernel",
-            "route": "route_grouped_kernel", "attn_combine": "attn_combine_kernel",
-            "final": "final_kernel"}
+PROFILED = {"attn_fwd": ("attn_fwd_tile_kernel",),
+            "leaf": ("leaf_split_kernel", "leaf_tile_kernel"),
+            "route": ("route_grouped_kernel",),
+            "route_dense": ("route_dense_lds_kernel", "route_dense_kernel"),
+            "attn_combine": ("attn_combine_kernel",), "final": ("final_kernel",)}
 
 
 def profiled_traffic(kernel, workload):
@@ -135,12 +137,12 @@ def profiled_traffic(kernel, workload):
     dispatch, scaled by a plain copy), or None when no summary covers it."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                         f"{workload}_kernels.md")
-    name = PROFILED.get(kernel)
-    if not name or not os.path.exists(path):
+    names = PROFILED.get(kernel)
+    if not names or not os.path.exists(path):
         return None
     for line in open(path):
         cells = [c.strip().strip("`") for c in line.strip().strip("|").split("|")]
-        if len(cells) >= 5 and cells[0].startswith(name + "<") and cells[0] != name:
+        if len(cells) >= 5 and any(cells[0].startswith(n + "<") for n in names):
             try:
                 return int(float(cells[4]) * 1e9)   # total GB per dispatch
             except ValueError:

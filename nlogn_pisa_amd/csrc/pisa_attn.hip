@@ -815,6 +815,107 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a, int64_t i
   }
 }
 
+// The same merge in two passes (rows of at most kCombinePairs (slot, head)
+// pairs, G a power of two <= 64): first one lane per pair reads the partial's
+// log-sum-exp; per head M = max over the visible slots, w_s = e^(lse_s - M) and
+// L = sum w_s (lanes of one head joined by xor shuffles), the weights going to
+// the wave's LDS.  Then O = sum_s w_s o_s / L in slot order, one FMA per
+// element and slot, and LSE = M + ln L.
+constexpr int kCombinePairs = 256;
+
+#ifndef PISA_COMBINE2
+#define PISA_COMBINE2 1
+#endif
+
+template <typename T>
+__global__ void __launch_bounds__(256) attn_combine2_kernel(AttnArgs a, int64_t items) {
+  typedef typename PartialT<T>::type PT;
+  constexpr int V = 16 / sizeof(PT);
+  constexpr int U = 8;  // slots in flight
+  __shared__ float wts[4][kCombinePairs];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t item = (int64_t)blockIdx.x * (blockDim.x >> 6) + wave;
+  if (item >= items) return;  // waves synchronise only with themselves
+  float* wl = wts[wave];
+  const int64_t slot0 = item * a.K;
+  const RowInfo ri = row_info(a, slot0);
+  const int G = a.G, pairs = a.K * G;
+  const int gl = 31 - __clz(G);
+  // pass 1: this lane's pairs lane + 64 j, all of head lane & (G - 1)
+  float m = -INFINITY;
+  float lse[kCombinePairs / 64];
+  bool vis[kCombinePairs / 64];
+#pragma unroll
+  for (int j = 0; j < kCombinePairs / 64; ++j) {
+    const int idx = lane + 64 * j;
+    const int ic = min(idx, pairs - 1);  // every lane loads; pairs past the row are masked
+    const int64_t blk = slot_block(a, slot0 + (ic >> gl));
+    lse[j] = stream_load(a.part_lse + slot0 * G + ic);
+    vis[j] = idx < pairs && slot_visible(a, blk, ri.pos);
+    if (vis[j]) m = fmaxf(m, lse[j]);
+  }
+  for (int off = G; off < 64; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+  float l = 0.f;
+#pragma unroll
+  for (int j = 0; j < kCombinePairs / 64; ++j) {
+    const int idx = lane + 64 * j;
+    const float w = vis[j] ? __expf(lse[j] - m) : 0.f;
+    l += w;
+    if (idx < pairs) wl[idx] = w;
+  }
+  for (int off = G; off < 64; off <<= 1) l += __shfl_xor(l, off);
+  wave_lds_sync();
+  // pass 2: lane (g, c) owns 16-byte chunk c of head g's row
+  const int chunks = a.Dv / V;
+  const int work = G * chunks;
+  const PT* part = static_cast<const PT*>(a.part_o);
+  for (int base = 0; base < work; base += 64) {
+    const int idx = min(base + lane, work - 1);
+    const bool writer = base + lane < work;
+    const int g = idx / chunks, c = idx % chunks;
+    const float mg = __shfl(m, g), lg = __shfl(l, g);  // lane g holds head g's M and L
+    float acc[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) acc[v] = 0.f;
+    for (int s0 = 0; s0 < a.K; s0 += 64) {
+      const int n = min(64, a.K - s0);
+      const bool vis_l = lane < n && slot_visible(a, slot_block(a, slot0 + s0 + lane), ri.pos);
+      const uint64_t vmask = __ballot(vis_l);
+      for (int s = 0; s < n; s += U) {
+        union {
+          uint4 u;
+          PT e[V];
+        } x[U];
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+          const int64_t row = (slot0 + s0 + min(s + j, n - 1)) * G + g;
+          x[j].u = stream_load16(part + row * a.Dv + c * V);
+        }
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+          if (s + j < n && ((vmask >> (s + j)) & 1)) {
+            const float w = wl[(s0 + s + j) * G + g];
+#pragma unroll
+            for (int v = 0; v < V; ++v) acc[v] = fmaf(w, (float)x[j].e[v], acc[v]);
+          }
+        }
+      }
+    }
+    if (!writer) continue;
+    const float inv = lg > 0.f ? 1.f / lg : 0.f;
+    const int64_t orow = item * G + g;  // == ((b*T + t)*Hq + h*G + g)
+    T* out = static_cast<T*>(a.out) + orow * a.Dv + c * V;
+#pragma unroll
+    for (int v = 0; v < V; ++v) out[v] = from_f<T>(acc[v] * inv);
+    if (a.out_f32) {
+      float* out32 = a.out_f32 + orow * a.Dv + c * V;
+#pragma unroll
+      for (int v = 0; v < V; ++v) out32[v] = acc[v] * inv;
+    }
+    if (c == 0) a.lse_out[orow] = mg == -INFINITY ? -INFINITY : mg + __logf(lg);
+  }
+}
+
 template <typename T>
 __global__ void __launch_bounds__(256) attn_delta_kernel(AttnArgs a, int64_t rows) {
   const int lane = threadIdx.x & 63;
@@ -1836,6 +1937,17 @@ int launch_attn_partials(int dtype, const AttnArgs& a, bool grouped, int64_t slo
 int launch_attn_combine(int dtype, const AttnArgs& a, int64_t items, hipStream_t stream) {
   if (items <= 0) return PISA_OK;
   const dim3 grid((unsigned)((items + 3) / 4)), block(256);
+  const bool two_pass = PISA_COMBINE2 && a.K >= 1 && (int64_t)a.K * a.G <= kCombinePairs &&
+                        a.G <= 64 && (a.G & (a.G - 1)) == 0;
+  if (two_pass) {
+    switch (dtype) {
+      case PISA_F32: PISA_TIMED("attn_combine", stream, hipLaunchKernelGGL(attn_combine2_kernel<float>, grid, block, 0, stream, a, items)); break;
+      case PISA_F16: PISA_TIMED("attn_combine", stream, hipLaunchKernelGGL(attn_combine2_kernel<f16_t>, grid, block, 0, stream, a, items)); break;
+      case PISA_BF16: PISA_TIMED("attn_combine", stream, hipLaunchKernelGGL(attn_combine2_kernel<bf16_t>, grid, block, 0, stream, a, items)); break;
+      default: return fail(PISA_ERR_INVALID, "unknown dtype %d", dtype);
+    }
+    return check_launch("attention combine");
+  }
   switch (dtype) {
     case PISA_F32: PISA_TIMED("attn_combine", stream, hipLaunchKernelGGL(attn_combine_kernel<float>, grid, block, 0, stream, a, items)); break;
     case PISA_F16: PISA_TIMED("attn_combine", stream, hipLaunchKernelGGL(attn_combine_kernel<f16_t>, grid, block, 0, stream, a, items)); break;
