@@ -128,7 +128,7 @@ PROFILED = {"attn_fwd": ("attn_fwd_tile_kernel",),
             "leaf": ("leaf_split_kernel", "leaf_tile_kernel"),
             "route": ("route_grouped_kernel",),
             "route_dense": ("route_dense_lds_kernel", "route_dense_kernel"),
-            "attn_combine": ("attn_combine_kernel",), "final": ("final_kernel",)}
+            "attn_combine": ("attn_combine2_kernel", "attn_combine_kernel"), "final": ("final_kernel",)}
 
 
 def profiled_traffic(kernel, workload):
