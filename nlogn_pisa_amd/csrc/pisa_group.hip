@@ -100,23 +100,41 @@ __global__ void __launch_bounds__(kBucketThreads) bucket_hist_kernel(Src src, in
 }
 
 // Column g of hist becomes exclusive offsets; counts[g] = the group's total.
+// A workgroup takes 16 groups x kOffSegs row segments (at most 64 rows each):
+// a thread loads its segment of one column (all loads in flight) and sums it,
+// the segment sums are scanned in LDS, and the thread rewrites its rows as
+// exclusive offsets - one read and one write per entry, groups / 16 workgroups.
+constexpr int kOffSegs = 16;
+static_assert(kMaxBucketGroups <= kOffSegs * 64, "histogram rows per column segment");
+
 __global__ void __launch_bounds__(256) bucket_offsets_kernel(int32_t* hist, int rows, int groups,
                                                              int32_t* counts) {
-  const int g = blockIdx.x * blockDim.x + threadIdx.x;
-  if (g >= groups) return;
-  constexpr int B = 16;  // rows loaded before their offsets are stored
-  int32_t run = 0;
-  for (int w0 = 0; w0 < rows; w0 += B) {
-    int32_t v[B];
+  __shared__ int32_t part[kOffSegs][17];
+  const int gl = threadIdx.x & 15, seg = threadIdx.x >> 4;
+  const int g = blockIdx.x * 16 + gl;
+  const int per = (rows + kOffSegs - 1) / kOffSegs;  // <= 64
+  const int r0 = seg * per, r1 = min(rows, r0 + per);
+  const int gc = min(g, groups - 1);  // every lane loads; columns past the end are not written
+  int32_t v[64];
+  int32_t sum = 0;
 #pragma unroll
-    for (int u = 0; u < B; ++u) v[u] = w0 + u < rows ? hist[(int64_t)(w0 + u) * groups + g] : 0;
-#pragma unroll
-    for (int u = 0; u < B; ++u) {
-      if (w0 + u < rows) hist[(int64_t)(w0 + u) * groups + g] = run;
-      run += v[u];
-    }
+  for (int i = 0; i < 64; ++i) {
+    const int r = min(r0 + i, rows - 1);
+    const int32_t x = hist[(int64_t)r * groups + gc];
+    v[i] = r0 + i < r1 ? x : 0;
+    sum += v[i];
   }
-  counts[g] = run;
+  part[seg][gl] = sum;
+  __syncthreads();
+  int32_t run = 0;
+  for (int s = 0; s < seg; ++s) run += part[s][gl];
+  if (g >= groups) return;
+#pragma unroll
+  for (int i = 0; i < 64; ++i) {
+    if (r0 + i < r1) hist[(int64_t)(r0 + i) * groups + g] = run;
+    run += v[i];
+  }
+  if (seg == kOffSegs - 1) counts[g] = run;
 }
 
 // Place the requests of chunk w: rank = offset of its group in row w + LDS rank.
@@ -338,7 +356,7 @@ static int run_buckets(const Src& src, int64_t slot_begin, int64_t slot_end, Buc
     allow_lds((const void*)bucket_place_kernel<Src>, lds);
     PISA_TIMED("bucket_count", stream, hipLaunchKernelGGL((bucket_hist_kernel<Src>), dim3(rows), dim3(kBucketThreads), lds, stream,
                        src, slot_begin, slot_end, chunk, (int)b.groups, b.hist));
-    PISA_TIMED("bucket_count", stream, hipLaunchKernelGGL(bucket_offsets_kernel, dim3((b.groups + 255) / 256), dim3(256), 0, stream,
+    PISA_TIMED("bucket_count", stream, hipLaunchKernelGGL(bucket_offsets_kernel, dim3((b.groups + 15) / 16), dim3(256), 0, stream,
                        b.hist, (int)rows, (int)b.groups, b.counts));
     PISA_TIMED("bucket_scan", stream, hipLaunchKernelGGL(bucket_scan_kernel, dim3(1), dim3(1024), 0, stream, b.counts, b.groups,
                        b.tile, b.tile_off, b.num_tiles));

@@ -23,6 +23,14 @@ namespace pisa {
 
 constexpr int kMaxWidth = 512;
 
+// Widest candidate list of a grouped route (the top level's first_width or
+// branching x topk below it), rounded up to whole waves; its LDS is three such
+// int/float arrays.
+__host__ __device__ inline int grouped_route_width(int first_width, int branching, int topk) {
+  const int w = first_width > branching * topk ? first_width : branching * topk;
+  return (w + 63) / 64 * 64;
+}
+
 // Fused-schedule launches with at least this many items (batch x tokens x kv
 // heads) run one wave per item.
 constexpr int64_t kFusedWaveItems = 8192;
@@ -556,9 +564,13 @@ __global__ void __launch_bounds__(64) route_grouped_kernel(RouteArgs a) {
   typedef typename S::Op Op;
   typedef typename S::frag frag;
   constexpr int E = S::E, QL = S::QL, DS = S::DS;
-  __shared__ int ids_s[kMaxWidth];
-  __shared__ float sc_s[kMaxWidth];
-  __shared__ int list_s[kMaxWidth];
+  // candidate ids, scores and the scoreable list, each sized for the widest
+  // network of this call (grouped_route_lds), so more waves fit a CU
+  extern __shared__ int route_lds[];
+  const int wmax = grouped_route_width(a.first_width, a.branching, a.topk);
+  int* ids_s = route_lds;
+  float* sc_s = reinterpret_cast<float*>(route_lds + wmax);
+  int* list_s = route_lds + 2 * wmax;
 
   const int item = blockIdx.x;
   const int h = item % a.Hkv;
@@ -1151,7 +1163,8 @@ static int launch_route_t(const RouteArgs& a, int64_t items, int threads, hipStr
 
 template <typename T, int HD, int RR, int MODE, bool FUSED>
 static void launch_route_rm(const RouteArgs& a, int64_t items, hipStream_t stream) {
-  PISA_TIMED("route", stream, hipLaunchKernelGGL((route_grouped_kernel<T, HD, RR, MODE, FUSED>), dim3(items), dim3(64), 0, stream, a));
+  const size_t lds = (size_t)3 * sizeof(int) * grouped_route_width(a.first_width, a.branching, a.topk);
+  PISA_TIMED("route", stream, hipLaunchKernelGGL((route_grouped_kernel<T, HD, RR, MODE, FUSED>), dim3(items), dim3(64), lds, stream, a));
 }
 
 // One kernel per (support rows per candidate, scoring mode); the fused
