@@ -12,8 +12,9 @@
 // each take one contiguous chunk of the range and
 //   hist    - write the LDS histogram of their chunk as row w of a [W, groups]
 //             matrix (no global atomics);
-//   offsets - one thread per group turns its column into exclusive offsets
-//             (requests of that group in earlier chunks) and the group total;
+//   offsets - each group's column becomes exclusive offsets (requests of
+//             that group in earlier chunks) and the group total, 16 threads
+//             per column each scanning a segment of its rows;
 //   scan    - tiles per group, exclusive prefix sum, total tile count;
 //   scatter - each workgroup ranks its requests from its row of offsets plus
 //             LDS atomics, and writes them into their tiles.
@@ -42,8 +43,16 @@ struct LeafSrc {
   __device__ __forceinline__ bool get(int64_t req, int& group) const {
     const int64_t slot = req * r.span;
     int blk = -1;
-    for (int c = 0; c < r.span; ++c)
-      if (blk < 0 && r.scoreable[slot + c]) blk = r.cand[slot + c];
+    if (r.span == 4 && ((reinterpret_cast<uintptr_t>(r.cand) | reinterpret_cast<uintptr_t>(r.scoreable)) & 15) == 0) {
+      // the span's four flags and candidates in two independent aligned loads
+      // (slot is a multiple of 4 and both buffers start 16-byte aligned)
+      const uint32_t f = *reinterpret_cast<const uint32_t*>(r.scoreable + slot);
+      const int4 cd = *reinterpret_cast<const int4*>(r.cand + slot);
+      blk = (f & 0xffu) ? cd.x : (f & 0xff00u) ? cd.y : (f & 0xff0000u) ? cd.z : (f >> 24) ? cd.w : -1;
+    } else {
+      for (int c = 0; c < r.span; ++c)
+        if (blk < 0 && r.scoreable[slot + c]) blk = r.cand[slot + c];
+    }
     if (blk < 0) return false;
     const int64_t item = slot / r.width;
     const int h = (int)(item % r.heads);
