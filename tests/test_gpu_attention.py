@@ -71,6 +71,10 @@ CASES = [
     ("fp16-d128", 1, 384, 384, 8, 2, 128, 64, 4, "fp16", True, None),
     ("bf16-d64-c128", 1, 512, 640, 8, 2, 64, 128, 3, "bf16", True, None),
     ("bf16-g3", 2, 200, 260, 6, 2, 64, 64, 3, "bf16", True, None),
+    # the combine's two-pass limit of 256 (slot, head) pairs: 16 x 16 at it, 16 x 17 past it
+    # (the online merge), G = 3 above takes the online merge too
+    ("bf16-g16-k16", 1, 300, 1024, 16, 1, 64, 32, 16, "bf16", True, None),
+    ("bf16-g16-k17", 1, 300, 1024, 16, 1, 64, 32, 17, "bf16", True, None),
 ]
 
 
