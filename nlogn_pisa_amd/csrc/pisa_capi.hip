@@ -11,7 +11,11 @@ using namespace pisa;
 
 namespace {
 
-constexpr int kAttnTile = 256;  // requests per attention tile
+constexpr int kAttnTile = 256;  // requests per attention tile (backward)
+#ifndef PISA_ATTN_FWD_TILE
+#define PISA_ATTN_FWD_TILE 256
+#endif
+constexpr int kAttnFwdTile = PISA_ATTN_FWD_TILE;  // requests per attention forward tile
 
 bool pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
 
@@ -483,7 +487,7 @@ void carve_attn(const pisa_attn_desc* d, const AttnPlan& pl, bool backward, Carv
     const size_t part_elem = d->dtype == PISA_F32 ? 4 : 2;
     a.part_o = c.take<char>(pl.slots * pl.G * d->value_dim * part_elem);
     a.part_lse = c.take<float>(pl.slots * pl.G);
-    if (pl.grouped) carve_buckets(c, b, pl.window_slots, pl.groups, kAttnTile);
+    if (pl.grouped) carve_buckets(c, b, pl.window_slots, pl.groups, kAttnFwdTile);
   } else {
     a.delta = c.take<float>(pl.items * pl.G);
     a.part_dq = c.take<float>(pl.slots * pl.G * d->head_dim);

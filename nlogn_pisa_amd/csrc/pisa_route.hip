@@ -1250,12 +1250,15 @@ int launch_route(int dtype, const RouteArgs& a, int64_t items, int threads, hipS
 // gathers.  With one item per tile (Gp = 16) the extra pass over the query
 // rows outweighs the saving (measured), so dense levels need P >= 2; a wave's
 // 4 P items fit its 16 staging rows for P <= 4, i.e. Gp in {4, 8}.
+#ifndef PISA_DENSE_FACTOR
+#define PISA_DENSE_FACTOR 16
+#endif
 bool route_level_dense(int G, int level, int top, int first_width, int branching, int topk,
                        int nodes) {
   const int gp = next_pow2(G);
   if (level < 1 || level > top || gp < 4 || gp > 8 || branching > 8) return false;
   const int width = level == top ? first_width : branching * topk;
-  return (int64_t)nodes <= (int64_t)(16 / next_pow2(G)) * width;
+  return (int64_t)nodes <= (int64_t)(PISA_DENSE_FACTOR / gp) * width;
 }
 
 template <typename T, int HD, int RR, int MODE>
