@@ -773,10 +773,14 @@ static void launch_leaf_tile(const LeafArgs& a, int cus, hipStream_t stream) {
 #ifndef PISA_LEAF_MAX_SPAN
 #define PISA_LEAF_MAX_SPAN kMaxSpan
 #endif
+// Largest head group served by spans.
+#ifndef PISA_LEAF_SPAN_GROUP
+#define PISA_LEAF_SPAN_GROUP 4
+#endif
 int leaf_span(int dtype, int head_dim, int block_size, int branching, int group) {
   const int es = dtype_size(dtype);
   if (!es || (head_dim != 16 && head_dim != 32 && head_dim != 64 && head_dim != 128)) return 1;
-  if (group > 4 || block_size > 64) return 1;
+  if (group > PISA_LEAF_SPAN_GROUP || block_size > 64) return 1;
   const int E = es == 4 ? 1 : ((head_dim / 4) % 8 == 0 ? 8 : 4);
   const int KQ = E == 8 ? 32 : 16;
   const int cq = (block_size + KQ - 1) / KQ * KQ;
