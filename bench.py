@@ -419,7 +419,9 @@ def main():
                 "traffic": traffic, "avg_launch_ms": round(dom_ms, 4),
                 "launches_per_step": n_launch,
                 "algorithmic_bytes_per_launch": int(info["bytes"] / n_launch)}
-    # the survey's Q4 gather model of selection bytes (reference schedule)
+    # selection bytes of the reference's Q4 schedule (grouping_triton.py, leaf_triton.py:63-232):
+    # q rows once, internal candidates' child rows, candidates, one key block per tile of
+    # four leaf requests plus each request's q rows and bookkeeping, the final network's reads
     q4_bytes = (w.batch * w.tokens * w.query_heads * D * e + r_int * w.branching * D * e
                 + items * width * 4
                 + math.ceil(r_leaf / 4) * w.block_size * D * e + r_leaf * (G * D * e + 24)
