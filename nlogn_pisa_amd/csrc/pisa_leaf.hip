@@ -477,15 +477,24 @@ __host__ __device__ inline size_t leaf_split_lds(int nu, int tile) {
 #define PISA_LEAF_SPLIT_WAVES 3
 #endif
 
-// NTM: key tiles of a block (2: up to 32 keys, 4: up to 64); LSE: log-sum-exp
-// support scores, else the moment form (pisa2).
-template <typename T, int HD, int SPAN, int NU, int NTM, bool LSE>
-__global__ void __launch_bounds__(64 * SPAN, PISA_LEAF_SPLIT_WAVES) leaf_split_kernel(LeafArgs a) {
+// NTM: key tiles a wave holds (2: up to 32 keys, 4: up to 64); LSE: log-sum-exp
+// support scores, else the moment form (pisa2).  BW: waves per block - with two,
+// the waves of a pair hold keys [0, 64) and [64, 128) of a 128-key block; after
+// each batch the odd wave leaves its rows' partial statistics (max and sum of
+// exponentials, or the two moment sums) in LDS, and past the batch barrier the
+// even wave joins them and writes the scores.
+#ifndef PISA_LEAF_HALF_WAVES
+#define PISA_LEAF_HALF_WAVES 3
+#endif
+template <typename T, int HD, int SPAN, int NU, int NTM, bool LSE, int BW = 1>
+__global__ void __launch_bounds__(64 * SPAN * BW, BW == 2 ? PISA_LEAF_HALF_WAVES : PISA_LEAF_SPLIT_WAVES)
+leaf_split_kernel(LeafArgs a) {
   typedef QkShape<T, HD> S;
   typedef typename S::Op Op;
   typedef typename S::frag frag;
   constexpr int E = S::E, DS = S::DS;
-  constexpr int THREADS = 64 * SPAN;
+  constexpr int THREADS = 64 * SPAN * BW;
+  static_assert(BW == 1 || (BW == 2 && NTM == 4), "two waves per block hold 64 keys each");
   constexpr int vec = 16 / (int)sizeof(T);
   constexpr int vpr = HD / vec;               // 16-byte chunks of a query row
   constexpr int LPT = NU * 16 * vpr / THREADS;  // staging loads per thread and batch
@@ -496,7 +505,10 @@ __global__ void __launch_bounds__(64 * SPAN, PISA_LEAF_SPLIT_WAVES) leaf_split_k
   int64_t* mq = reinterpret_cast<int64_t*>(smem + (size_t)2 * NU * 16 * LDQ * sizeof(T));
   int32_t* mslot = reinterpret_cast<int32_t*>(mq + a.tile);
   int32_t* mmask = mslot + a.tile;
-  const int tid = threadIdx.x, lane = tid & 63, c = tid >> 6;  // c: this wave's block
+  // partial statistics of the odd waves: [2 batches][SPAN blocks][NU units][16 rows] x 2
+  float2* xch = reinterpret_cast<float2*>(mmask + a.tile);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = wave / BW, hf = wave % BW;  // c: this wave's block, hf: its half of the block
   const int col = lane & 15, grp = lane >> 4;
   const int Gp = a.Gp;                        // a power of two <= 16
   const int gl = 31 - __clz(Gp);
@@ -516,6 +528,8 @@ __global__ void __launch_bounds__(64 * SPAN, PISA_LEAF_SPLIT_WAVES) leaf_split_k
     const int nreq = min(a.tile, a.counts[g] - start);
     const int rows_valid = max(0, min(a.C, a.src_rows - (blk0 + c) * a.C));
     const float inv_rows = 1.f / (float)max(rows_valid, 1);
+    const int keys0 = hf * NTM * 16;                                // this wave's first key
+    const int rows_w = max(0, min(NTM * 16, rows_valid - keys0));  // and its valid keys
     const int32_t* reqs = a.tile_req + (int64_t)tile * a.tile;
 
     __syncthreads();  // the previous tile's readers of the bookkeeping are done
@@ -538,8 +552,8 @@ __global__ void __launch_bounds__(64 * SPAN, PISA_LEAF_SPLIT_WAVES) leaf_split_k
 #pragma unroll
       for (int mt = 0; mt < NTM; ++mt) {
         const int row = mt * 16 + col;
-        if (row < rows_valid) {
-          load_row_frags<E>(kb + (int64_t)row * a.src_row + E * grp, kreg[mt]);
+        if (row < rows_w) {
+          load_row_frags<E>(kb + (int64_t)(keys0 + row) * a.src_row + E * grp, kreg[mt]);
         } else {
 #pragma unroll
           for (int d = 0; d < DS; ++d) kreg[mt][d] = frag{};
@@ -578,7 +592,7 @@ __global__ void __launch_bounds__(64 * SPAN, PISA_LEAF_SPLIT_WAVES) leaf_split_k
     // sum is at least about 1.
     auto head_of = [&](auto full_tag, const f4 (&s)[NTM]) __attribute__((always_inline)) {
       constexpr bool FULL = decltype(full_tag)::value;
-      const int lim = rows_valid - 4 * grp;  // this lane's keys 16 mt + i are valid below lim
+      const int lim = rows_w - 4 * grp;  // this lane's keys 16 mt + i are valid below lim
       auto valid = [&](int mt, int i) { return FULL || mt * 16 + i < lim; };
       if constexpr (LSE) {
         float m = -INFINITY;
@@ -611,6 +625,93 @@ __global__ void __launch_bounds__(64 * SPAN, PISA_LEAF_SPLIT_WAVES) leaf_split_k
         const float mean = s1 * inv_rows;
         const float var = fmaxf(s2 * inv_rows - mean * mean, 0.f);
         return a.scale * mean + half_scale2 * var;
+      }
+    };
+    // Two waves per block: this lane's row statistics over the wave's keys -
+    // (c max S in log2 units, sum 2^(c S - m)) or (sum S, sum S^2) - and the
+    // head score from both halves' statistics (an empty half adds nothing).
+    auto partial_of = [&](auto full_tag, const f4 (&s)[NTM]) __attribute__((always_inline)) {
+      constexpr bool FULL = decltype(full_tag)::value;
+      const int lim = rows_w - 4 * grp;
+      auto valid = [&](int mt, int i) { return FULL || mt * 16 + i < lim; };
+      if constexpr (LSE) {
+        float m = -INFINITY;
+#pragma unroll
+        for (int mt = 0; mt < NTM; ++mt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (valid(mt, i)) m = fmaxf(m, s[mt][i]);
+        m = xor32_max(xor16_max(m)) * scale2;
+        float e = 0.f;
+#pragma unroll
+        for (int mt = 0; mt < NTM; ++mt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (valid(mt, i)) e += __builtin_amdgcn_exp2f(fmaf(s[mt][i], scale2, -m));
+        return make_float2(m, xor32_sum(xor16_sum(e)));
+      } else {
+        float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+        for (int mt = 0; mt < NTM; ++mt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (valid(mt, i)) {
+              s1 += s[mt][i];
+              s2 = fmaf(s[mt][i], s[mt][i], s2);
+            }
+        return make_float2(xor32_sum(xor16_sum(s1)), xor32_sum(xor16_sum(s2)));
+      }
+    };
+    auto join = [&](float2 x, float2 y) __attribute__((always_inline)) {
+      if constexpr (LSE) {
+        const float m = fmaxf(x.x, y.x);  // x: the first half, never empty
+        const float e = x.y * __builtin_amdgcn_exp2f(x.x - m) + y.y * __builtin_amdgcn_exp2f(y.x - m);
+        return (m + __builtin_amdgcn_logf(e)) * 0.69314718055994530942f;
+      } else {
+        const float mean = (x.x + y.x) * inv_rows;
+        const float var = fmaxf((x.y + y.y) * inv_rows - mean * mean, 0.f);
+        return a.scale * mean + half_scale2 * var;
+      }
+    };
+    auto store_head = [&](int u, float head) __attribute__((always_inline)) {
+      const int rho = u * 16 + col;
+      const int rq = rho >> gl;
+      const bool real = rq < nreq && (rho & (Gp - 1)) < a.G;
+      const float v = group_sum(real ? head : 0.f, Gp);
+      if (grp == 0 && (col & (Gp - 1)) == 0 && rq < nreq && ((mmask[rq] >> c) & 1))
+        a.scores[mslot[rq] + c] = v;
+    };
+    float2 own[NU];  // even waves: their half's statistics of the batch's units
+    auto part_batch = [&](auto full_tag, int batch) __attribute__((always_inline)) {
+      const T* qb = qs + (size_t)(batch & 1) * NU * 16 * LDQ;
+#pragma unroll
+      for (int p = 0; p < NU; ++p) {
+        const int u = batch * NU + p;
+        if (u >= nunits) break;
+        frag qf[DS];
+        load_row_frags<E>(qb + (p * 16 + col) * LDQ + E * grp, qf);
+        f4 s[NTM];
+#pragma unroll
+        for (int mt = 0; mt < NTM; ++mt) {
+          s[mt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int d = 0; d < DS; ++d) s[mt] = Op::mma(kreg[mt][d], qf[d], s[mt]);
+        }
+        const float2 pr = partial_of(full_tag, s);
+        if (hf) {
+          if (grp == 0) xch[(((batch & 1) * SPAN + c) * NU + p) * 16 + col] = pr;
+        } else {
+          own[p] = pr;
+        }
+      }
+    };
+    auto join_batch = [&](int batch) __attribute__((always_inline)) {
+      if (hf) return;  // uniform over the wave
+#pragma unroll
+      for (int p = 0; p < NU; ++p) {
+        const int u = batch * NU + p;
+        if (u >= nunits) break;
+        store_head(u, join(own[p], xch[(((batch & 1) * SPAN + c) * NU + p) * 16 + col]));
       }
     };
     auto score_batch = [&](auto full_tag, int batch) __attribute__((always_inline)) {
@@ -672,12 +773,29 @@ __global__ void __launch_bounds__(64 * SPAN, PISA_LEAF_SPLIT_WAVES) leaf_split_k
         __syncthreads();
       }
     };
+    // Two waves per block: the odd waves' statistics of batch i (LDS buffer
+    // i & 1) are joined past the barrier that follows it; the buffer is written
+    // again for batch i + 2, after the next barrier.
+    auto run1h = [&](auto full_tag) __attribute__((always_inline)) {
+      u32x4v sa[LPT];
+      fetch(0, sa);
+      stage(0, sa);
+      __syncthreads();
+      for (int i = 0; i < nb; ++i) {
+        if (i + 1 < nb) fetch(i + 1, sa);
+        if (rows_valid > 0) part_batch(full_tag, i);
+        if (i + 1 < nb) stage((i + 1) & 1, sa);
+        __syncthreads();
+        if (rows_valid > 0) join_batch(i);
+      }
+    };
     auto run = [&](auto full_tag) __attribute__((always_inline)) {
-      if constexpr (PISA_LEAF_SPLIT_DEPTH >= 2) run2(full_tag);
+      if constexpr (BW == 2) run1h(full_tag);
+      else if constexpr (PISA_LEAF_SPLIT_DEPTH >= 2) run2(full_tag);
       else run1(full_tag);
     };
     // FULL: every key of every block of the span is valid (uniform over the workgroup)
-    const bool full = NTM * 16 == a.C && (blk0 + SPAN) * a.C <= a.src_rows;
+    const bool full = NTM * 16 * BW == a.C && (blk0 + SPAN) * a.C <= a.src_rows;
     if (full) run(std::true_type{});
     else run(std::false_type{});
   }
@@ -693,26 +811,30 @@ constexpr size_t kLeafWideLds = 48 << 10;
 
 // Split-span kernel of `SPAN` waves; grid = the resident workgroups of the device
 // (a multiple of 8 for the XCD tile walk).
-template <typename T, int HD, int SPAN, int NTM, bool LSE>
+template <typename T, int HD, int SPAN, int NTM, bool LSE, int BW = 1>
 static void launch_leaf_split(const LeafArgs& a, int cus, hipStream_t stream) {
   constexpr int vpr = HD * (int)sizeof(T) / 16;
+  constexpr int W = SPAN * BW;  // waves per workgroup
   // PISA_LEAF_NU units per batch at four waves, in proportion to the waves
   // otherwise (the same staging loads per thread), and at least one load per thread
-  constexpr int NU0 = PISA_LEAF_NU * SPAN / 4 > 0 ? PISA_LEAF_NU * SPAN / 4 : 1;
-  constexpr int NU = NU0 * 16 * vpr >= 64 * SPAN ? NU0 : 64 * SPAN / (16 * vpr);
-  const void* kernel = (const void*)leaf_split_kernel<T, HD, SPAN, NU, NTM, LSE>;
-  const size_t lds = leaf_split_lds<T, HD>(NU, a.tile);
+  constexpr int NU0 = PISA_LEAF_NU * W / 4 > 0 ? PISA_LEAF_NU * W / 4 : 1;
+  constexpr int NU = NU0 * 16 * vpr >= 64 * W ? NU0 : 64 * W / (16 * vpr);
+  const void* kernel = (const void*)leaf_split_kernel<T, HD, SPAN, NU, NTM, LSE, BW>;
+  // two waves per block: the odd waves' statistics, two batches of NU units of 16 rows per block
+  const size_t lds = leaf_split_lds<T, HD>(NU, a.tile) + (BW == 2 ? (size_t)2 * SPAN * NU * 16 * sizeof(float2) : 0);
   allow_lds(kernel, lds);
   static int per_cu = 0;  // per instance
   if (per_cu == 0) {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, 64 * SPAN, lds) != hipSuccess || n < 1) n = 1;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, 64 * W, lds) != hipSuccess || n < 1) n = 1;
     per_cu = n;
   }
   const dim3 grid(cus * per_cu / 8 * 8 > 0 ? cus * per_cu / 8 * 8 : 8);
-  PISA_TIMED("leaf", stream, hipLaunchKernelGGL((leaf_split_kernel<T, HD, SPAN, NU, NTM, LSE>), grid, dim3(64 * SPAN), lds, stream, a));
+  PISA_TIMED("leaf", stream, hipLaunchKernelGGL((leaf_split_kernel<T, HD, SPAN, NU, NTM, LSE, BW>), grid, dim3(64 * W), lds, stream, a));
 }
 
+// Blocks of up to 32 or 64 keys: one wave per block; of 128 keys (spans of two
+// blocks): two waves per block.
 template <typename T, int HD, int SPAN>
 static void launch_leaf_split_s(const LeafArgs& a, int cus, hipStream_t stream) {
   typedef QkShape<T, HD> S;
@@ -721,9 +843,12 @@ static void launch_leaf_split_s(const LeafArgs& a, int cus, hipStream_t stream) 
   if (nt <= 2) {
     if (lse) launch_leaf_split<T, HD, SPAN, 2, true>(a, cus, stream);
     else launch_leaf_split<T, HD, SPAN, 2, false>(a, cus, stream);
-  } else {
+  } else if (nt <= 4) {
     if (lse) launch_leaf_split<T, HD, SPAN, 4, true>(a, cus, stream);
     else launch_leaf_split<T, HD, SPAN, 4, false>(a, cus, stream);
+  } else if constexpr (SPAN == 2) {
+    if (lse) launch_leaf_split<T, HD, SPAN, 4, true, 2>(a, cus, stream);
+    else launch_leaf_split<T, HD, SPAN, 4, false, 2>(a, cus, stream);
   }
 }
 
@@ -777,10 +902,23 @@ static void launch_leaf_tile(const LeafArgs& a, int cus, hipStream_t stream) {
 #ifndef PISA_LEAF_SPAN_GROUP
 #define PISA_LEAF_SPAN_GROUP 4
 #endif
-int leaf_span(int dtype, int head_dim, int block_size, int branching, int group) {
+// 128-key blocks (16-bit keys, pisa or pisa2, head dims 64 and 128, head groups
+// up to PISA_LEAF_SPAN128_GROUP) go in pairs to the split kernel's two waves per
+// block, so a request's query rows serve both siblings.
+#ifndef PISA_LEAF_SPAN128_GROUP
+#define PISA_LEAF_SPAN128_GROUP 8
+#endif
+static bool span128(int es, int head_dim, int block_size, int branching, int group, int method) {
+  return PISA_LEAF_SPLIT && es == 2 && block_size == 128 && branching >= 2 &&
+         (head_dim == 64 || head_dim == 128) && group <= PISA_LEAF_SPAN128_GROUP &&
+         method != PISA_METHOD_PISA1;
+}
+
+int leaf_span(int dtype, int head_dim, int block_size, int branching, int group, int method) {
   const int es = dtype_size(dtype);
   if (!es || (head_dim != 16 && head_dim != 32 && head_dim != 64 && head_dim != 128)) return 1;
-  if (group > PISA_LEAF_SPAN_GROUP || block_size > 64) return 1;
+  if (block_size > 64) return span128(es, head_dim, block_size, branching, group, method) ? 2 : 1;
+  if (group > PISA_LEAF_SPAN_GROUP) return 1;
   const int E = es == 4 ? 1 : ((head_dim / 4) % 8 == 0 ? 8 : 4);
   const int KQ = E == 8 ? 32 : 16;
   const int cq = (block_size + KQ - 1) / KQ * KQ;
@@ -819,6 +957,9 @@ int launch_leaf(int dtype, const LeafArgs& a, hipStream_t stream) {
   if (a.C > 128) return fail(PISA_ERR_UNSUPPORTED, "leaf scoring supports block_size <= 128");
   if (lds > (size_t)device_lds_limit())
     return fail(PISA_ERR_UNSUPPORTED, "key block of %zu bytes exceeds LDS", lds);
+  if (a.span > 1 && a.C > 64 &&
+      !(a.span == 2 && a.scale > 0.f && span128(es, a.D, a.C, 2, a.G, a.method)))
+    return fail(PISA_ERR_UNSUPPORTED, "sibling spans of blocks over 64 keys need 16-bit keys, pisa or pisa2 and two blocks");
   const int cus = device_cus();
   const int grid = cus * 8;
   if (leaf_tile_path(a, es)) {
