@@ -119,6 +119,11 @@ CONFIGS = [
     # 63 blocks, the last one half full: the last span of four sibling blocks has three
     ("ragged-span", 2, 4000, 8, 2, 128, 64, 4, 8, "pisa", True, 1, "bf16", 0.0, None),
     ("ragged-span2", 1, 3000, 4, 2, 64, 64, 2, 8, "pisa2", True, 2, "bf16", 0.02, None),
+    # pairs of 128-key blocks, two waves per block: pisa2 moments with a 112-key tail block
+    # and an odd block count (the last span has one block); log-sum-exp in fp16 at D = 64,
+    # G = 8, with a 56-key tail block whose second half is empty
+    ("c128-pisa2-ragged", 1, 6000, 8, 2, 128, 128, 4, 8, "pisa2", True, 1, "bf16", 0.0, None),
+    ("c128-lse-fp16-d64", 2, 3000, 16, 2, 64, 128, 2, 8, "pisa", True, 2, "fp16", 0.0, None),
 ]
 
 
