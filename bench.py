@@ -74,13 +74,14 @@ def leaf_span(w, elem):
     """Sibling blocks per grouped leaf request (mirrors leaf_span in csrc/pisa_leaf.hip):
     head groups of up to 4 and blocks of up to 64 keys take the largest power of two
     <= min(branching, 4) whose blocks fit 256 LDS rows and 80 KB; 16-bit 128-key blocks
-    (head dims 64 and 128, groups up to 8) go in pairs."""
+    (head dims 64 and 128, groups up to 8, from 16384 row items) go in pairs."""
     G = w.query_heads // w.key_heads
     D = w.head_dim
     if w.method == "pisa1" or D not in (16, 32, 64, 128):
         return 1
     if w.block_size > 64:   # 128-key blocks: pairs, two waves per block (16-bit, G <= 8)
-        ok = elem == 2 and w.block_size == 128 and w.branching >= 2 and D in (64, 128) and G <= 8
+        ok = (elem == 2 and w.block_size == 128 and w.branching >= 2 and D in (64, 128) and G <= 8
+              and w.batch * w.tokens * w.key_heads >= 16384)
         return 2 if ok else 1
     if G > 4:
         return 1

@@ -110,7 +110,8 @@ int plan_select(const pisa_qk_desc* qk, const pisa_select_params* p, SelectPlan&
   const int es = dtype_size(qk->dtype);
   const bool aligned = ((qk->q_stride_batch | qk->q_stride_token | qk->k_stride_batch |
                          qk->k_stride_token) * es) % 16 == 0;
-  pl.span = pl.grouped && aligned ? leaf_span(qk->dtype, D, p->block_size, p->branching, G, p->method) : 1;
+  pl.span = pl.grouped && aligned ? leaf_span(qk->dtype, D, p->block_size, p->branching, G, p->method,
+                                                      pl.items) : 1;
   pl.spans = (pl.M0 + pl.span - 1) / pl.span;
   pl.groups = (int64_t)qk->batch * qk->key_heads * pl.spans;
   const int64_t flat = (int64_t)qk->batch * qk->query_tokens;

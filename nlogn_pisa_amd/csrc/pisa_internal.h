@@ -248,7 +248,8 @@ int launch_leaf(int dtype, const LeafArgs& a, hipStream_t stream);
 #endif
 constexpr int kLeafTile = PISA_LEAF_TILE;
 // Sibling blocks per leaf request for the grouped schedule (1: one block each).
-int leaf_span(int dtype, int head_dim, int block_size, int branching, int group, int method);
+int leaf_span(int dtype, int head_dim, int block_size, int branching, int group, int method,
+              int64_t items);
 int attn_check(const AttnArgs& a, int dtype, bool backward);
 // Forward partials (grouped tiles or one workgroup per slot), then the combine.
 int launch_attn_partials(int dtype, const AttnArgs& a, bool grouped, int64_t slots, hipStream_t stream);

@@ -122,8 +122,9 @@ CONFIGS = [
     # pairs of 128-key blocks, two waves per block: pisa2 moments with a 112-key tail block
     # and an odd block count (the last span has one block); log-sum-exp in fp16 at D = 64,
     # G = 8, with a 56-key tail block whose second half is empty
-    ("c128-pisa2-ragged", 1, 6000, 8, 2, 128, 128, 4, 8, "pisa2", True, 1, "bf16", 0.0, None),
-    ("c128-lse-fp16-d64", 2, 3000, 16, 2, 64, 128, 2, 8, "pisa", True, 2, "fp16", 0.0, None),
+    # (at least 16384 (token, kv head) items, where pairs are used)
+    ("c128-pisa2-ragged", 1, 9072, 8, 2, 128, 128, 4, 8, "pisa2", True, 1, "bf16", 0.0, None),
+    ("c128-lse-fp16-d64", 2, 5048, 16, 2, 64, 128, 2, 8, "pisa", True, 2, "fp16", 0.0, None),
 ]
 
 
