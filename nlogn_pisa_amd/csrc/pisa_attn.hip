@@ -327,6 +327,14 @@ __global__ void __launch_bounds__(64) attn_fwd_direct_kernel(AttnArgs a, int64_t
 // computed once per tile into LDS, and each wave loads the next unit's query
 // rows while it computes the current one.
 
+// 1: a unit's 16 partial rows pass through the wave's LDS rows 8 at a time (half
+// the staging LDS, so three forward workgroups fit a CU at 64-key blocks instead
+// of two: config 2 attn_fwd 7.97 -> 6.98 ms).
+#ifndef PISA_ATTN_HALF_STAGE
+#define PISA_ATTN_HALF_STAGE 1
+#endif
+constexpr int kStageRows = PISA_ATTN_HALF_STAGE ? 8 : 16;
+
 // LDS of one tile: K block [Cq][HD + PAD], V^T [HD][Cq + PAD], per request
 // the query row offset (int64), position (int64) and slot (int32), then per
 // wave the 16 partial rows of its current unit [16][HD + 16 B] (PartialT).
@@ -358,7 +366,7 @@ __host__ __device__ inline TileLds tile_lds(int C, int tile, int waves, bool wit
   off += (size_t)tile * 4;
   off = (off + 15) / 16 * 16;
   L.o_off = off;
-  off += (size_t)waves * 16 * L.ldo * sizeof(PT);
+  off += (size_t)waves * kStageRows * L.ldo * sizeof(PT);
   L.bytes = (off + 15) / 16 * 16;
   return L;
 }
@@ -624,7 +632,28 @@ __device__ void fwd_tile_units(const AttnArgs& a, const TileLds& L, const T* ks,
 #pragma unroll
         for (int i = 0; i < 4; ++i) vals[4 * dt + i] = (PT)(o[dt][i] * inv);
       if (so) {
-        store_vals(so + col * L.ldo + QL * grp, vals);
+        if constexpr (kStageRows == 8) {
+          // rows 8 hp .. 8 hp + 7 through the wave's 8 LDS rows, then out as whole rows
+          constexpr int CH = HD * (int)sizeof(PT) / 16;  // 16-byte chunks per row
+          constexpr int CE = 16 / (int)sizeof(PT);
+#pragma unroll
+          for (int hp = 0; hp < 2; ++hp) {
+            if ((col >> 3) == hp) store_vals(so + (col & 7) * L.ldo + QL * grp, vals);
+            wave_lds_sync();
+#pragma unroll
+            for (int idx = lane; idx < 8 * CH; idx += 64) {
+              const int r = idx / CH, cc = idx % CH;
+              const int rho2 = (u << 4) + 8 * hp + r, rq2 = rho2 >> gl, gh2 = rho2 & (Gp - 1);
+              if (rq2 < nreq && gh2 < a.G) {
+                const uint4 v = *reinterpret_cast<const uint4*>(so + r * L.ldo + cc * CE);
+                stream_store16(static_cast<PT*>(a.part_o) + ((int64_t)mslot[rq2] * a.G + gh2) * HD + cc * CE, v);
+              }
+            }
+            wave_lds_sync();  // the rows are out; the next half may overwrite them
+          }
+        } else {
+          store_vals(so + col * L.ldo + QL * grp, vals);
+        }
       } else if (valid) {
         PT* dst = static_cast<PT*>(a.part_o) + ((int64_t)mslot[rq] * a.G + gh) * HD + QL * grp;
         if constexpr (QL * sizeof(PT) % 16 == 0) {  // whole 16-byte chunks: streaming stores
@@ -639,7 +668,7 @@ __device__ void fwd_tile_units(const AttnArgs& a, const TileLds& L, const T* ks,
       }
       if (valid && grp == 0) stream_store(a.part_lse + (int64_t)mslot[rq] * a.G + gh, m + __logf(l));
     }
-    if (so) {
+    if (so && kStageRows == 16) {
       wave_lds_sync();
       constexpr int CH = HD * (int)sizeof(PT) / 16;  // 16-byte chunks per row
       constexpr int CE = 16 / (int)sizeof(PT);
@@ -668,7 +697,7 @@ __device__ void fwd_tile_units(const AttnArgs& a, const TileLds& L, const T* ks,
 template <typename T, int HD, int NTM>
 __global__ void __launch_bounds__(256, PISA_ATTN_WAVES) attn_fwd_tile_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  // partial rows staged per wave only where the staging keeps two workgroups per CU
+  // partial rows staged per wave only where the staging keeps several workgroups per CU
   constexpr bool STAGE = NTM <= 4;
   const TileLds L = tile_lds<T, HD>(a.C, a.tile, STAGE ? (int)(blockDim.x >> 6) : 0);
   T* ks = reinterpret_cast<T*>(smem + L.k_off);
@@ -678,7 +707,7 @@ __global__ void __launch_bounds__(256, PISA_ATTN_WAVES) attn_fwd_tile_kernel(Att
   int32_t* mslot = reinterpret_cast<int32_t*>(smem + L.slot_off);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   typedef typename PartialT<T>::type PT;
-  PT* so = STAGE ? reinterpret_cast<PT*>(smem + L.o_off) + wave * 16 * L.ldo : nullptr;
+  PT* so = STAGE ? reinterpret_cast<PT*>(smem + L.o_off) + wave * kStageRows * L.ldo : nullptr;
   const int ntiles = *a.num_tiles;
 #if PISA_ATTN_XCD
   const XcdTiles walk = xcd_tiles(ntiles);  // grid_size() is a multiple of 8
