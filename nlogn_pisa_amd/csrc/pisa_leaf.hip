@@ -449,17 +449,19 @@ leaf_tile_kernel(LeafArgs a) {
 
 // ------------------------------------------------------------------ split spans
 //
-// Spans of SPAN sibling blocks of at most 64 keys, 16-bit inputs.  Wave c of
-// a SPAN-wave workgroup owns block c of the tile's span: it holds the block's
-// MFMA A fragments (its key rows) in registers for the whole tile, and every
-// wave scores every unit of the tile against its own block.  The tile's query
-// rows pass through LDS once, NU units (16 rows each) at a time and double
-// buffered, so LDS serves 16 query rows per unit and block instead of the span's
-// whole key set per unit.  Loads of the next NU units are in flight while the
-// current ones are scored; one workgroup barrier per NU units.
+// Spans of SPAN sibling blocks of at most 64 keys (or two blocks of 128 keys),
+// 16-bit inputs.  Wave c of a SPAN-wave workgroup owns block c of the tile's
+// span (with 128-key blocks, waves 2c and 2c + 1 own its two halves): it holds
+// the block's MFMA A fragments (its key rows) in registers for the whole tile,
+// and every wave scores every unit of the tile against its own keys.  The
+// tile's query rows pass through LDS once, NU units (16 rows each) at a time and
+// double buffered, so LDS serves 16 query rows per unit and block instead of the
+// span's whole key set per unit.  Loads of the next NU units are in flight while
+// the current ones are scored; one workgroup barrier per NU units.
 
 // LDS of a split-span workgroup: two buffers of NU units of padded query rows,
-// then per request its query-row offset, first slot and scoreable mask.
+// then per request its query-row offset, first slot and scoreable mask (and,
+// with two waves per block, the odd waves' row statistics, added by the launch).
 template <typename T, int HD>
 __host__ __device__ inline size_t leaf_split_lds(int nu, int tile) {
   return (size_t)2 * nu * 16 * (HD + 16 / sizeof(T)) * sizeof(T) + (size_t)tile * 16;
@@ -892,9 +894,9 @@ static void launch_leaf_tile(const LeafArgs& a, int cus, hipStream_t stream) {
 // Sibling blocks per request: the largest power of two <= branching (and
 // kMaxSpan) whose blocks take at most 256 key rows and, with the request
 // bookkeeping, 80 KB of LDS.  Spans serve head groups of up to four heads and
-// blocks of up to 64 keys: there the query rows dominate a tile's traffic and
-// the kernel keeps four waves per SIMD (measured: larger groups or 128-key
-// blocks ran slower).
+// blocks of up to 64 keys, where the query rows dominate a tile's traffic
+// (measured: spans for groups of 16 ran slower at D = 128 and mixed at D = 64),
+// and pairs of 128-key blocks in the split kernel (below).
 #ifndef PISA_LEAF_MAX_SPAN
 #define PISA_LEAF_MAX_SPAN kMaxSpan
 #endif
