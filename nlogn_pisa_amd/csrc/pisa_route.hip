@@ -558,7 +558,10 @@ __device__ __forceinline__ void tile_scores(const f4& sv, const TileMeta<RR>& m,
   }
 }
 
-template <typename T, int HD, int RR, int MODE, bool FUSED>
+// DENSE: every level above the leaf is scored densely (the launch checks it) -
+// the support-row gathers, their prefetch buffers and the query rows are not
+// compiled in, so the wave needs fewer registers and more of them fit a SIMD.
+template <typename T, int HD, int RR, int MODE, bool FUSED, bool DENSE = false>
 __global__ void __launch_bounds__(64) route_grouped_kernel(RouteArgs a) {
   typedef QkShape<T, HD> S;
   typedef typename S::Op Op;
@@ -593,7 +596,7 @@ __global__ void __launch_bounds__(64) route_grouped_kernel(RouteArgs a) {
   bool gathers = FUSED;
   for (int l = 1; l <= a.top; ++l) gathers = gathers || !a.dense[l];
   frag qb[DS];
-  if (gathers && col < a.G)
+  if (!DENSE && gathers && col < a.G)
     load_row_frags<E>(static_cast<const T*>(a.q) + b * a.q_batch + t * a.q_token +
                           ((int64_t)h * a.G + col) * HD + E * grp,
                       qb);
@@ -654,7 +657,7 @@ __global__ void __launch_bounds__(64) route_grouped_kernel(RouteArgs a) {
         const int e = list_s[i];
         sc_s[e] = ds[ids_s[e]];
       }
-    } else {
+    } else if constexpr (!DENSE) {
     // score the scoreable candidates, 16 support rows at a time
     const int src_level = own ? level : level - 1;
     const T* base = static_cast<const T*>(a.summary) + b * a.sum_batch +
@@ -1164,6 +1167,14 @@ static int launch_route_t(const RouteArgs& a, int64_t items, int threads, hipStr
 template <typename T, int HD, int RR, int MODE, bool FUSED>
 static void launch_route_rm(const RouteArgs& a, int64_t items, hipStream_t stream) {
   const size_t lds = (size_t)3 * sizeof(int) * grouped_route_width(a.first_width, a.branching, a.topk);
+  if constexpr (!FUSED) {
+    bool dense = a.top >= 1;
+    for (int l = 1; l <= a.top; ++l) dense = dense && a.dense[l] != nullptr;
+    if (dense) {
+      PISA_TIMED("route", stream, hipLaunchKernelGGL((route_grouped_kernel<T, HD, RR, MODE, false, true>), dim3(items), dim3(64), lds, stream, a));
+      return;
+    }
+  }
   PISA_TIMED("route", stream, hipLaunchKernelGGL((route_grouped_kernel<T, HD, RR, MODE, FUSED>), dim3(items), dim3(64), lds, stream, a));
 }
 
