@@ -35,9 +35,15 @@ __host__ __device__ inline int grouped_route_width(int first_width, int branchin
 // heads) run one wave per item.
 constexpr int64_t kFusedWaveItems = 8192;
 
-// Support tiles of the MFMA routing in flight ahead of the one being scored.
+// Support tiles of the MFMA routing in flight ahead of the one being scored:
+// grouped schedule (one buffer fewer keeps more waves per SIMD; the reference
+// benchmark shape's Q4 selection 2.49 -> 2.28 ms at D = 128, 64K tokens) and
+// fused schedule (mixed there: kept at two).
 #ifndef PISA_ROUTE_DEPTH
-#define PISA_ROUTE_DEPTH 2
+#define PISA_ROUTE_DEPTH 1
+#endif
+#ifndef PISA_ROUTE_FUSED_DEPTH
+#define PISA_ROUTE_FUSED_DEPTH 2
 #endif
 
 
@@ -680,7 +686,7 @@ __global__ void __launch_bounds__(64) route_grouped_kernel(RouteArgs a) {
     };
     // tile mt: scored from `xf`, loads tile mt + DEPTH into `xn` (the buffer the
     // previous tile used); the buffers rotate by unrolling, never by copies
-    constexpr int DEPTH = PISA_ROUTE_DEPTH;
+    constexpr int DEPTH = FUSED ? PISA_ROUTE_FUSED_DEPTH : PISA_ROUTE_DEPTH;
     auto tile = [&](int mt, frag (&xf)[DS], frag (&xn)[DS], const TileMeta<R>& mf, TileMeta<R>& mn) {
       fetch(mt + DEPTH, xn, mn);
       f4 sv = f4{0.f, 0.f, 0.f, 0.f};
