@@ -9,7 +9,9 @@ per-sequence seeds for decode) so every box sees identical data.
 
 from __future__ import annotations
 
+import concurrent.futures
 import math
+import os
 from dataclasses import dataclass, field
 
 import torch
@@ -59,7 +61,8 @@ def config(index: int, tokens: int | None = None) -> Workload:
     raise ValueError(f"unknown configuration {index}")
 
 
-def _sequence(gen, w: Workload, batch: int, first_block_excluded: bool, last_excluded: bool):
+def _sequence(gen, w: Workload, batch: int, first_block_excluded: bool, last_excluded: bool,
+              needles: list | None = None):
     q = torch.randn(batch, w.tokens, w.query_heads, w.head_dim, generator=gen)
     noise = torch.randn(batch, w.keys, w.key_heads, w.head_dim, generator=gen)
     blocks = math.ceil(w.keys / 64)
@@ -72,22 +75,36 @@ def _sequence(gen, w: Workload, batch: int, first_block_excluded: bool, last_exc
             for h in range(w.key_heads):
                 ids = torch.randperm(high - low, generator=gen)[:count] + low
                 off[b, ids, h] = 2.0 * torch.randn(count, w.head_dim, generator=gen)
+                if needles is not None:
+                    needles.append((b, h, sorted(ids.tolist())))
     k = noise + off.repeat_interleave(64, 1)[:, :w.keys]
     v = torch.randn(batch, w.keys, w.key_heads, w.head_dim, generator=gen)
     return q, k, v
 
 
-def make_inputs(w: Workload, device="cuda"):
-    """(q, k, v[, dO]) of workload ``w`` in its dtype on ``device``."""
+def make_inputs(w: Workload, device="cuda", needles: list | None = None):
+    """(q, k, v[, dO]) of workload ``w`` in its dtype on ``device``.
+
+    ``needles``, when a list, receives one ``(batch, kv_head, [block ids])``
+    entry per sequence and kv head naming the planted needle blocks.
+    """
     if w.per_sequence_seed:
-        parts = []
-        for b in range(w.batch):
+        # every sequence has its own generator, so they are drawn concurrently
+        def draw(b):
             gen = torch.Generator("cpu").manual_seed(w.seed + b)
-            q, k, v = _sequence(gen, w, 1, True, True)
-            parts.append([x.to(w.dtype).to(device) for x in (q, k, v)])
-        return tuple(torch.cat([p[i] for p in parts], 0) for i in range(3))
+            found = []
+            q, k, v = _sequence(gen, w, 1, True, True, found)
+            return [x.to(w.dtype) for x in (q, k, v)], [(b, h, ids) for _, h, ids in found]
+
+        workers = max(1, min(16, os.cpu_count() or 1, w.batch))
+        with concurrent.futures.ThreadPoolExecutor(workers) as pool:
+            drawn = list(pool.map(draw, range(w.batch)))
+        if needles is not None:
+            for _, found in drawn:
+                needles.extend(found)
+        return tuple(torch.cat([part[i].to(device) for part, _ in drawn], 0) for i in range(3))
     gen = torch.Generator("cpu").manual_seed(w.seed)
-    q, k, v = _sequence(gen, w, w.batch, True, False)
+    q, k, v = _sequence(gen, w, w.batch, True, False, needles)
     out = [q, k, v]
     if w.grad:
         out.append(torch.randn(w.batch, w.tokens, w.query_heads, w.head_dim, generator=gen))

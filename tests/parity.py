@@ -134,3 +134,138 @@ def adjudicate_flat(got, want, scores, ids, tol=1e-4):
         else:
             failures.append(int(r))
     return len(bad), exempt, failures
+
+
+def stratified_tokens(length, count, seed=0, low=0):
+    """About ``count`` sorted query indices in [low, length): one uniform draw per
+    equal stratum, plus the first and last index (identity region and the end)."""
+    rng = np.random.default_rng(seed)
+    edges = np.linspace(low, length, count + 1)
+    picks = [int(rng.integers(int(a), max(int(a) + 1, int(b)))) for a, b in zip(edges[:-1], edges[1:])]
+    return np.unique(np.clip(np.array(picks + [low, length - 1], dtype=np.int64), low, length - 1))
+
+
+def selection_parity(qn, kn, ids, trace, tokens, method, block, topk, force_first, force_recent,
+                     branching, levels, positions, geometry=None):
+    """Compare GPU ids [B, Tq, H, K] (numpy, all tokens) on ``tokens`` with the oracle.
+
+    ``trace`` is the GPU's per-level ids [B, Tq, H, L, K].  Returns a dict with
+    the rows compared, mismatched rows, tie-exempt rows and the failing rows
+    (batch-major row index, kv head, diverging level).
+    """
+    expected, otrace = O.pyramid_select(qn, kn, method, block, topk, positions, force_first,
+                                        force_recent, levels, branching=branching, tokens=tokens,
+                                        trace=True, geometry=geometry)
+    got = ids[:, tokens]
+    heads = got.shape[2]
+    rows = got.shape[0] * got.shape[1] * heads
+    if np.array_equal(got, expected):
+        return {"rows": rows, "mismatched": 0, "exempt": 0, "failures": [], "expected": expected}
+    gtrace = trace[:, tokens]
+    _, mism, exempt, failures = adjudicate(
+        got.reshape(-1, heads, got.shape[-1]), gtrace.reshape(-1, heads, *gtrace.shape[-2:]),
+        expected.reshape(-1, heads, got.shape[-1]), otrace)
+    return {"rows": rows, "mismatched": mism, "exempt": exempt, "failures": failures,
+            "expected": expected}
+
+
+def needle_recall(qn, kn, selected, tokens, needles, block, topk, force_first, force_recent,
+                  positions):
+    """Needle blocks ranked inside the top ``topk - |forced|`` of the exhaustive leaf
+    log-sum-exp (summed over the query heads, forced blocks excluded) that the
+    selection ``selected`` [B, len(tokens), Hkv, K] contains: (hits, total)."""
+    batch, _, query_heads, dim = qn.shape
+    heads = kn.shape[2]
+    groups = query_heads // heads
+    scale = dim ** -0.5
+    hits = total = 0
+    for b, h, ids in needles:
+        planted = set(int(x) for x in ids)
+        query = qn[b, tokens, h * groups:(h + 1) * groups].reshape(-1, dim).astype(np.float64)
+        keys = kn[b, :, h].astype(np.float64)
+        n = keys.shape[0]
+        blocks = -(-n // block)
+        logits = np.full((len(tokens) * groups, blocks * block), -np.inf)
+        logits[:, :n] = query @ keys.T * scale
+        logits = logits.reshape(len(tokens), groups, blocks, block)
+        peak = logits.max(-1, keepdims=True)
+        lse = (peak[..., 0] + np.log(np.exp(logits - peak).sum(-1))).sum(1)   # [tokens, blocks]
+        for i, t in enumerate(tokens):
+            pos = int(positions[b, t])
+            current = pos // block
+            excluded = set(range(max(0, current - force_recent + 1), current + 1))
+            if force_first:
+                excluded.add(0)
+            cand = np.array([j for j in range(current + 1) if j not in excluded])
+            if cand.size == 0:
+                continue
+            best = cand[np.argsort(-lse[i, cand], kind="stable")[:topk - len(excluded)]]
+            must = planted.intersection(best.tolist())
+            chosen = set(selected[b, i, h].tolist())
+            hits += len(must & chosen)
+            total += len(must)
+    return hits, total
+
+
+def torch_sparse_attention(q, k, v, indices, block, positions, dout=None, scale=None, chunk=256):
+    """Float32 restatement of ``sparse_attn_torch.py:6-35`` on the tensors' device.
+
+    Returns (O, LSE) and, when ``dout`` is given, (dQ, dK, dV) from the closed-form
+    gradients (dV = P^T dO, dS = P (dO V^T - rowsum(dO O)), dQ = s dS K,
+    dK = s dS^T Q), scattered back through the gathers.  Chunks of ``chunk`` query
+    tokens bound the gathered keys.
+    """
+    batch, length, query_heads, dim = q.shape
+    n, heads = k.shape[1], k.shape[2]
+    groups = query_heads // heads
+    scale = dim ** -0.5 if scale is None else scale
+    dev = q.device
+    k32, v32 = k.float(), v.float()
+    out = torch.zeros(batch, length, query_heads, v.shape[-1], device=dev)
+    lse = torch.full((batch, length, query_heads), -float("inf"), device=dev)
+    grads = None
+    if dout is not None:
+        grads = (torch.zeros(batch, length, query_heads, dim, device=dev),
+                 torch.zeros(batch, n, heads, dim, device=dev),
+                 torch.zeros(batch, n, heads, v.shape[-1], device=dev))
+    offs = torch.arange(block, device=dev)
+    b_ids = torch.arange(batch, device=dev)[:, None, None, None]
+    h_ids = torch.arange(heads, device=dev)[None, None, :, None]
+    for s in range(0, length, chunk):
+        e = min(length, s + chunk)
+        ids = indices[:, s:e].long()
+        tok = (ids[..., None] * block + offs).flatten(-2)                     # [B,t,H,S]
+        valid = (ids[..., None] >= 0).expand(*ids.shape, block).flatten(-2)
+        valid &= (tok >= 0) & (tok < n) & (tok <= positions[:, s:e, None, None])
+        tok = tok.clamp(0, n - 1)
+        bb = b_ids.expand_as(tok)
+        hh = h_ids.expand_as(tok)
+        keys = k32[bb, tok, hh]                                                # [B,t,H,S,D]
+        vals = v32[bb, tok, hh]
+        query = q[:, s:e].float().reshape(batch, e - s, heads, groups, dim)
+        logits = torch.matmul(query, keys.transpose(-1, -2).contiguous()) * scale
+        mask = valid[:, :, :, None, :]
+        logits = logits.masked_fill(~mask, -float("inf"))
+        peak = logits.amax(-1, keepdim=True)
+        safe = torch.where(torch.isfinite(peak), peak, torch.zeros_like(peak))
+        w = torch.exp(logits - safe).masked_fill(~mask, 0.0)
+        den = w.sum(-1, keepdim=True)
+        prob = w / torch.where(den > 0, den, torch.ones_like(den))
+        o = torch.matmul(prob, vals)                                           # [B,t,H,G,Dv]
+        out[:, s:e] = o.reshape(batch, e - s, query_heads, -1)
+        row_lse = torch.where(den[..., 0] > 0, safe[..., 0] + torch.log(den[..., 0]),
+                              torch.full_like(den[..., 0], -float("inf")))
+        lse[:, s:e] = row_lse.reshape(batch, e - s, query_heads)
+        if dout is None:
+            continue
+        do = dout[:, s:e].float().reshape(batch, e - s, heads, groups, -1)
+        dprob = torch.matmul(do, vals.transpose(-1, -2).contiguous())
+        delta = (do * o).sum(-1, keepdim=True)
+        dlog = prob * (dprob - delta)
+        grads[0][:, s:e] = (torch.matmul(dlog, keys) * scale).reshape(batch, e - s, query_heads, dim)
+        dkeys = torch.matmul(dlog.transpose(-1, -2).contiguous(), query) * scale   # [B,t,H,S,D]
+        dvals = torch.matmul(prob.transpose(-1, -2).contiguous(), do)
+        sel = valid
+        grads[1].index_put_((bb[sel], tok[sel], hh[sel]), dkeys[sel], accumulate=True)
+        grads[2].index_put_((bb[sel], tok[sel], hh[sel]), dvals[sel], accumulate=True)
+    return (out, lse) if dout is None else (out, lse, *grads)

@@ -63,8 +63,9 @@ CASES = [
     ("fp32-d16", 1, 128, 256, 4, 1, 16, 16, 6, "fp32", True, None),
     ("fp16-d16-c48", 2, 200, 200, 4, 2, 16, 48, 3, "fp16", True, None),
     ("bf16-c128", 1, 512, 640, 8, 2, 128, 128, 3, "bf16", True, None),
-    # 2048-token windows over the flattened (batch, token) axis: two, the first across batches
-    ("bf16-windows", 2, 1500, 1500, 16, 1, 128, 64, 6, "bf16", True, None),
+    # 2 x 10000 tokens x 32 heads x 128 x 2 bytes = 160 MB of q rows: three forward windows of
+    # 8192 flattened (batch, token) rows under the 128 MiB budget, the second across batches
+    ("bf16-windows", 2, 10000, 10000, 32, 2, 128, 64, 6, "bf16", True, None),
     # 3 x 8 x 1024 = 24576 (batch, kv head, block) groups: bucketing with global atomics
     ("bf16-wide", 3, 40, 65536, 8, 8, 16, 64, 4, "bf16", True, None),
     # register-tile backward: fp16 at head dim 128, 128-key blocks at head dim 64, G = 3
