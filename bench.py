@@ -10,9 +10,12 @@ Prints ONE JSON line.  ``value`` is the selection latency (ms, lower is better),
 the first number of the metric; the sparse-attention TFLOP/s and the roofline
 fractions sit beside it.  The ``roofline`` object describes the kernel with the
 largest share of the step, timed by HIP events recorded on its own stream
-(``nlogn_pisa_amd._lib.profile_begin/end``).  ``cpu_baseline`` times the NumPy
-oracle (the reference's Torch equations restated) on a bounded token sample of
-the same workload on this host's cores, extrapolated to the full sequence.
+(``nlogn_pisa_amd._lib.profile_begin/end``): the attention forward against the
+bf16 MFMA peak (4 D G flops per visible (row, key) pair), the selection kernels
+against HBM.  ``cpu_baseline`` times the NumPy oracle (the reference's Torch
+equations restated) on a bounded sample of the same workload - the selection of
+1024 query tokens and the attention of eight 32-token chunks - on this host's
+cores, extrapolated to the full sequence.
 """
 
 from __future__ import annotations
@@ -39,7 +42,10 @@ def parse():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", type=int, default=2)
     ap.add_argument("--tokens", type=int, default=None, help="config 4 length")
-    ap.add_argument("--cpu-sample", type=int, default=384, help="oracle tokens timed on the CPU")
+    ap.add_argument("--cpu-sample", type=int, default=1024,
+                    help="query tokens of the oracle's selection timed on the CPU")
+    ap.add_argument("--cpu-chunks", type=int, default=8,
+                    help="32-token chunks of the oracle's attention timed on the CPU")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--backward", action="store_true",
                     help="also time sparse attention forward + backward (a training step's attention)")
@@ -219,13 +225,32 @@ def attention_counts(w, ids, positions, elem):
 
 # ---------------------------------------------------------------- CPU baseline
 
-def cpu_baseline(w, q, k, sample):
-    """Time the NumPy oracle on ``sample`` tokens (full pyramid) and extrapolate."""
+def cpu_model():
+    """The host CPU's model name (``lscpu``'s "Model name", read from /proc/cpuinfo)."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(w, q, k, v, sample, chunks):
+    """Time the NumPy oracle (the reference's Torch equations restated) on a bounded
+    sample of the workload and extrapolate to the whole step.
+
+    Selection: the full pyramid, then ``sample`` evenly spaced query tokens
+    (``pyramid_select``, ``top_k_pyramid_torch.py:137-177``).  Attention: ``chunks``
+    evenly spaced 32-token chunks of the same rows over the oracle's selected ids
+    (``sparse_attention``, ``sparse_attn_torch.py:6-35``, float32 as the reference's
+    CPU path computes).  Both per-token costs are scaled to every token.
+    """
     import numpy as np
+    import torch
     import oracle as O
-    dtype = {"torch.bfloat16": "bf16", "torch.float16": "fp16", "torch.float32": "fp32"}[str(w.dtype)]
-    qn = q.float().cpu().numpy()
-    kn = k.float().cpu().numpy()
+    dtype = {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[w.dtype]
+    qn, kn, vn = (x.float().cpu().numpy() for x in (q, k, v))
     positions = O.query_positions(w.batch, w.tokens, w.keys)
     tokens = np.unique(np.linspace(0, w.tokens - 1, sample).astype(np.int64))
     t0 = time.perf_counter()
@@ -234,19 +259,35 @@ def cpu_baseline(w, q, k, sample):
     O.pyramid_select(qn, kn, w.method, w.block_size, w.topk, positions, w.force_first,
                      w.force_recent, levels, branching=w.branching, tokens=tokens)
     t2 = time.perf_counter()
+    starts = np.unique(np.linspace(0, max(0, w.tokens - 32), chunks).astype(np.int64))
+    rows = np.unique(np.concatenate([np.arange(s, min(s + 32, w.tokens)) for s in starts]))
+    ids = O.pyramid_select(qn, kn, w.method, w.block_size, w.topk, positions, w.force_first,
+                           w.force_recent, levels, branching=w.branching, tokens=rows)
+    t3 = time.perf_counter()
+    O.sparse_attention(qn[:, rows], kn, vn, ids, w.block_size, positions=positions[:, rows],
+                       compute=np.float32)
+    t4 = time.perf_counter()
     per_token = (t2 - t1) / len(tokens)
-    total_ms = 1e3 * ((t1 - t0) + per_token * w.tokens)
-    threads = os.cpu_count()
+    attn_per_token = (t4 - t3) / len(rows)
+    sel_ms = 1e3 * ((t1 - t0) + per_token * w.tokens)
+    blas = None
     try:
         from threadpoolctl import threadpool_info
-        threads = max(int(x.get("num_threads", 1)) for x in threadpool_info()) or threads
+        blas = max(int(x.get("num_threads", 1)) for x in threadpool_info()) or None
     except Exception:
         pass
-    return {"value": round(total_ms, 1), "unit": "ms", "cores": int(threads), "kind": "port",
-            "sample": (f"oracle (NumPy restatement of the Torch path) selection on {len(tokens)} "
-                       f"evenly spaced of {w.tokens} query tokens with the full pyramid "
-                       f"({1e3 * (t1 - t0):.0f} ms pyramid + {1e3 * per_token:.2f} ms/token), "
-                       f"extrapolated to all tokens")}
+    return {"value": round(sel_ms, 1), "unit": "ms", "cores": int(blas or 1), "kind": "port",
+            "sample": (f"oracle (NumPy restatement of the reference's Torch path): pyramid over all "
+                       f"keys ({1e3 * (t1 - t0):.0f} ms) + selection of {len(tokens)} evenly spaced "
+                       f"of {w.tokens} query tokens ({1e3 * per_token:.2f} ms/token), and attention "
+                       f"forward of {len(starts)} evenly spaced 32-token chunks ({len(rows)} rows, "
+                       f"{1e3 * attn_per_token:.2f} ms/token), each extrapolated to all tokens; "
+                       f"matrix products on the BLAS pool, element-wise work on one thread"),
+            "selection_ms": round(sel_ms, 1),
+            "attention_fwd_ms": round(1e3 * attn_per_token * w.tokens * w.batch, 1),
+            "step_ms": round(sel_ms + 1e3 * attn_per_token * w.tokens * w.batch, 1),
+            "cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads(),
+            "blas_threads": blas, "cpu_model": cpu_model()}
 
 
 # ---------------------------------------------------------------- main
@@ -404,7 +445,9 @@ def main():
                  + r_leaf * 4,
                  "flops": 2 * r_leaf * w.block_size * D * G},
         "final": {"bound": "hbm", "bytes": items * (width * 9 + w.topk * 8)},
-        "attn_fwd": {"bound": "hbm",
+        # MFMA-bound: 4 D G flops per visible (row, key) pair; "bytes" is the design's own
+        # traffic (K/V per tile, q rows and the fp16 partial row of every request)
+        "attn_fwd": {"bound": "mfma",
                      "bytes": attn_tiles * 2 * w.block_size * D * e
                      + requests * G * (D * e + D * pe + 4),
                      "flops": 4 * D * G * pairs},
@@ -412,20 +455,39 @@ def main():
                          "bytes": requests * G * (D * pe + 4) + items * G * (D * e + 4)},
         "pool": {"bound": "hbm", "bytes": w.batch * w.keys * w.key_heads * D * e},
     }
-    # the dominant kernel: its algorithmic bytes per step over its time per step
-    # (= bytes per launch over the average launch: the windowed kernels launch
-    # once per window of query tokens)
+    # compulsory HBM bytes of the attention step: q, K, V once, O and LSE once
+    attn_compulsory = (w.batch * w.tokens * w.query_heads * D * e
+                       + 2 * w.batch * w.keys * w.key_heads * D * e
+                       + w.batch * w.tokens * w.query_heads * (D * e + 4))
+    # the dominant kernel: its algorithmic work per launch over its average launch
+    # (windowed kernels launch once per window of query tokens)
     dominant = max((n for n in per_step if n in algo), key=per_step.get)
     n_launch = max(launches[dominant], 1)
     dom_ms = per_step[dominant] / n_launch
     info = algo[dominant]
-    achieved = info["bytes"] / (per_step[dominant] * 1e-3)
     traffic = profiled_traffic(dominant, w.name)
-    roofline = {"kernel": dominant, "bound": "hbm", "achieved": round(achieved / 1e9, 1),
-                "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4),
-                "traffic": traffic, "avg_launch_ms": round(dom_ms, 4),
-                "launches_per_step": n_launch,
-                "algorithmic_bytes_per_launch": int(info["bytes"] / n_launch)}
+    if info["bound"] == "mfma":
+        achieved = info["flops"] / n_launch / (dom_ms * 1e-3)
+        peak = MFMA_PEAK[dname]
+        roofline = {"kernel": dominant, "bound": "mfma", "achieved": round(achieved / 1e12, 2),
+                    "peak": peak / 1e12, "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
+                    "traffic": traffic, "avg_launch_ms": round(dom_ms, 4),
+                    "launches_per_step": n_launch,
+                    "algorithmic_flops_per_launch": int(info["flops"] / n_launch),
+                    "design_bytes_per_launch": int(info["bytes"] / n_launch),
+                    "design_bytes_frac_hbm": round(info["bytes"] / n_launch / (dom_ms * 1e-3)
+                                                   / HBM_PEAK, 4)}
+        if dominant == "attn_fwd":
+            comp = attn_compulsory / n_launch
+            roofline["compulsory_bytes_per_launch"] = int(comp)
+            roofline["traffic_over_compulsory"] = round(traffic / comp, 2) if traffic else None
+    else:
+        achieved = info["bytes"] / n_launch / (dom_ms * 1e-3)
+        roofline = {"kernel": dominant, "bound": "hbm", "achieved": round(achieved / 1e9, 1),
+                    "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4),
+                    "traffic": traffic, "avg_launch_ms": round(dom_ms, 4),
+                    "launches_per_step": n_launch,
+                    "algorithmic_bytes_per_launch": int(info["bytes"] / n_launch)}
     # selection bytes of the reference's Q4 schedule (grouping_triton.py, leaf_triton.py:63-232):
     # q rows once, internal candidates' child rows, candidates, one key block per tile of
     # four leaf requests plus each request's q rows and bookkeeping, the final network's reads
@@ -436,10 +498,7 @@ def main():
     gather_bytes = items * 2 * w.topk * w.block_size * D * e
 
     attn_flops = 4 * D * G * pairs
-    attn_kernel_ms = per_step.get("attn_fwd", 0) + per_step.get("attn_combine", 0)
     leaf_ms = per_step.get("leaf", 0)
-    sel_kernels = ["pool", "route_dense", "route", "fill", "bucket_count", "bucket_scan",
-                   "bucket_scatter", "leaf", "final"]
     sel_bytes = sum(algo[n]["bytes"] for n in ("pool", "route", "route_dense", "leaf", "final"))
     result = {
         "metric": "selection ms + sparse-attn TFLOP/s at 64K prefill; % HBM / % MFMA peak",
@@ -486,10 +545,9 @@ def main():
         result["attn_fwd_bwd_ms"] = round(train_ms, 3)
         result["attn_fwd_bwd_tflops"] = round(14 * D * G * pairs / (train_ms * 1e-3) / 1e12, 2)
         result["attn_fwd_bwd_kernel_ms"] = dict(sorted(train_kernels.items(), key=lambda x: -x[1]))
-    del sel_kernels
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
-        result["cpu_baseline"] = cpu_baseline(w, q, k, args.cpu_sample)
+        result["cpu_baseline"] = cpu_baseline(w, q, k, v, args.cpu_sample, args.cpu_chunks)
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)

@@ -1,15 +1,19 @@
-"""Decode-time token and key-pyramid caches: ``TensorCache`` and ``PyramidCache``.
+"""Decode-time caches: appended key/value tokens and the key pyramid over them.
 
-Mirrors ``xmixers/xmixers/utils/attention_cache.py:8-140``.  ``TensorCache``
-keeps appended [B, T, H, D] tokens in a buffer whose capacity grows to the next
-power of two.  ``PyramidCache`` keeps every level of the key pyramid in one
-allocation -- level capacities are the next power of two of the leaf count, then
-``ceil(c / branching)`` down to 1, so level offsets change only when the leaf
-capacity grows -- and ``append`` recomputes only the changed leaf and its
-ancestors on the GPU (``pisa_pyramid_append``), with the numerics of
-``build_pyramid``.  The cache plugs into ``select_blocks(pyramid=...)``: it
-exposes ``storage``, ``starts``/``offsets``, ``lengths`` and ``level_sizes``, and
-its views have a batch stride larger than their length.
+Format and attributes of ``xmixers/xmixers/utils/attention_cache.py:8-140``
+(``TensorCache``, ``PyramidCache``), which ``select_blocks(pyramid=...)`` and the
+layer's decode path consume: one ``storage`` allocation ``[B, sum(capacity_l),
+Hkv, D]`` holding every level, host ``starts``/``capacities``/``level_sizes``,
+device ``offsets``/``lengths`` (int32), views whose batch stride exceeds their
+length.
+
+Design here: level capacities and live sizes both come from the library's
+``pisa_pyramid_layout`` (capacities are the layout of a power-of-two leaf
+count, so they halve - or divide by ``branching`` - down to one); the means are
+written by the HIP ``pisa_pyramid_append`` kernel, which recomputes only the
+changed leaves and their ancestors.  When the leaf capacity grows, the new
+storage is rebuilt from all held keys by the same kernel (a pass over the keys
+per doubling) instead of copying the old levels.
 """
 
 from __future__ import annotations
@@ -18,10 +22,19 @@ import torch
 
 from . import _lib
 from ._common import dtype_code, ptr, require_gpu, stream_of
+from .pooling import pyramid_layout
+
+
+def _pow2_at_least(n):
+    return 1 << max(0, int(n) - 1).bit_length()
 
 
 class TensorCache:
-    """Append-only, detached [B, T, H, D] storage for inference."""
+    """Append-only, detached [B, T, H, D] token storage for inference.
+
+    ``buffer`` holds a power-of-two number of token slots; ``tensor`` is the
+    filled prefix of ``length`` tokens.
+    """
 
     def __init__(self):
         self.buffer = None
@@ -29,37 +42,47 @@ class TensorCache:
 
     @classmethod
     def from_tensor(cls, tensor):
-        return cls().append(tensor)
+        cache = cls()
+        cache.append(tensor)
+        return cache
 
     @property
     def tensor(self):
         if self.buffer is None:
             raise ValueError("the token cache is empty")
-        return self.buffer[:, : self.length]
+        return self.buffer.narrow(1, 0, self.length)
+
+    @staticmethod
+    def _signature(t):
+        return t.shape[0], tuple(t.shape[2:]), t.dtype, t.device
+
+    def _admit(self, tensor):
+        if tensor.ndim != 4 or tensor.shape[1] == 0 or not tensor.is_floating_point():
+            raise ValueError("new tokens must be a nonempty [B,T,H,D] floating tensor")
+        if self.buffer is not None and self._signature(self.buffer) != self._signature(tensor):
+            raise ValueError("cache batch, heads, dimension, dtype and device cannot change")
+
+    def _room_for(self, tokens, like):
+        held = 0 if self.buffer is None else self.buffer.shape[1]
+        if tokens <= held:
+            return
+        slots = like.new_empty((like.shape[0], _pow2_at_least(tokens), *like.shape[2:]))
+        if self.length:
+            slots.narrow(1, 0, self.length).copy_(self.tensor)
+        self.buffer = slots
 
     @torch.no_grad()
     def append(self, tensor):
-        if tensor.ndim != 4 or tensor.shape[1] == 0 or not tensor.is_floating_point():
-            raise ValueError("new tokens must be a nonempty [B,T,H,D] floating tensor")
-        if self.buffer is not None:
-            held = (self.buffer.shape[0], *self.buffer.shape[2:], self.buffer.dtype,
-                    self.buffer.device)
-            if held != (tensor.shape[0], *tensor.shape[2:], tensor.dtype, tensor.device):
-                raise ValueError("cache batch, heads, dimension, dtype and device cannot change")
-        end = self.length + tensor.shape[1]
-        if self.buffer is None or end > self.buffer.shape[1]:
-            capacity = 1 << (end - 1).bit_length()
-            grown = tensor.new_empty(tensor.shape[0], capacity, *tensor.shape[2:])
-            if self.buffer is not None:
-                grown[:, : self.length].copy_(self.tensor)
-            self.buffer = grown
-        self.buffer[:, self.length : end].copy_(tensor)
-        self.length = end
+        self._admit(tensor)
+        count = tensor.shape[1]
+        self._room_for(self.length + count, tensor)
+        self.buffer.narrow(1, self.length, count).copy_(tensor)
+        self.length += count
         return self
 
 
 class PyramidCache:
-    """Key means of every pyramid level in one allocation, updated incrementally.
+    """Key means of every pyramid level in one allocation, updated incrementally on the GPU.
 
     ``branching`` generalises the reference's binary pyramid (2, the default).
     """
@@ -81,7 +104,9 @@ class PyramidCache:
 
     @classmethod
     def from_keys(cls, keys, block_size=64, branching=2):
-        return cls(block_size, branching).append(keys)
+        cache = cls(block_size, branching)
+        cache.append(keys)
+        return cache
 
     @property
     def length(self):
@@ -103,57 +128,63 @@ class PyramidCache:
     def buffers(self):
         if self.storage is None:
             return []
-        return [self.storage[:, start:start + capacity]
-                for start, capacity in zip(self.starts, self.capacities)]
+        return [self.storage.narrow(1, s, c) for s, c in zip(self.starts, self.capacities)]
 
     @property
     def levels(self):
-        return [buffer[:, :size] for buffer, size in zip(self.buffers, self.sizes)]
+        return [self.storage.narrow(1, s, n) for s, n in zip(self.starts, self.sizes)]
+
+    def _live_sizes(self):
+        """Nodes per level for the held tokens: the pyramid layout of ``length``
+        keys, continued at one node up to the capacity's level count."""
+        if not self.length:
+            return [0] * len(self.starts)
+        _, live = pyramid_layout(self.length, self.block_size, self.branching)
+        return (live + [1] * len(self.starts))[:len(self.starts)]
+
+    def _recompute(self, previous):
+        """Means of the leaves from ``previous // block_size`` on and their
+        ancestors, from the held keys (``previous = 0``: every node)."""
+        source = self.tokens.buffer
+        batch, _, heads, dim = source.shape
+        starts = (_lib.ctypes.c_int32 * len(self.starts))(*self.starts)
+        code = dtype_code(source, "HIP pooling requires float16, bfloat16, or float32 dtype")
+        with torch.cuda.device(source.device):
+            _lib.check(_lib.library().pisa_pyramid_append(
+                ptr(source), source.stride(0), source.stride(1), batch, previous, self.length,
+                heads, dim, self.block_size, self.branching, len(self.starts), starts,
+                ptr(self.storage), self.storage.stride(0), code, stream_of(source)))
+        self.sizes = self._live_sizes()
+        self.lengths = torch.tensor(self.sizes, dtype=torch.int32).to(source.device,
+                                                                      non_blocking=True)
 
     def reserve(self, reference, leaves):
-        """Room for ``leaves`` leaf means; grows (and re-lays out) to a power of two."""
+        """Room for ``leaves`` leaf means (a power-of-two capacity).  Growing re-lays
+        out the levels and rebuilds them from the held keys; returns whether it grew."""
         if self.capacities and leaves <= self.capacities[0]:
-            return
-        capacity = 1 << (leaves - 1).bit_length()
-        capacities, starts, total = [], [], 0
-        while True:
-            capacities.append(capacity)
-            starts.append(total)
-            total += capacity
-            if capacity == 1:
-                break
-            capacity = -(-capacity // self.branching)
-        storage = reference.new_empty(reference.shape[0], total, *reference.shape[2:])
-        for start, previous in zip(starts, self.levels):
-            storage[:, start:start + previous.shape[1]].copy_(previous)
-        self.storage = storage
-        self.capacities, self.starts = tuple(capacities), tuple(starts)
-        self.offsets = torch.tensor(starts, device=reference.device, dtype=torch.int32)
-        self.lengths = torch.zeros(len(starts), device=reference.device, dtype=torch.int32)
+            return False
+        cap = _pow2_at_least(leaves)
+        starts, capacities = pyramid_layout(cap * self.block_size, self.block_size,
+                                            self.branching)
+        total = starts[-1] + capacities[-1]
+        self.storage = reference.new_empty((reference.shape[0], total, *reference.shape[2:]))
+        self.starts, self.capacities = tuple(starts), tuple(capacities)
+        self.offsets = torch.tensor(starts, dtype=torch.int32).to(reference.device)
+        if self.length:
+            self._recompute(0)
+        else:
+            self.sizes = [0] * len(starts)
+            self.lengths = torch.zeros(len(starts), dtype=torch.int32, device=reference.device)
+        return True
 
     @torch.no_grad()
     def append(self, keys):
         """Append [B, T, Hkv, D] keys; recompute the changed leaves and their ancestors."""
         require_gpu(keys, "the pyramid cache")
-        code = dtype_code(keys, "HIP pooling requires float16, bfloat16, or float32 dtype")
+        dtype_code(keys, "HIP pooling requires float16, bfloat16, or float32 dtype")
         previous = self.length
         self.tokens.append(keys)
-        length = self.length
-        leaves = -(-length // self.block_size)
-        self.reserve(keys, leaves)
-        source = self.tokens.buffer
-        batch, _, heads, dim = source.shape
-        levels = len(self.starts)
-        starts = (_lib.ctypes.c_int32 * levels)(*self.starts)
-        with torch.cuda.device(keys.device):
-            _lib.check(_lib.library().pisa_pyramid_append(
-                ptr(source), source.stride(0), source.stride(1), batch, previous, length, heads,
-                dim, self.block_size, self.branching, levels, starts, ptr(self.storage),
-                self.storage.stride(0), code, stream_of(keys)))
-        sizes, count = [], leaves
-        for _ in range(levels):
-            sizes.append(count)
-            count = -(-count // self.branching)
-        self.sizes = sizes
-        self.lengths.copy_(torch.tensor(sizes, dtype=torch.int32))
+        leaves = -(-self.length // self.block_size)
+        if not self.reserve(keys, leaves):       # a grown storage is rebuilt already
+            self._recompute(previous)
         return self

@@ -14,7 +14,8 @@ Every function cites the reference file:line it restates (paths relative to
 * pooled sums are exact (float64) before the single rounding to float32 and to
   the storage dtype; the reference sums in float32 (``mean_pooling_torch.py:10-13``)
   whose order-dependent last bits the GPU cannot reproduce.  The two agree up
-  to one storage ulp on rare elements (pinned in ``tests/test_oracle_golden.py``).
+  to one storage ulp on rare elements; on the reference's golden selections
+  (``tests/golden/select_b2.npz``, ``tests/test_oracle.py``) the ids are equal.
 
 Parity status of each function (what pins it) is listed in the module
 docstring of ``tests/test_oracle.py``; none is "parity unpinned".

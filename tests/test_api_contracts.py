@@ -147,3 +147,69 @@ def test_pyramid_cache_layout():
         P.PyramidCache(branching=1)
     with pytest.raises(ValueError, match="runs on a ROCm GPU"):
         P.PyramidCache().append(torch.zeros(1, 4, 2, 8))
+
+
+def test_layer_config_methods_and_routing_default():
+    """``pisa_config.py:63-79``: every attention method of the reference is accepted
+    (bsa included), pisa1 defaults to fused prefill routing and the others to grouped;
+    the layer itself declines the NSA baseline."""
+    for method in ("full", "bsa", "pisa1", "pisa2", "pisa"):
+        cfg = P.PisaLayerConfig(attention_method=method)
+        assert cfg.prefill_routing == ("fused" if method == "pisa1" else "grouped")
+    with pytest.raises(ValueError, match="Unknown attention method"):
+        P.PisaLayerConfig(attention_method="dense")
+    with pytest.raises(ValueError, match="prefill_routing must be grouped or fused"):
+        P.PisaLayerConfig(prefill_routing="flat")
+    with pytest.raises(ValueError, match="not provided"):
+        P.PyramidSparseAttention(P.PisaLayerConfig(attention_method="nsa"))
+
+
+def test_token_positions_brute_force():
+    """Positions restart at each packed document (``pyramid_sparse_attention.py:6-11``):
+    token t of document [a, e) sits at t - a + offset, checked token by token."""
+    cu = torch.tensor([0, 3, 3, 10, 17])
+    got = P.token_positions(17, "cpu", cu, offset=4)
+    bounds = cu.tolist()
+    for t in range(17):
+        start = max(a for a in bounds[:-1] if a <= t)
+        assert int(got[0, t]) == t - start + 4
+    assert P.token_positions(5, "cpu", None, 7).tolist() == [[7, 8, 9, 10, 11]]
+
+
+@pytest.mark.parametrize("dim,base,fraction", [(64, 10000.0, 0.5), (128, 500000.0, 1.0),
+                                               (32, 10000.0, 0.25)])
+def test_rotary_table_closed_form(dim, base, fraction):
+    """The layer's float32 frequency table (``lrpe.py:20-28``, evaluated with torch's
+    float32 CPU power as the reference does) is base^(-2i/D) to within one float32 ulp
+    of the float64 closed form and of the oracle's table, zero past the fraction."""
+    import numpy as np
+    import oracle as O
+    theta = P.RotaryEmbedding(dim, base, fraction).theta
+    assert theta.dtype == torch.float32 and tuple(theta.shape) == (1, dim // 2)
+    got = theta.numpy()[0].astype(np.float64)
+    count = int(dim // 2 * fraction)
+    exact = base ** (-2.0 * np.arange(dim // 2) / dim)
+    ulp = np.spacing(np.float32(np.maximum(exact, 1e-30))).astype(np.float64)
+    assert (np.abs(got[:count] - exact[:count]) <= ulp[:count]).all()
+    assert not got[count:].any()
+    oracle = O.rotary_frequency(dim, base, fraction).astype(np.float64)
+    assert (np.abs(got - oracle) <= ulp).all()
+
+
+def test_benchmark_result_files(tmp_path):
+    """The selection sweep writes the reference benchmark's files: selection.json with
+    metadata and rows, selection.csv with head_dim, length and a "<label> (ms)" column
+    per provider (``benchmark.py:13-19`` labels)."""
+    import csv
+    import json
+    from nlogn_pisa_amd import benchmark as B
+    res = B.Results(tmp_path, {"seed": 2024}, ["fused", "q4", "bsa"])
+    res.add(64, 4096, {"fused": 1.25, "q4": 0.5, "bsa": "ERROR"}, {"bsa": "failed"})
+    res.add(128, 8192, {"fused": 2.0, "q4": 1.0, "bsa": 3.0}, {})
+    rows = list(csv.reader(open(tmp_path / "selection.csv")))
+    assert rows[0] == ["head_dim", "length", "Direct-LSE fused (ms)", "Direct-LSE Q4 (ms)",
+                       "BSA Top-K (ms)"]
+    assert rows[1] == ["64", "4096", "1.25", "0.5", "ERROR"]
+    data = json.load(open(tmp_path / "selection.json"))
+    assert data["metadata"] == {"seed": 2024} and len(data["rows"]) == 2
+    assert data["rows"][0]["errors"] == {"bsa": "failed"}

@@ -157,3 +157,31 @@ def test_layer_gradients_match_torch(P):
         err = (a - b).abs().max().item() / max(1.0, b.abs().max().item())
         print(f"grad {name} relative error {err:.2e}")
         assert err <= 1e-4, name
+
+
+def test_layer_bsa_prefill_and_decode(P):
+    """``attention_method="bsa"`` (``pisa_config.py:71-79``): prefill equals the flat BSA
+    selection followed by sparse attention on the layer's own rotated q/k, and decode
+    through the token cache (``key_storage``) equals decode over the concatenated keys."""
+    print("layer bsa", flush=True)
+    layer = _layer(P, "bf16", "bsa", block_size=32, topk=6, force_recent=2)
+    c = layer.config
+    torch.manual_seed(4)
+    x = torch.randn(1, 300, 128, device="cuda").to(torch.bfloat16)
+    with torch.no_grad():
+        out, cache = layer(x, use_cache=True)
+        pos = P.token_positions(300, x.device)
+        q = layer.rope(layer.q_proj(x).view(1, 300, 8, 32), pos)
+        k = layer.rope(layer.k_proj(x).view(1, 300, 2, 32), pos)
+        v = layer.v_proj(x).view(1, 300, 2, 32)
+        ids = P.bsa_fn(q, k, c.block_size, c.topk, force_first=c.force_first,
+                       force_recent=c.force_recent)
+        ref = layer.o_proj(P.sparse_attention(q, k, v, ids, block_size=c.block_size).flatten(2))
+        assert torch.equal(out, ref)
+        assert set(cache) == {"k", "v", "key_storage", "value_storage"}
+        step = torch.randn(1, 1, 128, device="cuda").to(torch.bfloat16)
+        plain = {"k": cache["k"].clone(), "v": cache["v"].clone()}
+        out_cached, cache = layer(step, cache=cache, use_cache=True)
+        out_plain, _ = layer(step, cache=plain, use_cache=False)
+        assert torch.equal(out_cached, out_plain)
+        assert cache["k"].shape[1] == 301

@@ -17,7 +17,7 @@ scores                 closed forms: LSE, mean+var/2, binary pisa2 == general fo
 sparse_attention       dense textbook attention (union mask), torch fp64 autograd,
                        finite differences for the gradients, LSE closed form
 rotary_frequency       closed form base^(-2i/d) within float32 rounding, zero tail count
-rotary                 invariants: pair norms kept, identity at position 0, turns compose
+rotary                 closed form of a unit vector's turn (sign), invariants: pair norms kept, identity at position 0, turns compose
                        (p1 then p2 == p1 + p2), negated frequencies undo the turn
 =====================  ==========================================================
 """
@@ -383,3 +383,27 @@ def test_rotary_invariants():
     # negated frequencies undo the turn
     np.testing.assert_allclose(O.rotary(y, -freq, pos), x, atol=1e-9)
 
+
+
+def test_rotary_sign_closed_form():
+    """Pins the direction of the turn (``rotary_torch.py:5-10``): a unit vector at
+    feature f, turned by theta = p * frequency[f], becomes cos(theta) at f and
+    +sin(theta) at f + D/2; a unit vector at f + D/2 becomes -sin(theta) at f and
+    cos(theta) at f + D/2.  A flipped sign fails both."""
+    dim, half = 16, 8
+    freq = O.rotary_frequency(dim, 10000.0, 1.0)
+    pos = np.array([[0, 1, 7, 300]])
+    for f in range(half):
+        theta = (pos[0].astype(np.float32) * freq[f]).astype(np.float64)
+        lo = np.zeros((1, 4, 1, dim))
+        lo[..., f] = 1.0
+        y = O.rotary(lo, freq, pos)[0, :, 0]
+        np.testing.assert_allclose(y[:, f], np.cos(theta), atol=1e-15)
+        np.testing.assert_allclose(y[:, f + half], np.sin(theta), atol=1e-15)
+        hi = np.zeros((1, 4, 1, dim))
+        hi[..., f + half] = 1.0
+        y = O.rotary(hi, freq, pos)[0, :, 0]
+        np.testing.assert_allclose(y[:, f], -np.sin(theta), atol=1e-15)
+        np.testing.assert_allclose(y[:, f + half], np.cos(theta), atol=1e-15)
+        others = [i for i in range(dim) if i not in (f, f + half)]
+        assert not y[:, others].any()
