@@ -59,8 +59,8 @@ def _compile(source, obj_dir, extra):
 def build(verbose=True, library=LIBRARY, extra_flags=(), obj_dir=OUT_DIR):
     """Compile every HIP source and link ``libpisa_hip.so``; returns its path.
 
-    ``library``, ``extra_flags`` (e.g. ``-D`` tuning constants) and ``obj_dir``
-    build another copy of the library, loadable through ``PISA_HIP_LIBRARY``.
+    ``library``, ``extra_flags`` (extra hipcc options) and ``obj_dir`` build
+    another copy of the library, loadable through ``PISA_HIP_LIBRARY``.
     """
     os.makedirs(obj_dir, exist_ok=True)
     sources = sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))

@@ -327,13 +327,10 @@ __global__ void __launch_bounds__(64) attn_fwd_direct_kernel(AttnArgs a, int64_t
 // computed once per tile into LDS, and each wave loads the next unit's query
 // rows while it computes the current one.
 
-// 1: a unit's 16 partial rows pass through the wave's LDS rows 8 at a time (half
-// the staging LDS, so three forward workgroups fit a CU at 64-key blocks instead
-// of two: config 2 attn_fwd 7.97 -> 6.98 ms).
-#ifndef PISA_ATTN_HALF_STAGE
-#define PISA_ATTN_HALF_STAGE 1
-#endif
-constexpr int kStageRows = PISA_ATTN_HALF_STAGE ? 8 : 16;
+// A unit's 16 partial rows pass through the wave's LDS rows 8 at a time (half
+// the staging LDS of 16, so three forward workgroups fit a CU at 64-key blocks
+// instead of two: config 2 attn_fwd 7.97 -> 6.98 ms).
+constexpr int kStageRows = 8;
 
 // LDS of one tile: K block [Cq][HD + PAD], V^T [HD][Cq + PAD], per request
 // the query row offset (int64), position (int64) and slot (int32), then per
@@ -371,30 +368,9 @@ __host__ __device__ inline TileLds tile_lds(int C, int tile, int waves, bool wit
   return L;
 }
 
-// Tuning constants of the forward tile kernel: query-row prefetch depth
-// (units), key fragments in registers (blocks of up to 64 keys), minimum waves
-// per SIMD requested from the compiler.
-#ifndef PISA_ATTN_DEPTH
-#define PISA_ATTN_DEPTH 2
-#endif
-#ifndef PISA_ATTN_KREG
-#define PISA_ATTN_KREG 0
-#endif
-#ifndef PISA_ATTN_WAVES
-#define PISA_ATTN_WAVES 2
-#endif
-// 1: the forward tile kernel walks its tiles XCD-contiguously (xcd_tiles).
-#ifndef PISA_ATTN_XCD
-#define PISA_ATTN_XCD 0
-#endif
-// 1: every backward takes the LDS-staged kernel (for comparisons).
-#ifndef PISA_BWD_LDS
-#define PISA_BWD_LDS 0
-#endif
-// 0: the register-tile backward never shares P/dS between waves.
-#ifndef PISA_BWD_SHARE
-#define PISA_BWD_SHARE 1
-#endif
+// Query-row prefetch depth of the forward tile kernel (units in flight while one
+// is computed; blocks of up to 64 keys).
+constexpr int kFwdDepth = 2;
 
 // LDS row of value dv in V^T: dv = (D/4) j + 4 dt + c is stored at row
 // 16 dt + 4 j + c, the row that lane col = 4 j + c reads for dv tile dt, so the
@@ -515,17 +491,7 @@ __device__ void fwd_tile_units(const AttnArgs& a, const TileLds& L, const T* ks,
   const int units = (nreq * Gp + 15) >> 4;
   const T* q = static_cast<const T*>(a.q);
 
-  // key-block A fragments held in registers when they take at most 64 VGPRs
-  // (blocks of up to 64 keys)
-  constexpr bool KREG = PISA_ATTN_KREG && NTM <= 4 && NTM * QL * sizeof(T) <= 256;
-  constexpr int DEPTH = NTM <= 4 ? PISA_ATTN_DEPTH : 1;
-  constexpr int KR = KREG ? NTM : 1;
-  frag kreg[KR][DS];
-#pragma unroll
-  for (int mt = 0; mt < KR; ++mt) {
-    if (KREG && mt < NT) load_row_frags<E>(ks + (mt * 16 + col) * L.ldk + E * grp, kreg[mt]);
-    else zero_frags(kreg[mt]);
-  }
+  constexpr int DEPTH = NTM <= 4 ? kFwdDepth : 1;
 
   // Query rows of unit u.  The load is issued by every lane: rows that do not
   // exist (padding heads or requests, units past the end) read request 0's
@@ -548,18 +514,13 @@ __device__ void fwd_tile_units(const AttnArgs& a, const TileLds& L, const T* ks,
     for (int mt = 0; mt < NTM; ++mt) {
       s[mt] = f4{0.f, 0.f, 0.f, 0.f};
       if (mt < NT) {
-        if constexpr (KREG) {
+        frag kf[DS];
+        if (kg)  // key rows straight from memory (rows past the block repeat its last)
+          load_row_frags<E>(kg + (int64_t)min(mt * 16 + col, rows - 1) * kg_stride + E * grp, kf);
+        else
+          load_row_frags<E>(ks + (mt * 16 + col) * L.ldk + E * grp, kf);
 #pragma unroll
-          for (int d = 0; d < DS; ++d) s[mt] = Op::mma(kreg[mt][d], qf[d], s[mt]);
-        } else {
-          frag kf[DS];
-          if (kg)  // key rows straight from memory (rows past the block repeat its last)
-            load_row_frags<E>(kg + (int64_t)min(mt * 16 + col, rows - 1) * kg_stride + E * grp, kf);
-          else
-            load_row_frags<E>(ks + (mt * 16 + col) * L.ldk + E * grp, kf);
-#pragma unroll
-          for (int d = 0; d < DS; ++d) s[mt] = Op::mma(kf[d], qf[d], s[mt]);
-        }
+        for (int d = 0; d < DS; ++d) s[mt] = Op::mma(kf[d], qf[d], s[mt]);
       }
     }
     // softmax statistics of row `col` (lane groups hold disjoint keys); this
@@ -632,27 +593,23 @@ __device__ void fwd_tile_units(const AttnArgs& a, const TileLds& L, const T* ks,
 #pragma unroll
         for (int i = 0; i < 4; ++i) vals[4 * dt + i] = (PT)(o[dt][i] * inv);
       if (so) {
-        if constexpr (kStageRows == 8) {
-          // rows 8 hp .. 8 hp + 7 through the wave's 8 LDS rows, then out as whole rows
-          constexpr int CH = HD * (int)sizeof(PT) / 16;  // 16-byte chunks per row
-          constexpr int CE = 16 / (int)sizeof(PT);
+        // rows 8 hp .. 8 hp + 7 through the wave's 8 LDS rows, then out as whole rows
+        constexpr int CH = HD * (int)sizeof(PT) / 16;  // 16-byte chunks per row
+        constexpr int CE = 16 / (int)sizeof(PT);
 #pragma unroll
-          for (int hp = 0; hp < 2; ++hp) {
-            if ((col >> 3) == hp) store_vals(so + (col & 7) * L.ldo + QL * grp, vals);
-            wave_lds_sync();
+        for (int hp = 0; hp < 2; ++hp) {
+          if ((col >> 3) == hp) store_vals(so + (col & 7) * L.ldo + QL * grp, vals);
+          wave_lds_sync();
 #pragma unroll
-            for (int idx = lane; idx < 8 * CH; idx += 64) {
-              const int r = idx / CH, cc = idx % CH;
-              const int rho2 = (u << 4) + 8 * hp + r, rq2 = rho2 >> gl, gh2 = rho2 & (Gp - 1);
-              if (rq2 < nreq && gh2 < a.G) {
-                const uint4 v = *reinterpret_cast<const uint4*>(so + r * L.ldo + cc * CE);
-                stream_store16(static_cast<PT*>(a.part_o) + ((int64_t)mslot[rq2] * a.G + gh2) * HD + cc * CE, v);
-              }
+          for (int idx = lane; idx < 8 * CH; idx += 64) {
+            const int r = idx / CH, cc = idx % CH;
+            const int rho2 = (u << 4) + 8 * hp + r, rq2 = rho2 >> gl, gh2 = rho2 & (Gp - 1);
+            if (rq2 < nreq && gh2 < a.G) {
+              const uint4 v = *reinterpret_cast<const uint4*>(so + r * L.ldo + cc * CE);
+              stream_store16(static_cast<PT*>(a.part_o) + ((int64_t)mslot[rq2] * a.G + gh2) * HD + cc * CE, v);
             }
-            wave_lds_sync();  // the rows are out; the next half may overwrite them
           }
-        } else {
-          store_vals(so + col * L.ldo + QL * grp, vals);
+          wave_lds_sync();  // the rows are out; the next half may overwrite them
         }
       } else if (valid) {
         PT* dst = static_cast<PT*>(a.part_o) + ((int64_t)mslot[rq] * a.G + gh) * HD + QL * grp;
@@ -668,21 +625,6 @@ __device__ void fwd_tile_units(const AttnArgs& a, const TileLds& L, const T* ks,
       }
       if (valid && grp == 0) stream_store(a.part_lse + (int64_t)mslot[rq] * a.G + gh, m + __logf(l));
     }
-    if (so && kStageRows == 16) {
-      wave_lds_sync();
-      constexpr int CH = HD * (int)sizeof(PT) / 16;  // 16-byte chunks per row
-      constexpr int CE = 16 / (int)sizeof(PT);
-#pragma unroll
-      for (int idx = lane; idx < 16 * CH; idx += 64) {
-        const int r = idx / CH, c = idx % CH;
-        const int rho2 = (u << 4) + r, rq2 = rho2 >> gl, gh2 = rho2 & (Gp - 1);
-        if (rq2 < nreq && gh2 < a.G) {
-          const uint4 v = *reinterpret_cast<const uint4*>(so + r * L.ldo + c * CE);
-          stream_store16(static_cast<PT*>(a.part_o) + ((int64_t)mslot[rq2] * a.G + gh2) * HD + c * CE, v);
-        }
-      }
-      wave_lds_sync();  // the rows are out; the next unit may overwrite them
-    }
   };
   frag qb[DEPTH + 1][DS];
 #pragma unroll
@@ -695,7 +637,7 @@ __device__ void fwd_tile_units(const AttnArgs& a, const TileLds& L, const T* ks,
 }
 
 template <typename T, int HD, int NTM>
-__global__ void __launch_bounds__(256, PISA_ATTN_WAVES) attn_fwd_tile_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(256, 2) attn_fwd_tile_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   // partial rows staged per wave only where the staging keeps several workgroups per CU
   constexpr bool STAGE = NTM <= 4;
@@ -709,12 +651,7 @@ __global__ void __launch_bounds__(256, PISA_ATTN_WAVES) attn_fwd_tile_kernel(Att
   typedef typename PartialT<T>::type PT;
   PT* so = STAGE ? reinterpret_cast<PT*>(smem + L.o_off) + wave * kStageRows * L.ldo : nullptr;
   const int ntiles = *a.num_tiles;
-#if PISA_ATTN_XCD
-  const XcdTiles walk = xcd_tiles(ntiles);  // grid_size() is a multiple of 8
-#else
-  const XcdTiles walk{(int)blockIdx.x, ntiles, (int)gridDim.x};
-#endif
-  for (int tile = walk.begin; tile < walk.end; tile += walk.step) {
+  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
     const int g = a.tile_group[tile];
     const int64_t blk = g % a.M0;
     const int bh = g / a.M0;
@@ -851,10 +788,6 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a, int64_t i
 // the wave's LDS.  Then O = sum_s w_s o_s / L in slot order, one FMA per
 // element and slot, and LSE = M + ln L.
 constexpr int kCombinePairs = 256;
-
-#ifndef PISA_COMBINE2
-#define PISA_COMBINE2 1
-#endif
 
 template <typename T>
 __global__ void __launch_bounds__(256) attn_combine2_kernel(AttnArgs a, int64_t items) {
@@ -1966,7 +1899,7 @@ int launch_attn_partials(int dtype, const AttnArgs& a, bool grouped, int64_t slo
 int launch_attn_combine(int dtype, const AttnArgs& a, int64_t items, hipStream_t stream) {
   if (items <= 0) return PISA_OK;
   const dim3 grid((unsigned)((items + 3) / 4)), block(256);
-  const bool two_pass = PISA_COMBINE2 && a.K >= 1 && (int64_t)a.K * a.G <= kCombinePairs &&
+  const bool two_pass = a.K >= 1 && (int64_t)a.K * a.G <= kCombinePairs &&
                         a.G <= 64 && (a.G & (a.G - 1)) == 0;
   if (two_pass) {
     switch (dtype) {
@@ -2014,12 +1947,12 @@ static bool launch_bwd_tiles(const AttnArgs& a, hipStream_t stream) {
     if (bwd_tile_lds<T, HD>(nt, a.tile).bytes > (size_t)device_lds_limit()) return false;
     if constexpr (HD == 128) {
       // shared P/dS: two workgroups per CU up to 64-key blocks, one at 128 keys
-      if (PISA_BWD_SHARE && nt <= 4 && 2 * bwd_share_lds<T, HD>(nt, a.tile) <= (size_t)device_lds_limit()) {
+      if (nt <= 4 && 2 * bwd_share_lds<T, HD>(nt, a.tile) <= (size_t)device_lds_limit()) {
         if (nt == 2) launch_bwd_share<T, HD, 2>(a, stream);
         else launch_bwd_share<T, HD, 4>(a, stream);
         return true;
       }
-      if (PISA_BWD_SHARE && nt == 8 && bwd_share_lds<T, HD>(nt, a.tile) <= (size_t)device_lds_limit()) {
+      if (nt == 8 && bwd_share_lds<T, HD>(nt, a.tile) <= (size_t)device_lds_limit()) {
         launch_bwd_share<T, HD, 8>(a, stream);
         return true;
       }
@@ -2044,7 +1977,7 @@ static bool launch_bwd_tiles(const AttnArgs& a, hipStream_t stream) {
 
 template <typename T, int HD>
 static void launch_bwd_kernel(const AttnArgs& a, hipStream_t stream) {
-  if (!PISA_BWD_LDS && tile_path(a) && launch_bwd_tiles<T, HD>(a, stream)) return;
+  if (tile_path(a) && launch_bwd_tiles<T, HD>(a, stream)) return;
   const int Cp = (a.C + 15) / 16 * 16;
   const size_t lds = bwd_lds(a, sizeof(T));
   allow_lds((const void*)attn_bwd_grouped_kernel<T, HD>, lds);

@@ -12,10 +12,7 @@ using namespace pisa;
 namespace {
 
 constexpr int kAttnTile = 256;  // requests per attention tile (backward)
-#ifndef PISA_ATTN_FWD_TILE
-#define PISA_ATTN_FWD_TILE 256
-#endif
-constexpr int kAttnFwdTile = PISA_ATTN_FWD_TILE;  // requests per attention forward tile
+constexpr int kAttnFwdTile = 256;  // requests per attention forward tile
 
 bool pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
 
@@ -29,17 +26,11 @@ int padded_group(int g) { return next_pow2(g); }
 
 namespace pisa {
 
-// Window budgets: q bytes of all heads per window of leaf scoring and of the
-// attention forward (0: a single window).
-#ifndef PISA_WINDOW_BYTES
-#define PISA_WINDOW_BYTES (128 << 20)
-#endif
-#ifndef PISA_ATTN_WINDOW_BYTES
-#define PISA_ATTN_WINDOW_BYTES PISA_WINDOW_BYTES
-#endif
+// Window budget: q bytes of all heads per window of leaf scoring and of the
+// attention forward.
+constexpr int64_t kWindowBytes = 128 << 20;
 
 int query_window(int64_t tokens, int64_t row_bytes, int64_t budget) {
-  if (budget <= 0) return (int)std::max<int64_t>(1, tokens);
   int64_t w = 256;
   while (w * 2 * std::max<int64_t>(row_bytes, 1) <= budget) w *= 2;
   return (int)std::max<int64_t>(1, std::min<int64_t>(w, tokens));
@@ -115,7 +106,7 @@ int plan_select(const pisa_qk_desc* qk, const pisa_select_params* p, SelectPlan&
   pl.spans = (pl.M0 + pl.span - 1) / pl.span;
   pl.groups = (int64_t)qk->batch * qk->key_heads * pl.spans;
   const int64_t flat = (int64_t)qk->batch * qk->query_tokens;
-  pl.window = query_window(flat, (int64_t)qk->query_heads * D * es, PISA_WINDOW_BYTES);
+  pl.window = query_window(flat, (int64_t)qk->query_heads * D * es, kWindowBytes);
   pl.window_slots = (int64_t)pl.window * qk->key_heads * pl.W / pl.span;
   // routing levels scored densely (every node for every item) before the route
   for (int l = 0; l < PISA_MAX_LEVELS; ++l) pl.dense_nodes[l] = 0;
@@ -318,7 +309,7 @@ namespace {
 int leaf_window(const pisa_qk_desc* qk) {
   return query_window((int64_t)qk->batch * qk->query_tokens,
                       (int64_t)qk->query_heads * qk->head_dim * dtype_size(qk->dtype),
-                      PISA_WINDOW_BYTES);
+                      kWindowBytes);
 }
 
 void carve_leaf(const pisa_qk_desc* qk, int block_size, int width, Carve& c, uint8_t** mask,
@@ -445,7 +436,7 @@ int plan_attn(const pisa_attn_desc* d, AttnPlan& pl) {
   pl.Cp = (d->block_size + 15) / 16 * 16;
   pl.grouped = pl.slots >= 4 * pl.groups;
   pl.window = query_window((int64_t)d->batch * d->query_tokens, (int64_t)d->query_heads * d->head_dim * es,
-                           PISA_ATTN_WINDOW_BYTES);
+                           kWindowBytes);
   pl.window_slots = (int64_t)pl.window * d->key_heads * d->topk;
   return PISA_OK;
 }

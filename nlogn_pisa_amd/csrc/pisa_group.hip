@@ -30,10 +30,7 @@
 namespace pisa {
 
 constexpr int kLdsGroups = 16384;  // 64 KB of int32 bins
-#ifndef PISA_BUCKET_ROWS
-#define PISA_BUCKET_ROWS 1024
-#endif
-constexpr int kMaxBucketGroups = PISA_BUCKET_ROWS;  // counting-sort workgroups (histogram rows) per range
+constexpr int kMaxBucketGroups = 1024;  // counting-sort workgroups (histogram rows) per range
 constexpr int kBucketThreads = 256;
 constexpr int64_t kSmallChunk = 4096;    // slots per workgroup with global atomics
 constexpr int64_t kMinChunk = 2048;      // fewest slots per counting-sort workgroup

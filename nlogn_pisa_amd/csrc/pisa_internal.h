@@ -243,10 +243,7 @@ int launch_final(const FinalArgs& a, hipStream_t stream);
 int launch_scoreable(const MaskArgs& a, hipStream_t stream);
 int launch_leaf(int dtype, const LeafArgs& a, hipStream_t stream);
 // Leaf requests per tile (one key-span load each).
-#ifndef PISA_LEAF_TILE
-#define PISA_LEAF_TILE 256
-#endif
-constexpr int kLeafTile = PISA_LEAF_TILE;
+constexpr int kLeafTile = 256;
 // Sibling blocks per leaf request for the grouped schedule (1: one block each).
 int leaf_span(int dtype, int head_dim, int block_size, int branching, int group, int method,
               int64_t items);

@@ -171,9 +171,7 @@ __global__ void __launch_bounds__(256) leaf_kernel(LeafArgs a) {
 // units (Gp > 16).
 
 // Padding of an LDS key row (bytes; a multiple of 8).
-#ifndef PISA_LEAF_PAD_BYTES
-#define PISA_LEAF_PAD_BYTES 16
-#endif
+constexpr int kLeafPadBytes = 16;
 
 struct LeafLds {
   int Cq, ldk;
@@ -188,7 +186,7 @@ __host__ __device__ inline LeafLds leaf_lds(int C, int tile, int span = 1) {
   typedef QkShape<T, HD> S;
   LeafLds L;
   L.Cq = (C + S::KQ - 1) / S::KQ * S::KQ;
-  L.ldk = HD + PISA_LEAF_PAD_BYTES / (int)sizeof(T);
+  L.ldk = HD + kLeafPadBytes / (int)sizeof(T);
   size_t off = 0;
   L.k_off = off;
   off += (size_t)span * L.Cq * L.ldk * sizeof(T);
@@ -203,18 +201,9 @@ __host__ __device__ inline LeafLds leaf_lds(int C, int tile, int span = 1) {
   return L;
 }
 
-// Tuning constants of the leaf tile kernel: query-row prefetch depth (units),
-// key fragments in registers (blocks of up to 64 keys), and the minimum waves
-// per SIMD requested from the compiler at up to 64 keys.
-#ifndef PISA_LEAF_DEPTH
-#define PISA_LEAF_DEPTH 2
-#endif
-#ifndef PISA_LEAF_KREG
-#define PISA_LEAF_KREG 0
-#endif
-#ifndef PISA_LEAF_WAVES
-#define PISA_LEAF_WAVES 3
-#endif
+// Query-row prefetch depth of the leaf tile kernel (units in flight while one is
+// scored).
+constexpr int kLeafDepth = 2;
 
 // Sibling blocks scored per request at most (a power of two).
 constexpr int kMaxSpan = 4;
@@ -222,16 +211,13 @@ constexpr int kMaxSpan = 4;
 // SPAN: the most sibling blocks a request of this instance scores (1, or
 // kMaxSpan with the span read from the arguments).
 template <typename T, int HD, int NTM, int SPAN>
-__global__ void __launch_bounds__(SPAN > 1 ? 512 : 256, (NTM <= 4 ? PISA_LEAF_WAVES : 2))
+__global__ void __launch_bounds__(SPAN > 1 ? 512 : 256, (NTM <= 4 ? 3 : 2))
 leaf_tile_kernel(LeafArgs a) {
   typedef QkShape<T, HD, NTM> S;
   typedef typename S::Op Op;
   typedef typename S::frag frag;
   constexpr int E = S::E, QL = S::QL, DS = S::DS;
-  constexpr int DEPTH = PISA_LEAF_DEPTH;
-  // key-block A fragments held in registers when they take at most 64 VGPRs
-  constexpr bool KREG = PISA_LEAF_KREG && NTM <= 4 && NTM * QL * sizeof(T) <= 256;
-  constexpr int KR = KREG ? NTM : 1;
+  constexpr int DEPTH = kLeafDepth;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int span = SPAN > 1 ? a.span : 1;
   const LeafLds L = leaf_lds<T, HD>(a.C, a.tile, span);
@@ -301,14 +287,6 @@ leaf_tile_kernel(LeafArgs a) {
       *reinterpret_cast<uint4*>(ks + r * L.ldk + c) = v;
     }
     __syncthreads();
-
-    // this wave's A fragments of the whole key block, read from LDS once per tile
-    frag kreg[KR][DS];
-#pragma unroll
-    for (int mt = 0; mt < KR; ++mt) {
-      if (KREG && mt < NT) load_row_frags<E>(ks + (mt * 16 + col) * L.ldk + E * grp, kreg[mt]);
-      else zero_frags(kreg[mt]);
-    }
 
     const int items = (nreq + rpu - 1) >> rpl;
     // Query rows of unit j of item r.  The load is issued by every lane: rows
@@ -413,15 +391,10 @@ leaf_tile_kernel(LeafArgs a) {
         for (int mt = 0; mt < NTM; ++mt) {
           s[mt] = f4{0.f, 0.f, 0.f, 0.f};
           if (mt < NT) {
-            if (KREG && SPAN == 1) {
+            frag kf[DS];
+            load_row_frags<E>(kc + (mt * 16 + col) * L.ldk + E * grp, kf);
 #pragma unroll
-              for (int d = 0; d < DS; ++d) s[mt] = Op::mma(kreg[mt][d], cur[d], s[mt]);
-            } else {
-              frag kf[DS];
-              load_row_frags<E>(kc + (mt * 16 + col) * L.ldk + E * grp, kf);
-#pragma unroll
-              for (int d = 0; d < DS; ++d) s[mt] = Op::mma(kf[d], cur[d], s[mt]);
-            }
+            for (int d = 0; d < DS; ++d) s[mt] = Op::mma(kf[d], cur[d], s[mt]);
           }
         }
         const float head = head_of(full_tag, s, c);
@@ -467,17 +440,8 @@ __host__ __device__ inline size_t leaf_split_lds(int nu, int tile) {
   return (size_t)2 * nu * 16 * (HD + 16 / sizeof(T)) * sizeof(T) + (size_t)tile * 16;
 }
 
-// Units per staged batch, batches of query rows in flight (1 or 2), and the
-// minimum waves per SIMD requested from the compiler.
-#ifndef PISA_LEAF_NU
-#define PISA_LEAF_NU 4
-#endif
-#ifndef PISA_LEAF_SPLIT_DEPTH
-#define PISA_LEAF_SPLIT_DEPTH 1
-#endif
-#ifndef PISA_LEAF_SPLIT_WAVES
-#define PISA_LEAF_SPLIT_WAVES 3
-#endif
+// Units (16 rows each) per staged batch of query rows at four waves.
+constexpr int kLeafBatchUnits = 4;
 
 // NTM: key tiles a wave holds (2: up to 32 keys, 4: up to 64); LSE: log-sum-exp
 // support scores, else the moment form (pisa2).  BW: waves per block - with two,
@@ -485,11 +449,8 @@ __host__ __device__ inline size_t leaf_split_lds(int nu, int tile) {
 // each batch the odd wave leaves its rows' partial statistics (max and sum of
 // exponentials, or the two moment sums) in LDS, and past the batch barrier the
 // even wave joins them and writes the scores.
-#ifndef PISA_LEAF_HALF_WAVES
-#define PISA_LEAF_HALF_WAVES 3
-#endif
 template <typename T, int HD, int SPAN, int NU, int NTM, bool LSE, int BW = 1>
-__global__ void __launch_bounds__(64 * SPAN * BW, BW == 2 ? PISA_LEAF_HALF_WAVES : PISA_LEAF_SPLIT_WAVES)
+__global__ void __launch_bounds__(64 * SPAN * BW, 3)
 leaf_split_kernel(LeafArgs a) {
   typedef QkShape<T, HD> S;
   typedef typename S::Op Op;
@@ -740,28 +701,6 @@ leaf_split_kernel(LeafArgs a) {
           a.scores[mslot[rq] + c] = v;
       }
     };
-    // Two register sets: batch i + 2 is loaded while batch i is scored and batch
-    // i + 1 (loaded during batch i - 1) goes to LDS after it; the loop is
-    // unrolled by two so the sets alternate without copies.  nb is uniform over
-    // the workgroup, so every wave meets the same barriers.
-    auto run2 = [&](auto full_tag) __attribute__((always_inline)) {
-      u32x4v sa[LPT], sb[LPT];
-      fetch(0, sa);
-      stage(0, sa);
-      if (1 < nb) fetch(1, sb);
-      __syncthreads();
-      for (int i = 0; i < nb; i += 2) {
-        if (i + 2 < nb) fetch(i + 2, sa);
-        if (rows_valid > 0) score_batch(full_tag, i);
-        if (i + 1 < nb) stage((i + 1) & 1, sb);
-        __syncthreads();
-        if (i + 1 >= nb) break;
-        if (i + 3 < nb) fetch(i + 3, sb);
-        if (rows_valid > 0) score_batch(full_tag, i + 1);
-        if (i + 2 < nb) stage(i & 1, sa);
-        __syncthreads();
-      }
-    };
     // One register set: batch i + 1 is loaded while batch i is scored.
     auto run1 = [&](auto full_tag) __attribute__((always_inline)) {
       u32x4v sa[LPT];
@@ -793,7 +732,6 @@ leaf_split_kernel(LeafArgs a) {
     };
     auto run = [&](auto full_tag) __attribute__((always_inline)) {
       if constexpr (BW == 2) run1h(full_tag);
-      else if constexpr (PISA_LEAF_SPLIT_DEPTH >= 2) run2(full_tag);
       else run1(full_tag);
     };
     // FULL: every key of every block of the span is valid (uniform over the workgroup)
@@ -807,19 +745,15 @@ leaf_split_kernel(LeafArgs a) {
 // workgroups per CU still fit), smaller ones four.
 constexpr size_t kLeafWideLds = 48 << 10;
 
-#ifndef PISA_LEAF_SPLIT
-#define PISA_LEAF_SPLIT 1
-#endif
-
 // Split-span kernel of `SPAN` waves; grid = the resident workgroups of the device
 // (a multiple of 8 for the XCD tile walk).
 template <typename T, int HD, int SPAN, int NTM, bool LSE, int BW = 1>
 static void launch_leaf_split(const LeafArgs& a, int cus, hipStream_t stream) {
   constexpr int vpr = HD * (int)sizeof(T) / 16;
   constexpr int W = SPAN * BW;  // waves per workgroup
-  // PISA_LEAF_NU units per batch at four waves, in proportion to the waves
+  // kLeafBatchUnits units per batch at four waves, in proportion to the waves
   // otherwise (the same staging loads per thread), and at least one load per thread
-  constexpr int NU0 = PISA_LEAF_NU * W / 4 > 0 ? PISA_LEAF_NU * W / 4 : 1;
+  constexpr int NU0 = kLeafBatchUnits * W / 4 > 0 ? kLeafBatchUnits * W / 4 : 1;
   constexpr int NU = NU0 * 16 * vpr >= 64 * W ? NU0 : 64 * W / (16 * vpr);
   const void* kernel = (const void*)leaf_split_kernel<T, HD, SPAN, NU, NTM, LSE, BW>;
   // two waves per block: the odd waves' statistics, two batches of NU units of 16 rows per block
@@ -863,7 +797,7 @@ static void launch_leaf_split_t(const LeafArgs& a, int cus, hipStream_t stream) 
 template <typename T, int HD>
 static void launch_leaf_tile(const LeafArgs& a, int cus, hipStream_t stream) {
   if constexpr (sizeof(T) == 2) {
-    if (PISA_LEAF_SPLIT && (a.span == 2 || a.span == 4) && a.method != PISA_METHOD_PISA1 && a.scale > 0.f)
+    if ((a.span == 2 || a.span == 4) && a.method != PISA_METHOD_PISA1 && a.scale > 0.f)
       return launch_leaf_split_t<T, HD>(a, cus, stream);
   }
   const LeafLds L = leaf_lds<T, HD>(a.C, a.tile, a.span);
@@ -897,25 +831,18 @@ static void launch_leaf_tile(const LeafArgs& a, int cus, hipStream_t stream) {
 // blocks of up to 64 keys, where the query rows dominate a tile's traffic
 // (measured: spans for groups of 16 ran slower at D = 128 and mixed at D = 64),
 // and pairs of 128-key blocks in the split kernel (below).
-#ifndef PISA_LEAF_MAX_SPAN
-#define PISA_LEAF_MAX_SPAN kMaxSpan
-#endif
 // Largest head group served by spans.
-#ifndef PISA_LEAF_SPAN_GROUP
-#define PISA_LEAF_SPAN_GROUP 4
-#endif
+constexpr int kSpanGroup = 4;
 // 128-key blocks (16-bit keys, pisa or pisa2, head dims 64 and 128, head groups
-// up to PISA_LEAF_SPAN128_GROUP) go in pairs to the split kernel's two waves per
+// up to kSpan128Group) go in pairs to the split kernel's two waves per
 // block, so a request's query rows serve both siblings - from kSpan128Items
 // (batch x token x kv head) items: below, the single-block tile kernel is faster
 // (config 4 shape at 4K tokens: selection 0.158 ms unpaired, 0.209 ms paired).
-#ifndef PISA_LEAF_SPAN128_GROUP
-#define PISA_LEAF_SPAN128_GROUP 8
-#endif
+constexpr int kSpan128Group = 8;
 constexpr int64_t kSpan128Items = 16384;
 static bool span128(int es, int head_dim, int block_size, int branching, int group, int method) {
-  return PISA_LEAF_SPLIT && es == 2 && block_size == 128 && branching >= 2 &&
-         (head_dim == 64 || head_dim == 128) && group <= PISA_LEAF_SPAN128_GROUP &&
+  return es == 2 && block_size == 128 && branching >= 2 &&
+         (head_dim == 64 || head_dim == 128) && group <= kSpan128Group &&
          method != PISA_METHOD_PISA1;
 }
 
@@ -925,13 +852,13 @@ int leaf_span(int dtype, int head_dim, int block_size, int branching, int group,
   if (!es || (head_dim != 16 && head_dim != 32 && head_dim != 64 && head_dim != 128)) return 1;
   if (block_size > 64)
     return items >= kSpan128Items && span128(es, head_dim, block_size, branching, group, method) ? 2 : 1;
-  if (group > PISA_LEAF_SPAN_GROUP) return 1;
+  if (group > kSpanGroup) return 1;
   const int E = es == 4 ? 1 : ((head_dim / 4) % 8 == 0 ? 8 : 4);
   const int KQ = E == 8 ? 32 : 16;
   const int cq = (block_size + KQ - 1) / KQ * KQ;
-  const int ldk = head_dim + PISA_LEAF_PAD_BYTES / es;
+  const int ldk = head_dim + kLeafPadBytes / es;
   int span = 1;
-  while (span * 2 <= branching && span * 2 <= PISA_LEAF_MAX_SPAN && span * 2 * cq <= 256 &&
+  while (span * 2 <= branching && span * 2 <= kMaxSpan && span * 2 * cq <= 256 &&
          (size_t)span * 2 * cq * ldk * es + (size_t)kLeafTile * 16 <= (80u << 10))
     span *= 2;
   return span;

@@ -39,12 +39,8 @@ constexpr int64_t kFusedWaveItems = 8192;
 // grouped schedule (one buffer fewer keeps more waves per SIMD; the reference
 // benchmark shape's Q4 selection 2.49 -> 2.28 ms at D = 128, 64K tokens) and
 // fused schedule (mixed there: kept at two).
-#ifndef PISA_ROUTE_DEPTH
-#define PISA_ROUTE_DEPTH 1
-#endif
-#ifndef PISA_ROUTE_FUSED_DEPTH
-#define PISA_ROUTE_FUSED_DEPTH 2
-#endif
+constexpr int kRouteDepth = 1;
+constexpr int kRouteFusedDepth = 2;
 
 
 __device__ __forceinline__ int64_t ipow(int64_t b, int e) {
@@ -686,7 +682,7 @@ __global__ void __launch_bounds__(64) route_grouped_kernel(RouteArgs a) {
     };
     // tile mt: scored from `xf`, loads tile mt + DEPTH into `xn` (the buffer the
     // previous tile used); the buffers rotate by unrolling, never by copies
-    constexpr int DEPTH = FUSED ? PISA_ROUTE_FUSED_DEPTH : PISA_ROUTE_DEPTH;
+    constexpr int DEPTH = FUSED ? kRouteFusedDepth : kRouteDepth;
     auto tile = [&](int mt, frag (&xf)[DS], frag (&xn)[DS], const TileMeta<R>& mf, TileMeta<R>& mn) {
       fetch(mt + DEPTH, xn, mn);
       f4 sv = f4{0.f, 0.f, 0.f, 0.f};
@@ -903,10 +899,6 @@ __global__ void __launch_bounds__(256) route_dense_kernel(RouteArgs a) {
 // and each wave takes its MFMA fragments from there.  The products, their order
 // and the per-node scores are the same as route_dense_kernel's.  16-bit inputs.
 constexpr int kDenseCT = 4;
-
-#ifndef PISA_DENSE_LDS
-#define PISA_DENSE_LDS 1
-#endif
 
 template <typename T, int HD, int RR, int MODE>
 __global__ void __launch_bounds__(256) route_dense_lds_kernel(RouteArgs a) {
@@ -1267,20 +1259,18 @@ int launch_route(int dtype, const RouteArgs& a, int64_t items, int threads, hipS
 // gathers.  With one item per tile (Gp = 16) the extra pass over the query
 // rows outweighs the saving (measured), so dense levels need P >= 2; a wave's
 // 4 P items fit its 16 staging rows for P <= 4, i.e. Gp in {4, 8}.
-#ifndef PISA_DENSE_FACTOR
-#define PISA_DENSE_FACTOR 16
-#endif
+constexpr int kDenseFactor = 16;
 bool route_level_dense(int G, int level, int top, int first_width, int branching, int topk,
                        int nodes) {
   const int gp = next_pow2(G);
   if (level < 1 || level > top || gp < 4 || gp > 8 || branching > 8) return false;
   const int width = level == top ? first_width : branching * topk;
-  return (int64_t)nodes <= (int64_t)(PISA_DENSE_FACTOR / gp) * width;
+  return (int64_t)nodes <= (int64_t)(kDenseFactor / gp) * width;
 }
 
 template <typename T, int HD, int RR, int MODE>
 static void launch_dense_rm(const RouteArgs& a, int blocks, hipStream_t stream) {
-  if constexpr (sizeof(T) == 2 && PISA_DENSE_LDS) {
+  if constexpr (sizeof(T) == 2) {
     // four waves of 16 / Gp items x 4 query tiles per workgroup, one (batch, kv head) each
     const int per = 16 * (16 / next_pow2(a.G));
     const int64_t groups = (int64_t)a.batch * a.Hkv * ((a.T + per - 1) / per);
