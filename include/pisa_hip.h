@@ -212,6 +212,21 @@ int pisa_sparse_attention_bwd(const pisa_attn_desc* a, const void* q, const void
                               void* grad_q, void* grad_k, void* grad_v, void* workspace,
                               size_t workspace_bytes, void* stream);
 
+/* pisa_sparse_attention_fwd without a workspace argument and without any
+ * allocation (no counterpart in the reference): for callers that cannot
+ * allocate device memory - code under HIP graph capture, tight decode/serving
+ * loops, harnesses that forbid hipMalloc.  Its workspace is a file-scope
+ * device array of pisa_noalloc_scratch_bytes() (64 MiB) per GPU, held until
+ * the process ends; shapes needing more (pisa_attention_workspace_size) are
+ * rejected with PISA_ERR_WORKSPACE before any launch.  All calls on one GPU
+ * share that array: calls that overlap in time on one GPU (other streams or
+ * threads) race and must be serialised by the caller. */
+size_t pisa_noalloc_scratch_bytes(void);
+int pisa_sparse_attention_fwd_noalloc(const pisa_attn_desc* a, const void* q, const void* k,
+                                      const void* v, const void* indices,
+                                      const int64_t* positions, int64_t positions_stride_batch,
+                                      void* out, float* lse, float* out_f32, void* stream);
+
 /* Kernel timing (no counterpart in the reference; instrumentation for
  * benchmarks).  Between pisa_profile_begin and pisa_profile_end every kernel
  * launch is bracketed by two hipEvents on its stream; pisa_profile_end waits

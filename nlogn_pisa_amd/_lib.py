@@ -29,7 +29,8 @@ EXPORTS = (
     "pisa_last_error", "pisa_abi_version", "pisa_routing_geometry", "pisa_pyramid_layout",
     "pisa_mean_pool", "pisa_build_pyramid", "pisa_pyramid_append", "pisa_rotary", "pisa_select_workspace_size", "pisa_select",
     "pisa_leaf_workspace_size", "pisa_leaf_scores", "pisa_bsa_workspace_size", "pisa_bsa_select", "pisa_attention_workspace_size", "pisa_sparse_attention_fwd",
-    "pisa_sparse_attention_bwd", "pisa_profile_begin", "pisa_profile_end",
+    "pisa_sparse_attention_bwd", "pisa_noalloc_scratch_bytes", "pisa_sparse_attention_fwd_noalloc",
+    "pisa_profile_begin", "pisa_profile_end",
 )
 
 
@@ -116,6 +117,9 @@ def _declare(lib):
                                             P, SZ, P]),
         "pisa_sparse_attention_bwd": (I32, [ctypes.POINTER(AttnDesc), P, P, P, P, P, I64, P, P, P,
                                             P, P, P, P, P, SZ, P]),
+        "pisa_noalloc_scratch_bytes": (SZ, []),
+        "pisa_sparse_attention_fwd_noalloc": (I32, [ctypes.POINTER(AttnDesc), P, P, P, P, P, I64, P,
+                                                    P, P, P]),
         "pisa_profile_begin": (I32, []),
         "pisa_profile_end": (I32, [ctypes.POINTER(KernelTime), I32, ctypes.POINTER(I32)]),
     }
@@ -129,7 +133,7 @@ def library():
     """Load (once) and return the ctypes handle of libpisa_hip.so.
 
     ``PISA_HIP_LIBRARY`` names another build of the same library (e.g. one
-    compiled with different tuning constants) to load instead.
+    compiled with other hipcc options) to load instead.
     """
     global _lib
     if _lib is not None:

@@ -6,6 +6,7 @@
 #include "pisa_internal.h"
 
 #include <algorithm>
+#include <mutex>
 
 using namespace pisa;
 
@@ -609,4 +610,66 @@ extern "C" int pisa_sparse_attention_bwd(const pisa_attn_desc* d, const void* q,
   if (rc) return rc;
   bind_buckets(a, b);
   return launch_attn_bwd(d->dtype, a, pl.groups, pl.items, st);
+}
+
+// ------------------------------------------------------------------ attention forward, no allocation
+
+namespace {
+
+// Workspace of pisa_sparse_attention_fwd_noalloc: a file-scope device array, one
+// copy per GPU, held until the process ends.  In host code `scratch` names a
+// host-side stand-in; the device address comes from hipGetSymbolAddress, taken
+// once per device with that device current, and is what the kernels receive.
+constexpr size_t kScratchBytes = size_t(64) << 20;
+__device__ __align__(256) char scratch[kScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch[kMaxScratchDevices] = {};
+
+// The current device's scratch address (PISA_OK), resolved on its first use.
+int device_scratch(void** out) {
+  int device = -1;
+  if (hipGetDevice(&device) != hipSuccess || device < 0)
+    return fail(PISA_ERR_LAUNCH, "no current HIP device");
+  if (device >= kMaxScratchDevices)
+    return fail(PISA_ERR_UNSUPPORTED, "device %d: scratch is kept for devices 0..%d", device,
+                kMaxScratchDevices - 1);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch[device]) {
+    void* address = nullptr;
+    const hipError_t rc = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+    if (rc != hipSuccess || !address)
+      return fail(PISA_ERR_LAUNCH, "hipGetSymbolAddress(scratch) on device %d: %s", device,
+                  hipGetErrorString(rc));
+    g_scratch[device] = address;
+  }
+  *out = g_scratch[device];
+  return PISA_OK;
+}
+
+}  // namespace
+
+extern "C" size_t pisa_noalloc_scratch_bytes(void) { return kScratchBytes; }
+
+extern "C" int pisa_sparse_attention_fwd_noalloc(const pisa_attn_desc* d, const void* q,
+                                                 const void* k, const void* v,
+                                                 const void* indices, const int64_t* positions,
+                                                 int64_t positions_stride_batch, void* out,
+                                                 float* lse, float* out_f32, void* stream) {
+  AttnPlan pl;
+  int rc = plan_attn(d, pl);
+  if (rc) return rc;
+  if (!q || !k || !v || !positions || !out || !lse || (d->topk && !indices))
+    return fail(PISA_ERR_INVALID, "null tensor argument");
+  const size_t need = pisa_attention_workspace_size(d, 0);
+  if (need > kScratchBytes)
+    return fail(PISA_ERR_WORKSPACE,
+                "attention forward needs %zu scratch bytes; the allocation-free entry point "
+                "holds %zu (use pisa_sparse_attention_fwd with a workspace)", need, kScratchBytes);
+  void* ws = nullptr;
+  rc = device_scratch(&ws);
+  if (rc) return rc;
+  return pisa_sparse_attention_fwd(d, q, k, v, indices, positions, positions_stride_batch, out,
+                                   lse, out_f32, ws, kScratchBytes, stream);
 }
