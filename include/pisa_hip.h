@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PISA_ABI_VERSION 1
+#define PISA_ABI_VERSION 2
 #define PISA_MAX_LEVELS 32
 
 enum pisa_status {
@@ -84,6 +84,15 @@ typedef struct pisa_attn_desc {
   int32_t block_size;    /* C */
   int32_t causal;        /* bool */
   float scale;           /* softmax scale */
+  /* Optional key-block tables for packed documents (both or neither; B = 1):
+   * the indices then address `blocks` key blocks, block j holding keys
+   * block_key_start[j] .. + block_key_rows[j] - 1 (rows <= block_size) of k/v,
+   * and positions count in the same block coordinates (a document's first block
+   * j0 puts its token p at j0 * block_size + p).  NULL: block j holds keys
+   * j * block_size .. min(key_tokens, (j + 1) * block_size) - 1. */
+  const int64_t* block_key_start;
+  const int32_t* block_key_rows;
+  int32_t blocks;
 } pisa_attn_desc;
 
 /* Last error message of this thread ("" when none). */

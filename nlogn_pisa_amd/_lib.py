@@ -74,6 +74,8 @@ class AttnDesc(ctypes.Structure):
         ("v_stride_batch", ctypes.c_int64), ("v_stride_token", ctypes.c_int64),
         ("dtype", ctypes.c_int32), ("topk", ctypes.c_int32), ("index_bits", ctypes.c_int32),
         ("block_size", ctypes.c_int32), ("causal", ctypes.c_int32), ("scale", ctypes.c_float),
+        ("block_key_start", ctypes.c_void_p), ("block_key_rows", ctypes.c_void_p),
+        ("blocks", ctypes.c_int32),
     ]
 
 

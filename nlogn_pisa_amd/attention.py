@@ -12,6 +12,7 @@ from __future__ import annotations
 
 import ctypes
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -20,7 +21,45 @@ from ._common import (dtype_code, kernel_layout, positions_layout, ptr, require_
 from .validation import packed_queries, query_positions, validate_qkv
 
 
-def _attn_desc(q, k, v, indices, block_size, scale, causal):
+class PackedKeys:
+    """Packed documents laid out on whole key blocks, for one launch over all of them.
+
+    Document d (keys [ks, ke), ``nb = ceil((ke - ks) / C)`` blocks) takes blocks
+    ``base_d .. base_d + nb - 1`` of the launch; block ``base_d + j`` holds its keys
+    ``ks + j C .. min(ke, ks + (j + 1) C) - 1``.  A query of the document at local
+    position p sits at ``base_d C + p`` and its local id j becomes ``base_d + j``
+    (ids outside ``[0, nb)`` select nothing, as for a document alone), so the
+    kernels see one sequence of whole blocks and no row reaches another document.
+    """
+
+    def __init__(self, segments, tokens, block_size, device):
+        seg = np.asarray(segments, dtype=np.int64).reshape(-1, 5)
+        qs, qe, ks, ke, offset = seg.T
+        nb = (ke - ks + block_size - 1) // block_size
+        base = np.concatenate([[0], np.cumsum(nb)[:-1]])
+        owner = np.repeat(np.arange(len(seg)), qe - qs)           # document of each query
+        if owner.shape[0] != tokens:
+            raise ValueError("packed segments must cover every query token")
+        local = offset[owner] + np.arange(tokens) - qs[owner]
+        doc_of_block = np.repeat(np.arange(len(seg)), nb)
+        j = np.arange(doc_of_block.shape[0]) - base[doc_of_block]
+        start = ks[doc_of_block] + j * block_size
+        rows = np.minimum(block_size, ke[doc_of_block] - start)
+        self.blocks = int(doc_of_block.shape[0])
+        self.key_start = torch.from_numpy(start).to(device)
+        self.key_rows = torch.from_numpy(rows.astype(np.int32)).to(device)
+        self.positions = torch.from_numpy(base[owner] * block_size + local)[None].to(device)
+        self._base = torch.from_numpy(base[owner]).to(device)[None, :, None, None]
+        self._count = torch.from_numpy(nb[owner]).to(device)[None, :, None, None]
+
+    def block_ids(self, indices):
+        """Document-local ids [1, Tq, Hkv, K] -> ids of the launch's blocks (-1: none)."""
+        ids = indices.long()
+        return torch.where((ids >= 0) & (ids < self._count), ids + self._base,
+                           torch.full_like(ids, -1))
+
+
+def _attn_desc(q, k, v, indices, block_size, scale, causal, packed=None):
     d = _lib.AttnDesc()
     d.batch, d.query_tokens, d.query_heads, d.head_dim = q.shape
     d.key_tokens, d.key_heads = k.shape[1], k.shape[2]
@@ -34,11 +73,16 @@ def _attn_desc(q, k, v, indices, block_size, scale, causal):
     d.block_size = block_size
     d.causal = int(bool(causal))
     d.scale = float(scale)
+    if packed is not None:
+        d.block_key_start = packed.key_start.data_ptr()
+        d.block_key_rows = packed.key_rows.data_ptr()
+        d.blocks = packed.blocks
     return d
 
 
-def _forward(q, k, v, indices, positions, block_size, scale, causal, keep_f32=False):
-    desc = _attn_desc(q, k, v, indices, block_size, scale, causal)
+def _forward(q, k, v, indices, positions, block_size, scale, causal, keep_f32=False,
+             packed=None):
+    desc = _attn_desc(q, k, v, indices, block_size, scale, causal, packed)
     lib = _lib.library()
     out = torch.empty((*q.shape[:3], v.shape[-1]), device=q.device, dtype=q.dtype)
     lse = torch.empty(q.shape[:3], device=q.device, dtype=torch.float32)
@@ -54,8 +98,8 @@ def _forward(q, k, v, indices, positions, block_size, scale, causal, keep_f32=Fa
 
 
 def _backward(q, k, v, indices, positions, out, out32, lse, grad_out, block_size, scale,
-              causal):
-    desc = _attn_desc(q, k, v, indices, block_size, scale, causal)
+              causal, packed=None):
+    desc = _attn_desc(q, k, v, indices, block_size, scale, causal, packed)
     lib = _lib.library()
     grad_out = grad_out.contiguous()
     dq = torch.empty_like(q, memory_format=torch.contiguous_format)
@@ -73,21 +117,22 @@ def _backward(q, k, v, indices, positions, out, out32, lse, grad_out, block_size
 
 class _SparseAttention(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, q, k, v, indices, positions, block_size, scale, causal):
+    def forward(ctx, q, k, v, indices, positions, block_size, scale, causal, packed):
         keep = any(ctx.needs_input_grad[:3])
-        out, lse, out32 = _forward(q, k, v, indices, positions, block_size, scale, causal, keep)
+        out, lse, out32 = _forward(q, k, v, indices, positions, block_size, scale, causal, keep,
+                                   packed)
         ctx.save_for_backward(q, k, v, indices, positions, out, out32, lse)
-        ctx.config = (block_size, scale, causal)
+        ctx.config = (block_size, scale, causal, packed)
         ctx.mark_non_differentiable(lse)
         return out, lse
 
     @staticmethod
     def backward(ctx, grad_out, grad_lse):
         q, k, v, indices, positions, out, out32, lse = ctx.saved_tensors
-        block_size, scale, causal = ctx.config
+        block_size, scale, causal, packed = ctx.config
         dq, dk, dv = _backward(q, k, v, indices, positions, out, out32, lse, grad_out,
-                               block_size, scale, causal)
-        return dq, dk, dv, None, None, None, None, None
+                               block_size, scale, causal, packed)
+        return dq, dk, dv, None, None, None, None, None, None
 
 
 def _check(q, k, v, indices, block_size, backend):
@@ -100,8 +145,7 @@ def _check(q, k, v, indices, block_size, backend):
         raise ValueError("invalid block_size or attention backend")
 
 
-def _unpacked(q, k, v, indices, block_size, scale, query_offset, causal):
-    positions = positions_layout(query_positions(q, k, query_offset))
+def _launch(q, k, v, indices, positions, block_size, scale, causal, packed=None):
     require_gpu(q, "sparse_attention")
     if q.dtype not in (torch.float16, torch.bfloat16, torch.float32):
         raise ValueError("CUDA attention supports FP16, BF16 and FP32")
@@ -110,7 +154,23 @@ def _unpacked(q, k, v, indices, block_size, scale, query_offset, causal):
     k = kernel_layout(k)
     v = kernel_layout(v)
     indices = indices.contiguous()
-    return _SparseAttention.apply(q, k, v, indices, positions, block_size, scale, causal)
+    return _SparseAttention.apply(q, k, v, indices, positions_layout(positions), block_size,
+                                  scale, causal, packed)
+
+
+def _unpacked(q, k, v, indices, block_size, scale, query_offset, causal):
+    return _launch(q, k, v, indices, query_positions(q, k, query_offset), block_size, scale,
+                   causal)
+
+
+def _packed(q, k, v, indices, block_size, scale, cu_seqlens, query_offset, causal):
+    """Every document of a packed batch in one launch sequence (``sparse_attn.py:29-54``
+    semantics: document-local ids and positions, keys of the row's own document)."""
+    require_gpu(q, "sparse_attention")
+    layout = PackedKeys(packed_queries(q, k, cu_seqlens, query_offset), q.shape[1], block_size,
+                        q.device)
+    return _launch(q, k, v, layout.block_ids(indices), layout.positions, block_size, scale,
+                   causal, layout)
 
 
 def sparse_attention_with_lse(q, k, v, indices, block_size=64, scale=None, cu_seqlens=None,
@@ -118,13 +178,7 @@ def sparse_attention_with_lse(q, k, v, indices, block_size=64, scale=None, cu_se
     """(O [B,Tq,Hq,Dv], LSE float32 [B,Tq,Hq]); O is differentiable w.r.t. q, k, v."""
     _check(q, k, v, indices, block_size, backend)
     if cu_seqlens is not None:
-        outs, lses = [], []
-        for qs, qe, ks, ke, offset in packed_queries(q, k, cu_seqlens, query_offset):
-            o, l = _unpacked(q[:, qs:qe], k[:, ks:ke], v[:, ks:ke], indices[:, qs:qe],
-                             block_size, scale, offset, causal)
-            outs.append(o)
-            lses.append(l)
-        return torch.cat(outs, 1), torch.cat(lses, 1)
+        return _packed(q, k, v, indices, block_size, scale, cu_seqlens, query_offset, causal)
     return _unpacked(q, k, v, indices, block_size, scale, query_offset, causal)
 
 

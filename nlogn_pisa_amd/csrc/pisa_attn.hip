@@ -39,6 +39,16 @@ __device__ __forceinline__ int64_t slot_block(const AttnArgs& a, int64_t slot) {
                             : load_index<int32_t>(a.indices, slot);
 }
 
+// Key blocks: block `blk` holds keys [block_key, block_key + block_rows) of the
+// key sequence - blk * C and the rest of the sequence, or, for packed documents
+// laid out one per run of whole blocks, the host's per-block tables.
+__device__ __forceinline__ int64_t block_key(const AttnArgs& a, int64_t blk) {
+  return a.kv_start ? a.kv_start[blk] : blk * a.C;
+}
+__device__ __forceinline__ int block_rows(const AttnArgs& a, int64_t blk) {
+  return a.kv_rows ? a.kv_rows[blk] : (int)min((int64_t)a.C, (int64_t)a.N - blk * a.C);
+}
+
 // A slot is a request iff its block exists and (causal) starts at or before the
 // row's position - exactly the rows bucketed by AttnSrc in pisa_group.hip.
 __device__ __forceinline__ bool slot_visible(const AttnArgs& a, int64_t blk, int64_t pos) {
@@ -72,9 +82,9 @@ template <typename T>
 __device__ void stage_kv(const AttnArgs& a, int b, int h, int64_t blk, int rows, T* ks, int ldk,
                          T* vt, int ldv, int Cp, int tid, int nthr) {
   const int vec = 16 / (int)sizeof(T);
-  const T* kb = static_cast<const T*>(a.k) + (int64_t)b * a.k_batch + blk * a.C * a.k_token +
+  const T* kb = static_cast<const T*>(a.k) + (int64_t)b * a.k_batch + block_key(a, blk) * a.k_token +
                 (int64_t)h * a.D;
-  const T* vb = static_cast<const T*>(a.v) + (int64_t)b * a.v_batch + blk * a.C * a.v_token +
+  const T* vb = static_cast<const T*>(a.v) + (int64_t)b * a.v_batch + block_key(a, blk) * a.v_token +
                 (int64_t)h * a.Dv;
   const int kv_vecs = a.D / vec;
   for (int idx = tid; idx < Cp * kv_vecs; idx += nthr) {
@@ -270,7 +280,7 @@ __global__ void __launch_bounds__(256) attn_fwd_grouped_kernel(AttnArgs a) {
     const int h = bh % a.Hkv, b = bh / a.Hkv;
     const int start = (tile - a.tile_off[g]) * a.tile;
     const int nreq = min(a.tile, a.counts[g] - start);
-    const int rows = (int)min((int64_t)a.C, (int64_t)a.N - blk * a.C);
+    const int rows = block_rows(a, blk);
     __syncthreads();
     stage_kv<T>(a, b, h, blk, rows, ks, ldk, vt, ldv, Cp, tid, blockDim.x);
     __syncthreads();
@@ -301,7 +311,7 @@ __global__ void __launch_bounds__(64) attn_fwd_direct_kernel(AttnArgs a, int64_t
   T* ks = reinterpret_cast<T*>(smem);
   T* vt = ks + Cp * ldk;
   char* wave_lds = smem + (size_t)(Cp * ldk + a.Dv * ldv) * sizeof(T);
-  const int rows = (int)min((int64_t)a.C, (int64_t)a.N - blk * a.C);
+  const int rows = block_rows(a, blk);
   stage_kv<T>(a, ri.b, ri.h, blk, rows, ks, ldk, vt, ldv, Cp, threadIdx.x, blockDim.x);
   __syncthreads();
   const int units = (a.Gp + 15) / 16;
@@ -443,9 +453,9 @@ __device__ void stage_transposed(const T* src, int64_t stride, int rows, int Cq,
 template <typename T, int HD>
 __device__ void stage_tile(const AttnArgs& a, int b, int h, int64_t blk, int rows, T* ks, T* vt,
                            const TileLds& L, int tid, int nthr) {
-  const T* kb = static_cast<const T*>(a.k) + (int64_t)b * a.k_batch + blk * a.C * a.k_token +
+  const T* kb = static_cast<const T*>(a.k) + (int64_t)b * a.k_batch + block_key(a, blk) * a.k_token +
                 (int64_t)h * HD;
-  const T* vb = static_cast<const T*>(a.v) + (int64_t)b * a.v_batch + blk * a.C * a.v_token +
+  const T* vb = static_cast<const T*>(a.v) + (int64_t)b * a.v_batch + block_key(a, blk) * a.v_token +
                 (int64_t)h * HD;
   stage_rows<T, HD>(kb, a.k_token, rows, L.Cq, ks, L.ldk, tid, nthr);
   stage_transposed<T, HD>(vb, a.v_token, rows, L.Cq, vt, L.ldv, tid, nthr);
@@ -658,7 +668,7 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_tile_kernel(AttnArgs a) {
     const int h = bh % a.Hkv, b = bh / a.Hkv;
     const int start = (tile - a.tile_off[g]) * a.tile;
     const int nreq = min(a.tile, a.counts[g] - start);
-    const int rows = (int)min((int64_t)a.C, (int64_t)a.N - blk * a.C);
+    const int rows = block_rows(a, blk);
     const int32_t* reqs = a.tile_req + (int64_t)tile * a.tile;
     __syncthreads();
     for (int i = tid; i < nreq; i += blockDim.x) {
@@ -696,10 +706,10 @@ __global__ void __launch_bounds__(64, 2) attn_fwd_tile_direct_kernel(AttnArgs a,
     mpos[0] = ri.pos;
     mslot[0] = (int32_t)slot;
   }
-  const int rows = (int)min((int64_t)a.C, (int64_t)a.N - blk * a.C);
-  const T* kb = static_cast<const T*>(a.k) + (int64_t)ri.b * a.k_batch + blk * a.C * a.k_token +
+  const int rows = block_rows(a, blk);
+  const T* kb = static_cast<const T*>(a.k) + (int64_t)ri.b * a.k_batch + block_key(a, blk) * a.k_token +
                 (int64_t)ri.h * HD;
-  const T* vb = static_cast<const T*>(a.v) + (int64_t)ri.b * a.v_batch + blk * a.C * a.v_token +
+  const T* vb = static_cast<const T*>(a.v) + (int64_t)ri.b * a.v_batch + block_key(a, blk) * a.v_token +
                 (int64_t)ri.h * HD;
   stage_transposed<T, HD>(vb, a.v_token, rows, L.Cq, vt, L.ldv, threadIdx.x, blockDim.x);
   __syncthreads();
@@ -960,11 +970,11 @@ __global__ void __launch_bounds__(512) attn_bwd_grouped_kernel(AttnArgs a) {
     const int h = bh % a.Hkv, b = bh / a.Hkv;
     const int start = (tile - a.tile_off[g]) * a.tile;
     const int nreq = min(a.tile, a.counts[g] - start);
-    const int rows = (int)min((int64_t)a.C, (int64_t)a.N - blk * a.C);
+    const int rows = block_rows(a, blk);
     const int32_t* reqs = a.tile_req + (int64_t)tile * a.tile;
-    const T* kb = static_cast<const T*>(a.k) + (int64_t)b * a.k_batch + blk * a.C * a.k_token +
+    const T* kb = static_cast<const T*>(a.k) + (int64_t)b * a.k_batch + block_key(a, blk) * a.k_token +
                   (int64_t)h * HD;
-    const T* vb = static_cast<const T*>(a.v) + (int64_t)b * a.v_batch + blk * a.C * a.v_token +
+    const T* vb = static_cast<const T*>(a.v) + (int64_t)b * a.v_batch + block_key(a, blk) * a.v_token +
                   (int64_t)h * HD;
     __syncthreads();
     // K transposed into LDS (B operand of dQ = dS K)
@@ -1143,7 +1153,7 @@ __global__ void __launch_bounds__(256) attn_dkv_reduce_kernel(AttnArgs a, int64_
   const int64_t blk = g % a.M0;
   const int64_t bh = g / a.M0;
   const int h = (int)(bh % a.Hkv), b = (int)(bh / a.Hkv);
-  const int rows = (int)min((int64_t)a.C, (int64_t)a.N - blk * a.C);
+  const int rows = block_rows(a, blk);
   const int first = a.tile_off[g];
   const int n = (a.counts[g] + a.tile - 1) / a.tile;
   const int width = a.D + a.Dv;  // a multiple of 4
@@ -1175,7 +1185,7 @@ __global__ void __launch_bounds__(256) attn_dkv_reduce_kernel(AttnArgs a, int64_
       acc.z += v.z;
       acc.w += v.w;
     }
-    const int64_t tok = blk * a.C + r;
+    const int64_t tok = block_key(a, blk) + r;
     const float vals[4] = {acc.x, acc.y, acc.z, acc.w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -1377,7 +1387,7 @@ __global__ void __launch_bounds__(64 * W, W == 4 ? 2 : 1) attn_bwd_tile_kernel(A
     const int h = bh % a.Hkv, b = bh / a.Hkv;
     const int start = (tile - a.tile_off[g]) * a.tile;
     const int nreq = min(a.tile, a.counts[g] - start);
-    const int rows = (int)min((int64_t)a.C, (int64_t)a.N - blk * a.C);
+    const int rows = block_rows(a, blk);
     const int32_t* reqs = a.tile_req + (int64_t)tile * a.tile;
     __syncthreads();  // every wave is done with the previous tile's LDS
     for (int i = tid; i < nreq; i += blockDim.x) {
@@ -1389,9 +1399,9 @@ __global__ void __launch_bounds__(64 * W, W == 4 ? 2 : 1) attn_bwd_tile_kernel(A
       mslot[i] = slot;
     }
     {
-      const T* kb = static_cast<const T*>(a.k) + (int64_t)b * a.k_batch + blk * a.C * a.k_token +
+      const T* kb = static_cast<const T*>(a.k) + (int64_t)b * a.k_batch + block_key(a, blk) * a.k_token +
                     (int64_t)h * HD;
-      const T* vb = static_cast<const T*>(a.v) + (int64_t)b * a.v_batch + blk * a.C * a.v_token +
+      const T* vb = static_cast<const T*>(a.v) + (int64_t)b * a.v_batch + block_key(a, blk) * a.v_token +
                     (int64_t)h * HD;
       stage_rows<T, HD>(kb, a.k_token, rows, L.Cq, ks, L.ldk, tid, blockDim.x);
       stage_rows<T, HD>(vb, a.v_token, rows, L.Cq, vs, L.ldk, tid, blockDim.x);
@@ -1609,7 +1619,7 @@ __global__ void __launch_bounds__(256, NT <= 4 ? 2 : 1) attn_bwd_share_kernel(At
     const int h = bh % a.Hkv, b = bh / a.Hkv;
     const int start = (tile - a.tile_off[g]) * a.tile;
     const int nreq = min(a.tile, a.counts[g] - start);
-    const int rows = (int)min((int64_t)a.C, (int64_t)a.N - blk * a.C);
+    const int rows = block_rows(a, blk);
     const int32_t* reqs = a.tile_req + (int64_t)tile * a.tile;
     __syncthreads();  // every wave is done with the previous tile's LDS
     for (int i = tid; i < nreq; i += blockDim.x) {
@@ -1621,9 +1631,9 @@ __global__ void __launch_bounds__(256, NT <= 4 ? 2 : 1) attn_bwd_share_kernel(At
       mslot[i] = slot;
     }
     {
-      const T* kb = static_cast<const T*>(a.k) + (int64_t)b * a.k_batch + blk * a.C * a.k_token +
+      const T* kb = static_cast<const T*>(a.k) + (int64_t)b * a.k_batch + block_key(a, blk) * a.k_token +
                     (int64_t)h * HD;
-      const T* vb = static_cast<const T*>(a.v) + (int64_t)b * a.v_batch + blk * a.C * a.v_token +
+      const T* vb = static_cast<const T*>(a.v) + (int64_t)b * a.v_batch + block_key(a, blk) * a.v_token +
                     (int64_t)h * HD;
       stage_rows<T, HD>(kb, a.k_token, rows, L.Cq, ks, L.ldk, tid, blockDim.x);
       stage_rows<T, HD>(vb, a.v_token, rows, L.Cq, vs, L.ldk, tid, blockDim.x);

@@ -430,7 +430,11 @@ int plan_attn(const pisa_attn_desc* d, AttnPlan& pl) {
       d->k_stride_token % vec || d->v_stride_batch % vec || d->v_stride_token % vec)
     return fail(PISA_ERR_UNSUPPORTED, "batch and token strides must be multiples of 16 bytes");
   pl.G = d->query_heads / d->key_heads;
-  pl.M0 = (d->key_tokens + d->block_size - 1) / d->block_size;
+  if ((d->block_key_start == nullptr) != (d->block_key_rows == nullptr))
+    return fail(PISA_ERR_INVALID, "block_key_start and block_key_rows come together");
+  if (d->block_key_start && (d->batch != 1 || d->blocks < 1))
+    return fail(PISA_ERR_INVALID, "key-block tables need batch 1 and blocks >= 1");
+  pl.M0 = d->block_key_start ? d->blocks : (d->key_tokens + d->block_size - 1) / d->block_size;
   pl.items = (int64_t)d->batch * d->query_tokens * d->key_heads;
   pl.slots = pl.items * d->topk;
   pl.groups = (int64_t)d->batch * d->key_heads * pl.M0;
@@ -471,6 +475,8 @@ AttnArgs attn_args(const pisa_attn_desc* d, const AttnPlan& pl, const void* q, c
   a.M0 = pl.M0;
   a.causal = d->causal ? 1 : 0;
   a.scale = d->scale;
+  a.kv_start = d->block_key_start;
+  a.kv_rows = d->block_key_rows;
   return a;
 }
 

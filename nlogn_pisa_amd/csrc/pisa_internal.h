@@ -205,6 +205,10 @@ struct AttnArgs {
   int64_t pos_batch;
   int T, Hkv, G, Gp, D, Dv, N, K, C, M0, causal;
   float scale;
+  // optional per-block key tables (packed documents): first key and valid keys
+  // of block blk; null: blk * C and min(C, N - blk * C)
+  const int64_t* kv_start;
+  const int32_t* kv_rows;
   // request tiles (pisa_group.hip)
   const int32_t* tile_group;
   const int32_t* tile_req;

@@ -185,17 +185,20 @@ def _select_unpacked(q, k, method, block_size, topk, query_offset, force_first, 
 @torch.no_grad()
 def select_blocks_traced(q, k, method="pisa", block_size=64, topk=8, query_offset=None,
                          force_first=True, force_recent=2, routing_schedule="auto", branching=2,
-                         pyramid=None):
+                         pyramid=None, geometry=None):
     """``select_blocks`` plus int32 [B, Tq, Hkv, top + 1, K]: the ids each level kept.
 
-    For tie adjudication against a CPU restatement; not a reference API.
+    ``geometry`` (top, first width) overrides the keys' own routing geometry, as a
+    packed fused selection shares the longest document's.  For tie adjudication
+    against a CPU restatement; not a reference API.
     """
     validate_qkv(q, k)
     if routing_schedule == "auto":
         grouped = method != "pisa1" and q.shape[1] > 1
         routing_schedule = "grouped" if grouped else "fused"
     return _select_unpacked(q, k, method, block_size, topk, query_offset, force_first,
-                            force_recent, pyramid, routing_schedule, None, branching, trace=True)
+                            force_recent, pyramid, routing_schedule, geometry, branching,
+                            trace=True)
 
 
 @torch.no_grad()

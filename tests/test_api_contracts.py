@@ -213,3 +213,41 @@ def test_benchmark_result_files(tmp_path):
     data = json.load(open(tmp_path / "selection.json"))
     assert data["metadata"] == {"seed": 2024} and len(data["rows"]) == 2
     assert data["rows"][0]["errors"] == {"bsa": "failed"}
+
+
+@pytest.mark.parametrize("bounds,decode", [([0, 700, 1500, 1536, 2300], False),
+                                           ([0, 64, 65, 200, 4096], False),
+                                           ([0, 900, 2000, 4096], True)])
+def test_packed_key_layout(bounds, decode):
+    """One-launch packed attention: every document's local block j is a whole block
+    of the launch whose keys are exactly the document's keys [ks + jC, min(ke, ks + (j+1)C)),
+    a query's position lies in its own document's blocks at its local offset, and ids
+    outside the document's blocks select nothing (``sparse_attn.py:29-54``)."""
+    import numpy as np
+    from nlogn_pisa_amd.attention import PackedKeys
+    C, n = 64, bounds[-1]
+    docs = list(zip(bounds[:-1], bounds[1:]))
+    tq = len(docs) if decode else n
+    q = torch.zeros(1, tq, 2, 8)
+    k = torch.zeros(1, n, 1, 8)
+    segments = P.packed_queries(q, k, torch.tensor(bounds), None)
+    layout = PackedKeys(segments, tq, C, "cpu")
+    start, rows = layout.key_start.numpy(), layout.key_rows.numpy()
+    positions = layout.positions.numpy()[0]
+    nb = [-(-(e - s) // C) for s, e in docs]
+    assert layout.blocks == sum(nb)
+    local = torch.arange(-2, max(nb) + 2).repeat(tq, 1)[None, :, None, :]   # [1, Tq, 1, ids]
+    mapped = layout.block_ids(local).numpy()[0, :, 0]
+    for t in range(tq):
+        d = t if decode else next(i for i, (s, e) in enumerate(docs) if s <= t < e)
+        s, e = docs[d]
+        base = sum(nb[:d])
+        p = (e - s - 1) if decode else t - s
+        assert positions[t] == base * C + p
+        for j, g in zip(local[0, t, 0].tolist(), mapped[t].tolist()):
+            if 0 <= j < nb[d]:
+                assert g == base + j
+                assert start[g] == s + j * C and rows[g] == min(C, e - s - j * C)
+                assert g * C <= positions[t] or j * C > p      # causal test in block coordinates
+            else:
+                assert g == -1

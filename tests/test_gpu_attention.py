@@ -229,3 +229,31 @@ def test_packed_decode(P):
                                             positions=pos)
         assert excess_error(out[:, d:d + 1].float().cpu().numpy(), ref_o, "bf16") <= 2e-2
         assert np.abs(lse[:, d:d + 1].cpu().numpy() - ref_lse).max() <= 2e-2
+
+
+def test_packed_attention_is_one_launch_sequence(P):
+    """The packed forward runs every document in one launch of each kernel (the
+    documents share the launch's key blocks) - not one launch series per document,
+    the per-document loop of ``sparse_attn.py:40-54`` - and equals the documents
+    attended one at a time, bit for bit."""
+    from nlogn_pisa_amd import _lib
+    bounds = [0, 130, 700, 1500, 1536, 2300, 2301, 4096]
+    n, qh, kh, dim, block, topk = bounds[-1], 8, 2, 64, 64, 6
+    q, k, v = structured_qkv(33, 1, n, qh, kh, dim, "bf16")
+    idx = _packed_indices(41, bounds, kh, topk, block)
+    qg, kg, vg = (to_gpu(x, "bf16") for x in (q, k, v))
+    ig = torch.from_numpy(idx).cuda()
+    cu = torch.tensor(bounds, dtype=torch.int32, device="cuda")
+    with torch.no_grad():
+        _lib.profile_begin()
+        out, lse = P.sparse_attention_with_lse(qg, kg, vg, ig, block, cu_seqlens=cu)
+        kernels = _lib.profile_end()
+        launches = {name: count for name, (count, _) in kernels.items()}
+        print("packed launches:", launches)
+        assert launches.get("attn_fwd", 0) + launches.get("attn_fwd_direct", 0) == 1
+        assert launches["attn_combine"] == 1
+        for s, e in zip(bounds[:-1], bounds[1:]):
+            o, l = P.sparse_attention_with_lse(qg[:, s:e], kg[:, s:e], vg[:, s:e], ig[:, s:e],
+                                               block)
+            assert torch.equal(out[:, s:e], o), f"document [{s}, {e})"
+            assert torch.equal(lse[:, s:e], l), f"document [{s}, {e})"

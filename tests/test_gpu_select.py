@@ -14,6 +14,7 @@ import pytest
 import torch
 
 import oracle as O
+import parity
 from parity import adjudicate, structured_qkv, to_gpu
 
 pytestmark = pytest.mark.gpu
@@ -199,3 +200,37 @@ def test_packed_documents(P):
     for s, e in ((0, 1000), (1000, 1700), (1700, 3000)):
         alone = P.select_blocks(qg[:, s:e], kg[:, s:e], "pisa", 64, 8, force_recent=1)
         assert torch.equal(out[:, s:e], alone)
+
+
+@pytest.mark.parametrize("method", ["pisa", "pisa1"])
+def test_packed_fused_geometry_matches_oracle(P, method):
+    """Fused packed routing shares the longest document's geometry
+    (``top_k_pyramid.py:73-86``): each document's ids, checked against the oracle run
+    with that shared geometry on the document alone (its pyramid padded to the shared
+    depth, ``top_k_pyramid_torch.py:147``)."""
+    print(f"packed fused geometry {method}", flush=True)
+    bounds = [0, 3000, 3300, 9000]
+    block, topk, b = 64, 8, 4
+    q, k = structured_qkv(13, 1, bounds[-1], 8, 2, 64, "bf16", value=False)
+    qg, kg = to_gpu(q, "bf16"), to_gpu(k, "bf16")
+    cu = torch.tensor(bounds, dtype=torch.int32, device="cuda")
+    out = P.select_blocks(qg, kg, method, block, topk, cu_seqlens=cu, force_recent=1,
+                          routing_schedule="fused", branching=b).cpu().numpy()
+    longest = max(-(-(e - s) // block) for s, e in zip(bounds[:-1], bounds[1:]))
+    geometry = O.routing_geometry(longest, topk, b)
+    for s, e in zip(bounds[:-1], bounds[1:]):
+        qd, kd = q[:, s:e], k[:, s:e]
+        alone = -(-(e - s) // block)
+        ids, trace = P.selection.select_blocks_traced(
+            qg[:, s:e], kg[:, s:e], method, block, topk, force_recent=1,
+            routing_schedule="fused", branching=b, geometry=geometry)
+        assert np.array_equal(out[:, s:e], ids.cpu().numpy())
+        levels = O.build_pyramid(kd, block, b, None, "bf16")
+        pos = O.query_positions(1, e - s, e - s)
+        tokens = np.unique(np.linspace(0, e - s - 1, 200).astype(np.int64))
+        res = parity.selection_parity(qd, kd, ids.cpu().numpy(), trace.cpu().numpy(), tokens,
+                                      method, block, topk, True, 1, b, levels, pos,
+                                      geometry=geometry)
+        print(f"document [{s}, {e}) ({alone} blocks, shared top {geometry[0]}): "
+              f"{res['rows']} rows, {res['mismatched']} differ, {res['exempt']} tie-exempt")
+        assert not res["failures"]
