@@ -72,19 +72,49 @@ def select_blocks(q, k, method="pisa", block_size=64, topk=8, cu_seqlens=None, q
             q.shape[1] == k.shape[1] or (cu_seqlens is None and q.shape[1] > 1))
         routing_schedule = "grouped" if grouped else "fused"
     if cu_seqlens is not None:
-        segments = packed_queries(q, k, cu_seqlens, query_offset)
-        blocks = max((ke - ks + block_size - 1) // block_size for _, _, ks, ke, _ in segments)
-        geometry = (routing_geometry(blocks, topk, branching) if routing_schedule == "fused"
-                    else None)
-        pieces = [
-            _select_unpacked(q[:, qs:qe], k[:, ks:ke], method, block_size, topk, offset,
-                             force_first, force_recent, None, routing_schedule, geometry,
-                             branching)
-            for qs, qe, ks, ke, offset in segments
-        ]
-        return torch.cat(pieces, 1)
+        return _select_packed(q, k, method, block_size, topk, cu_seqlens, query_offset,
+                              force_first, force_recent, routing_schedule, branching)
     return _select_unpacked(q, k, method, block_size, topk, query_offset, force_first,
                             force_recent, pyramid, routing_schedule, None, branching)
+
+
+def _select_packed(q, k, method, block_size, topk, cu_seqlens, query_offset, force_first,
+                   force_recent, routing_schedule, branching):
+    """Packed documents (``top_k_pyramid.py:73-86``): document-local ids, each document
+    routed with its own depth (grouped) or the longest document's (fused).
+
+    Documents run as the rows of zero-padded batches, one launch series per batch:
+    a document's ids do not depend on keys past its end, because a scored block or
+    node lies wholly before the query's current block (later ones fail the position
+    test, the current block's ancestors are forced), so padding and a document's
+    partial last block are never scored.  A batch holds the documents of one routing
+    geometry and one power-of-two length class, which bounds the padding to 2x.
+    """
+    segments = packed_queries(q, k, cu_seqlens, query_offset)
+    nblocks = [(ke - ks + block_size - 1) // block_size for _, _, ks, ke, _ in segments]
+    shared = (routing_geometry(max(nblocks), topk, branching) if routing_schedule == "fused"
+              else None)
+    classes = {}
+    for index, ((qs, qe, ks, ke, _), nb) in enumerate(zip(segments, nblocks)):
+        geometry = shared or routing_geometry(nb, topk, branching)
+        size = 1 << max(0, ke - ks - 1).bit_length()
+        classes.setdefault((geometry, size), []).append(index)
+    out = torch.empty((1, q.shape[1], k.shape[2], topk), device=q.device, dtype=torch.long)
+    dev = q.device
+    for (geometry, _), members in classes.items():
+        qs, qe, ks, ke, offsets = (torch.tensor(col, device=dev, dtype=torch.long)
+                                   for col in zip(*(segments[i] for i in members)))
+        # rows of the padded batch (padding repeats the document's first row)
+        kj = torch.arange(int((ke - ks).max()), device=dev)[None]
+        qj = torch.arange(int((qe - qs).max()), device=dev)[None]
+        key_rows = ks[:, None] + torch.where(kj < (ke - ks)[:, None], kj, 0)
+        live = qj < (qe - qs)[:, None]
+        query_rows = qs[:, None] + torch.where(live, qj, 0)
+        ids = _select_unpacked(q[0][query_rows], k[0][key_rows], method, block_size, topk,
+                               offsets, force_first, force_recent, None, routing_schedule,
+                               geometry, branching)
+        out[0, query_rows[live]] = ids[live]
+    return out
 
 
 def _pyramid_desc(q, k, block_size, branching, top, pyramid):

@@ -234,3 +234,68 @@ def test_packed_fused_geometry_matches_oracle(P, method):
         print(f"document [{s}, {e}) ({alone} blocks, shared top {geometry[0]}): "
               f"{res['rows']} rows, {res['mismatched']} differ, {res['exempt']} tie-exempt")
         assert not res["failures"]
+
+
+@pytest.mark.parametrize("method,schedule", [("pisa", "auto"), ("pisa2", "grouped"),
+                                             ("pisa", "fused"), ("pisa1", "auto")])
+def test_packed_many_documents_batched(P, method, schedule):
+    """Forty documents of 1 to 1500 tokens: the packed call equals selecting each
+    document alone (its own depth, or the longest document's for fused routing), and
+    runs one launch series per (geometry, length class), not one per document."""
+    from nlogn_pisa_amd import _lib
+    print(f"packed many documents {method} {schedule}", flush=True)
+    rng = np.random.default_rng(14)
+    lengths = rng.integers(1, 1500, size=40).tolist()
+    lengths[3], lengths[7] = 1, 64                      # a one-token and a one-block document
+    bounds = np.concatenate([[0], np.cumsum(lengths)]).tolist()
+    q, k = structured_qkv(15, 1, bounds[-1], 8, 2, 64, "bf16", value=False)
+    qg, kg = to_gpu(q, "bf16"), to_gpu(k, "bf16")
+    cu = torch.tensor(bounds, dtype=torch.int64, device="cuda")
+    kw = dict(method=method, block_size=32, topk=8, force_recent=1, branching=4,
+              routing_schedule=schedule)
+    _lib.profile_begin()
+    out = P.select_blocks(qg, kg, cu_seqlens=cu, **kw)
+    launches = {n: c for n, (c, _) in _lib.profile_end().items()}
+    print("launches:", launches)
+    assert launches.get("route", 0) <= 16 < len(lengths)
+    fused = schedule == "fused" or (schedule == "auto" and method == "pisa1")
+    longest = max(-(-n // 32) for n in lengths)
+    geometry = O.routing_geometry(longest, 8, 4) if fused else None
+    for s, e in zip(bounds[:-1], bounds[1:]):
+        alone, _ = P.selection.select_blocks_traced(
+            qg[:, s:e], kg[:, s:e], method, 32, 8, force_recent=1, branching=4,
+            routing_schedule="fused" if fused else "grouped", geometry=geometry)
+        assert torch.equal(out[:, s:e], alone), f"document [{s}, {e})"
+
+
+def test_packed_decode_batched(P):
+    """One decode query per document (``validation.py:72-79``): fused routing with the
+    longest document's geometry (``top_k_pyramid.py:64-86``), all documents in one
+    batch; each document's ids against the oracle with that geometry."""
+    from nlogn_pisa_amd import _lib
+    bounds = [0, 900, 2000, 4096, 4100, 6000]
+    docs = list(zip(bounds[:-1], bounds[1:]))
+    q, k = structured_qkv(16, 1, bounds[-1], 8, 2, 64, "bf16", value=False)
+    qd = q[:, :len(docs)]
+    qg, kg = to_gpu(qd, "bf16"), to_gpu(k, "bf16")
+    cu = torch.tensor(bounds, dtype=torch.int32, device="cuda")
+    _lib.profile_begin()
+    out = P.select_blocks(qg, kg, "pisa", 64, 8, cu_seqlens=cu, force_recent=1,
+                          branching=2).cpu().numpy()
+    launches = {n: c for n, (c, _) in _lib.profile_end().items()}
+    assert launches.get("route", 0) <= 4          # length classes of 4, 1024, 2048, 4096 keys
+    geometry = O.routing_geometry(max(-(-(e - s) // 64) for s, e in docs), 8, 2)
+    for d, (s, e) in enumerate(docs):
+        pos = O.query_positions(1, 1, e - s)
+        levels = O.build_pyramid(k[:, s:e], 64, 2, None, "bf16")
+        want = O.pyramid_select(qd[:, d:d + 1], k[:, s:e], "pisa", 64, 8, pos, True, 1, levels,
+                                branching=2, geometry=geometry)
+        if not np.array_equal(out[:, d:d + 1], want):
+            ids, trace = P.selection.select_blocks_traced(
+                qg[:, d:d + 1], kg[:, s:e], "pisa", 64, 8, force_recent=1,
+                routing_schedule="fused", branching=2, geometry=geometry)
+            assert np.array_equal(out[:, d:d + 1], ids.cpu().numpy())
+            res = parity.selection_parity(qd[:, d:d + 1], k[:, s:e], ids.cpu().numpy(),
+                                          trace.cpu().numpy(), np.array([0]), "pisa", 64, 8,
+                                          True, 1, 2, levels, pos, geometry=geometry)
+            assert not res["failures"], f"document {d}"
