@@ -97,8 +97,27 @@ def _forward(q, k, v, indices, positions, block_size, scale, causal, keep_f32=Fa
     return out, lse, out32
 
 
+BACKWARD_DIMS = (16, 32, 64, 128)
+
+
+def _pad_dim(x, dim):
+    return x if x is None or x.shape[-1] == dim else torch.nn.functional.pad(x, (0, dim - x.shape[-1]))
+
+
 def _backward(q, k, v, indices, positions, out, out32, lse, grad_out, block_size, scale,
               causal, packed=None):
+    d, dv_ = q.shape[-1], v.shape[-1]
+    if (d, dv_) != (d, d) or d not in BACKWARD_DIMS:
+        # zero dimensions up to the next kernel head dim change no logit, probability or
+        # rowsum(dO O); their gradient columns are dropped
+        width = next((w for w in BACKWARD_DIMS if w >= max(d, dv_)), None)
+        if width is None:
+            raise ValueError("attention backward supports head dims up to 128")
+        padded = [_pad_dim(x, width).contiguous() if x is not None else None
+                  for x in (q, k, v, out, out32, grad_out)]
+        dq, dk, dv = _backward(padded[0], padded[1], padded[2], indices, positions, padded[3],
+                               padded[4], lse, padded[5], block_size, scale, causal, packed)
+        return dq[..., :d], dk[..., :d], dv[..., :dv_]
     desc = _attn_desc(q, k, v, indices, block_size, scale, causal, packed)
     lib = _lib.library()
     grad_out = grad_out.contiguous()
@@ -145,6 +164,27 @@ def _check(q, k, v, indices, block_size, backend):
         raise ValueError("invalid block_size or attention backend")
 
 
+# Largest key block the attention kernels stage (keys of a block in LDS).
+MAX_KERNEL_BLOCK = 128
+
+
+def split_blocks(indices, block_size):
+    """Ids of blocks over MAX_KERNEL_BLOCK keys as ids of their sub-blocks.
+
+    A block of C keys is f consecutive sub-blocks of C / f keys (the largest divisor
+    of C that is at most MAX_KERNEL_BLOCK); block j becomes sub-blocks j f .. j f + f - 1
+    and -1 stays -1.  The keys a row attends are the same set, so O, LSE and the
+    gradients are those of the original blocks.  Returns (ids, sub-block size).
+    """
+    if block_size <= MAX_KERNEL_BLOCK:
+        return indices, block_size
+    sub = max(d for d in range(1, MAX_KERNEL_BLOCK + 1) if block_size % d == 0)
+    f = block_size // sub
+    ids = indices.long()
+    parts = ids[..., None] * f + torch.arange(f, device=ids.device)
+    return torch.where(ids[..., None] >= 0, parts, torch.full_like(parts, -1)).flatten(-2), sub
+
+
 def _launch(q, k, v, indices, positions, block_size, scale, causal, packed=None):
     require_gpu(q, "sparse_attention")
     if q.dtype not in (torch.float16, torch.bfloat16, torch.float32):
@@ -159,6 +199,7 @@ def _launch(q, k, v, indices, positions, block_size, scale, causal, packed=None)
 
 
 def _unpacked(q, k, v, indices, block_size, scale, query_offset, causal):
+    indices, block_size = split_blocks(indices, block_size)
     return _launch(q, k, v, indices, query_positions(q, k, query_offset), block_size, scale,
                    causal)
 
@@ -167,6 +208,7 @@ def _packed(q, k, v, indices, block_size, scale, cu_seqlens, query_offset, causa
     """Every document of a packed batch in one launch sequence (``sparse_attn.py:29-54``
     semantics: document-local ids and positions, keys of the row's own document)."""
     require_gpu(q, "sparse_attention")
+    indices, block_size = split_blocks(indices, block_size)
     layout = PackedKeys(packed_queries(q, k, cu_seqlens, query_offset), q.shape[1], block_size,
                         q.device)
     return _launch(q, k, v, layout.block_ids(indices), layout.positions, block_size, scale,

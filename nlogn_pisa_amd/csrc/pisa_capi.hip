@@ -77,8 +77,8 @@ int plan_select(const pisa_qk_desc* qk, const pisa_select_params* p, SelectPlan&
   if (!p) return fail(PISA_ERR_INVALID, "null parameters");
   if (p->method < PISA_METHOD_PISA1 || p->method > PISA_METHOD_LSE)
     return fail(PISA_ERR_INVALID, "method must be pisa1, pisa2 or pisa");
-  if (!pow2(p->block_size) || p->block_size < 16 || p->block_size > 128)
-    return fail(PISA_ERR_UNSUPPORTED, "GPU routing requires a power-of-two block_size in [16, 128]");
+  if (!pow2(p->block_size) || p->block_size < 16 || p->block_size > 512)
+    return fail(PISA_ERR_UNSUPPORTED, "GPU routing requires a power-of-two block_size in [16, 512]");
   if (!pow2(p->branching) || p->branching < 2 || p->branching > 16)
     return fail(PISA_ERR_UNSUPPORTED, "branching must be a power of two in [2, 16]");
   if (p->topk < 1 || p->topk > 64) return fail(PISA_ERR_UNSUPPORTED, "topk must be in [1, 64]");
@@ -86,10 +86,10 @@ int plan_select(const pisa_qk_desc* qk, const pisa_select_params* p, SelectPlan&
   if (p->first_width < 1 || p->first_width > 512 || p->branching * p->topk > 512)
     return fail(PISA_ERR_UNSUPPORTED, "network width above 512");
   const int G = qk->query_heads / qk->key_heads;
-  if (G > 16) return fail(PISA_ERR_UNSUPPORTED, "routing supports up to 16 query heads per KV head");
+  if (G > 64) return fail(PISA_ERR_UNSUPPORTED, "routing supports up to 64 query heads per KV head");
   const int D = qk->head_dim;
-  if (D != 16 && D != 32 && D != 64 && D != 128)
-    return fail(PISA_ERR_UNSUPPORTED, "routing supports head_dim 16, 32, 64 or 128");
+  if (D % 16 || D > 256)
+    return fail(PISA_ERR_UNSUPPORTED, "routing supports head_dim a multiple of 16 up to 256");
   pl.G = G;
   pl.M0 = (qk->key_tokens + p->block_size - 1) / p->block_size;
   pl.items = (int64_t)qk->batch * qk->query_tokens * qk->key_heads;
@@ -117,7 +117,7 @@ int plan_select(const pisa_qk_desc* qk, const pisa_select_params* p, SelectPlan&
                              offsets, lengths);
     if (rc) return rc;
     for (int l = 1; l <= p->top && l < levels; ++l)
-      if (route_level_dense(G, l, p->top, p->first_width, p->branching, p->topk, lengths[l]))
+      if (route_level_dense(G, D, l, p->top, p->first_width, p->branching, p->topk, lengths[l]))
         pl.dense_nodes[l] = lengths[l];
   }
   return PISA_OK;

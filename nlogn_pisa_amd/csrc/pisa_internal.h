@@ -239,8 +239,8 @@ int launch_route(int dtype, const RouteArgs& a, int64_t items, int threads, hipS
 __host__ __device__ inline int64_t dense_stride(int nodes) { return (nodes + 63) / 64 * 64; }
 // Whether routing level `level` (>= 1) of the grouped schedule is scored densely
 // (every node for every item, route_dense_kernel) rather than per candidate.
-bool route_level_dense(int G, int level, int top, int first_width, int branching, int topk,
-                       int nodes);
+bool route_level_dense(int G, int head_dim, int level, int top, int first_width, int branching,
+                       int topk, int nodes);
 // Scores every node of dense level `level` for every item into a.dense[level].
 int launch_route_dense(int dtype, const RouteArgs& a, int level, hipStream_t stream);
 int launch_final(const FinalArgs& a, hipStream_t stream);

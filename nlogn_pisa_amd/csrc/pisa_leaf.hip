@@ -75,56 +75,75 @@ __global__ void __launch_bounds__(256) leaf_kernel(LeafArgs a) {
           qrow = static_cast<const T*>(a.q) + b * a.q_batch + t * a.q_token +
                  ((int64_t)h * a.G + gh) * a.D;
         }
-        f4 acc[8];
+        // keys in chunks of 8 tiles (128 keys); per C-layout row i the running
+        // statistics: log-sum-exp (max, sum of exponentials) or the two moment sums
+        float st0[4], st1[4];
 #pragma unroll
-        for (int nt = 0; nt < 8; ++nt) acc[nt] = f4{0.f, 0.f, 0.f, 0.f};
-        for (int k0 = 0; k0 < a.D; k0 += M::KS) {
-          typename M::frag fa;
-          if (qrow) {
-            fa = M::load(qrow + k0 + M::E * grp);
-          } else {
-            float z[4] = {0.f, 0.f, 0.f, 0.f};
-            fa = M::make(z);
+        for (int i = 0; i < 4; ++i) {
+          st0[i] = lse ? -INFINITY : 0.f;
+          st1[i] = 0.f;
+        }
+        for (int kc = 0; kc < NT; kc += 8) {
+          f4 acc[8];
+#pragma unroll
+          for (int nt = 0; nt < 8; ++nt) acc[nt] = f4{0.f, 0.f, 0.f, 0.f};
+          for (int k0 = 0; k0 < a.D; k0 += M::KS) {
+            typename M::frag fa;
+            if (qrow) {
+              fa = M::load(qrow + k0 + M::E * grp);
+            } else {
+              float z[4] = {0.f, 0.f, 0.f, 0.f};
+              fa = M::make(z);
+            }
+#pragma unroll
+            for (int nt = 0; nt < 8; ++nt) {
+              if (kc + nt < NT) {
+                const typename M::frag fb = M::load(ks + ((kc + nt) * 16 + col) * ldk + k0 + M::E * grp);
+                acc[nt] = M::mma(fa, fb, acc[nt]);
+              }
+            }
           }
 #pragma unroll
-          for (int nt = 0; nt < 8; ++nt) {
-            if (nt < NT) {
-              const typename M::frag fb = M::load(ks + (nt * 16 + col) * ldk + k0 + M::E * grp);
-              acc[nt] = M::mma(fa, fb, acc[nt]);
+          for (int i = 0; i < 4; ++i) {
+            if (pisa1) {
+              st0[i] = row_sum16(col == 0 ? acc[0][i] : 0.f);
+            } else if (lse) {
+              float m = -INFINITY;
+#pragma unroll
+              for (int nt = 0; nt < 8; ++nt)
+                if (kc + nt < NT && (kc + nt) * 16 + col < rows_valid) m = fmaxf(m, acc[nt][i] * a.scale);
+              m = fmaxf(row_max16(m), st0[i]);
+              float e = 0.f;
+#pragma unroll
+              for (int nt = 0; nt < 8; ++nt)
+                if (kc + nt < NT && (kc + nt) * 16 + col < rows_valid) e += __expf(acc[nt][i] * a.scale - m);
+              e = row_sum16(e);
+              st1[i] = (st0[i] == -INFINITY ? 0.f : st1[i] * __expf(st0[i] - m)) + e;
+              st0[i] = m;
+            } else {
+              float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+              for (int nt = 0; nt < 8; ++nt)
+                if (kc + nt < NT && (kc + nt) * 16 + col < rows_valid) {
+                  s1 += acc[nt][i];
+                  s2 = fmaf(acc[nt][i], acc[nt][i], s2);
+                }
+              st0[i] += row_sum16(s1);
+              st1[i] += row_sum16(s2);
             }
           }
         }
-        // per C-layout row i: reduce over the valid keys
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           float head;
           if (pisa1) {
-            head = row_sum16(col == 0 ? acc[0][i] : 0.f);
+            head = st0[i];
           } else if (lse) {
-            float m = -INFINITY;
-#pragma unroll
-            for (int nt = 0; nt < 8; ++nt)
-              if (nt < NT && nt * 16 + col < rows_valid) m = fmaxf(m, acc[nt][i] * a.scale);
-            m = row_max16(m);
-            float e = 0.f;
-#pragma unroll
-            for (int nt = 0; nt < 8; ++nt)
-              if (nt < NT && nt * 16 + col < rows_valid) e += __expf(acc[nt][i] * a.scale - m);
-            e = row_sum16(e);
-            head = m + __logf(e);
+            head = st0[i] + __logf(st1[i]);
           } else {
-            float s1 = 0.f, s2 = 0.f;
-#pragma unroll
-            for (int nt = 0; nt < 8; ++nt)
-              if (nt < NT && nt * 16 + col < rows_valid) {
-                s1 += acc[nt][i];
-                s2 = fmaf(acc[nt][i], acc[nt][i], s2);
-              }
-            s1 = row_sum16(s1);
-            s2 = row_sum16(s2);
             const float cnt = (float)rows_valid;
-            const float mean = s1 / cnt;
-            const float var = fmaxf(s2 / cnt - mean * mean, 0.f);
+            const float mean = st0[i] / cnt;
+            const float var = fmaxf(st1[i] / cnt - mean * mean, 0.f);
             head = a.scale * mean + (float)(0.5 * (double)a.scale * (double)a.scale) * var;
           }
           const int r = s * 16 + 4 * grp + i;
@@ -877,7 +896,7 @@ static void launch_leaf_tile_t(const LeafArgs& a, int cus, hipStream_t stream) {
 // The transposed-tile kernel serves D in {16, 32, 64, 128} with 16-byte aligned
 // query and key rows; other shapes take the general kernel.
 static bool leaf_tile_path(const LeafArgs& a, int es) {
-  const bool dim = a.D == 16 || a.D == 32 || a.D == 64 || a.D == 128;
+  const bool dim = (a.D == 16 || a.D == 32 || a.D == 64 || a.D == 128) && a.C <= 128;
   const bool ptrs = (((uintptr_t)a.q | (uintptr_t)a.src) & 15) == 0;
   const bool strides = ((a.q_batch | a.q_token | a.src_batch | a.src_row) * es) % 16 == 0;
   return dim && ptrs && strides;
@@ -888,7 +907,7 @@ int launch_leaf(int dtype, const LeafArgs& a, hipStream_t stream) {
   const int ldk = a.D + 16 / es;
   const size_t lds = (size_t)((a.C + 15) / 16 * 16) * ldk * es;
   if (a.D % 16 != 0 || a.D > 256) return fail(PISA_ERR_UNSUPPORTED, "leaf scoring needs head_dim % 16 == 0, <= 256");
-  if (a.C > 128) return fail(PISA_ERR_UNSUPPORTED, "leaf scoring supports block_size <= 128");
+  if (a.C > 512) return fail(PISA_ERR_UNSUPPORTED, "leaf scoring supports block_size <= 512");
   if (lds > (size_t)device_lds_limit())
     return fail(PISA_ERR_UNSUPPORTED, "key block of %zu bytes exceeds LDS", lds);
   if (a.span > 1 && a.C > 64 &&

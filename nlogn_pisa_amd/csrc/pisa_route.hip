@@ -146,6 +146,104 @@ __device__ float score_node(const RouteArgs& a, const float (&qr)[MAXG][CH], int
   return row_sum16(sub < G ? head : 0.f);
 }
 
+// score_node for shapes outside the register kernel: the item's query rows are
+// float rows [G][D] in LDS (any D = 16 ch <= 256, G <= kLdsHeads), lane `sub`
+// of a 16-lane group holds dimensions [sub ch, sub ch + ch) of a support row
+// and, for the support statistics, heads sub, sub + 16, ... .
+constexpr int kLdsHeads = 64;
+template <typename T>
+__device__ float score_node_lds(const RouteArgs& a, const float* qs, int b, int h, int id,
+                                int level, int sub) {
+  const int G = a.G, D = a.D, ch = D / 16;
+  const float* qlane = qs + sub * ch;
+  auto load_row = [&](const T* row, float (&x)[16]) {
+#pragma unroll
+    for (int c = 0; c < 16; ++c) x[c] = c < ch ? to_f(row[sub * ch + c]) : 0.f;
+  };
+  auto dot = [&](int g, const float (&x)[16]) {
+    float p = 0.f;
+#pragma unroll
+    for (int c = 0; c < 16; ++c)
+      if (c < ch) p = fmaf(qlane[g * D + c], x[c], p);
+    return row_sum16(p);
+  };
+  if (a.method == PISA_METHOD_PISA1) {
+    float x[16];
+    load_row(static_cast<const T*>(a.summary) + b * a.sum_batch +
+                 ((int64_t)(a.offsets[level] + id) * a.Hkv + h) * D, x);
+    float tot = 0.f;
+    for (int g = 0; g < G; ++g) tot += dot(g, x);
+    return tot;
+  }
+  const T* src;
+  int64_t stride;
+  int rows, support;
+  if (level > 0) {
+    support = a.branching;
+    src = static_cast<const T*>(a.summary) + b * a.sum_batch +
+          ((int64_t)(a.offsets[level - 1] + (int64_t)id * a.branching) * a.Hkv + h) * D;
+    stride = (int64_t)a.Hkv * D;
+    rows = min(support, a.lengths[level - 1] - id * a.branching);
+  } else {
+    support = a.C;
+    src = static_cast<const T*>(a.key) + b * a.key_batch + (int64_t)id * a.C * a.key_token +
+          (int64_t)h * D;
+    stride = a.key_token;
+    rows = (int)min((int64_t)a.C, (int64_t)a.N - (int64_t)id * a.C);
+  }
+  const bool lse = a.method == PISA_METHOD_LSE;
+  const bool binary = !lse && support == 2;
+  constexpr int NH = kLdsHeads / 16;  // heads per lane: sub + 16 j
+  float acc0[NH], acc1[NH];
+#pragma unroll
+  for (int j = 0; j < NH; ++j) {
+    acc0[j] = lse ? -INFINITY : 0.f;
+    acc1[j] = 0.f;
+  }
+  for (int r = 0; r < rows; ++r) {
+    float x[16];
+    load_row(src + (int64_t)r * stride, x);
+#pragma unroll
+    for (int j = 0; j < NH; ++j) {
+      float v = 0.f;
+      for (int g = 16 * j; g < min(G, 16 * j + 16); ++g) {
+        const float p = dot(g, x);
+        v = (g == sub + 16 * j) ? p : v;
+      }
+      if (lse) {
+        const float z = v * a.scale;
+        const float m = fmaxf(acc0[j], z);
+        acc1[j] = acc1[j] * __expf(acc0[j] - m) + __expf(z - m);
+        acc0[j] = m;
+      } else if (binary) {
+        const float z = v * a.scale;
+        if (r == 0) acc0[j] = z; else acc1[j] = z;
+      } else {
+        acc0[j] += v;
+        acc1[j] = fmaf(v, v, acc1[j]);
+      }
+    }
+  }
+  float total = 0.f;
+#pragma unroll
+  for (int j = 0; j < NH; ++j) {
+    float head;
+    if (lse) {
+      head = acc0[j] + __logf(acc1[j]);
+    } else if (binary) {
+      const float d = acc0[j] - acc1[j];
+      head = rows == 2 ? 0.5f * (acc0[j] + acc1[j]) + 0.125f * d * d : acc0[j];
+    } else {
+      const float count = (float)max(rows, 1);
+      const float mean = acc0[j] / count;
+      const float var = fmaxf(acc1[j] / count - mean * mean, 0.f);
+      head = a.scale * mean + (float)(0.5 * (double)a.scale * (double)a.scale) * var;
+    }
+    total += sub + 16 * j < G ? head : 0.f;
+  }
+  return row_sum16(total);
+}
+
 // Leaf score of candidate block `id` for the fused schedule, one wave on the
 // matrix cores (the leaf_tile_kernel formulation for a single request):
 // S^T = K Q^T per 16 keys (A = the block's key rows gathered from memory in the
@@ -284,8 +382,11 @@ __device__ void leaf_scores_mfma(const RouteArgs& a, const typename QkShape<T, H
   }
 }
 
-template <typename T, int CH, int MAXG>
+// QLDS: the query rows live in LDS (score_node_lds: wide head groups, head dims
+// other than 16/32/64/128, blocks over 128 keys); otherwise in registers.
+template <typename T, int CH, int MAXG, bool QLDS = false>
 __global__ void __launch_bounds__(512) route_kernel(RouteArgs a) {
+  extern __shared__ __attribute__((aligned(16))) float qsm[];  // QLDS: [G][D]
   __shared__ int ids_s[kMaxWidth];
   __shared__ float sc_s[kMaxWidth];
   __shared__ int list_s[kMaxWidth];
@@ -304,8 +405,11 @@ __global__ void __launch_bounds__(512) route_kernel(RouteArgs a) {
   const int K = a.topk;
   const int levels_traced = a.top + 1;
 
-  float qr[MAXG][CH];
-  {
+  float qr[QLDS ? 1 : MAXG][CH];
+  if constexpr (QLDS) {
+    const T* qp = static_cast<const T*>(a.q) + b * a.q_batch + t * a.q_token + (int64_t)h * a.G * a.D;
+    for (int i = tid; i < a.G * a.D; i += nthr) qsm[i] = to_f(qp[i]);  // used past the next barrier
+  } else {
     const T* qp = static_cast<const T*>(a.q) + b * a.q_batch + t * a.q_token +
                   (int64_t)h * a.G * a.D + sub * CH;
 #pragma unroll
@@ -357,8 +461,8 @@ __global__ void __launch_bounds__(512) route_kernel(RouteArgs a) {
     const int nlist = cnt_s[1];
     // the leaf level of pisa / pisa2 on the matrix cores: a wave per candidate
     constexpr int HD = 16 * CH;
-    constexpr bool kMfmaLeaf = sizeof(T) == 2 && HD >= 32 && MAXG <= 16;
-    if (kMfmaLeaf && level == 0 && a.method != PISA_METHOD_PISA1) {
+    constexpr bool kMfmaLeaf = !QLDS && sizeof(T) == 2 && HD >= 32 && MAXG <= 16;
+    if (kMfmaLeaf && level == 0 && a.method != PISA_METHOD_PISA1 && a.C <= 128) {
       typedef QkShape<T, HD> Sh;
       typename Sh::frag qb[Sh::DS];
       const int col = lane & 15, grp = lane >> 4;
@@ -377,7 +481,9 @@ __global__ void __launch_bounds__(512) route_kernel(RouteArgs a) {
     } else {
       for (int i = rgrp; i < nlist; i += nrgrp) {
         const int e = list_s[i];
-        const float s = score_node<T, CH, MAXG>(a, qr, b, h, ids_s[e], level, sub);
+        float s;
+        if constexpr (QLDS) s = score_node_lds<T>(a, qsm, b, h, ids_s[e], level, sub);
+        else s = score_node<T, CH, MAXG>(a, qr, b, h, ids_s[e], level, sub);
         if (sub == 0) sc_s[e] = s;
       }
     }
@@ -1140,6 +1246,21 @@ __global__ void __launch_bounds__(256) scoreable_kernel(MaskArgs a) {
 
 // ------------------------------------------------------------------ launchers
 
+// Query rows in LDS: any head dim that is a multiple of 16 up to 256 and head
+// groups up to kLdsHeads.
+template <typename T>
+static int launch_route_lds(const RouteArgs& a, int64_t items, int threads, hipStream_t stream) {
+  if (a.D % 16 || a.D > 256 || a.G > kLdsHeads)
+    return fail(PISA_ERR_UNSUPPORTED,
+                "routing supports head_dim % 16 == 0 up to 256 and up to %d query heads per kv head",
+                kLdsHeads);
+  const size_t lds = (size_t)a.G * a.D * sizeof(float);
+  const void* kernel = (const void*)route_kernel<T, 1, 1, true>;
+  allow_lds(kernel, lds);
+  PISA_TIMED("route", stream, hipLaunchKernelGGL((route_kernel<T, 1, 1, true>), dim3(items), dim3(threads), lds, stream, a));
+  return check_launch("route");
+}
+
 template <typename T, int CH>
 static int launch_route_ch(const RouteArgs& a, int64_t items, int threads, hipStream_t stream) {
   if (a.G <= 4)
@@ -1147,7 +1268,7 @@ static int launch_route_ch(const RouteArgs& a, int64_t items, int threads, hipSt
   else if (a.G <= 16)
     PISA_TIMED("route", stream, hipLaunchKernelGGL((route_kernel<T, CH, 16>), dim3(items), dim3(threads), 0, stream, a));
   else
-    return fail(PISA_ERR_UNSUPPORTED, "routing supports up to 16 query heads per kv head (got %d)", a.G);
+    return launch_route_lds<T>(a, items, threads, stream);
   return check_launch("route");
 }
 
@@ -1158,7 +1279,7 @@ static int launch_route_t(const RouteArgs& a, int64_t items, int threads, hipStr
     case 32: return launch_route_ch<T, 2>(a, items, threads, stream);
     case 64: return launch_route_ch<T, 4>(a, items, threads, stream);
     case 128: return launch_route_ch<T, 8>(a, items, threads, stream);
-    default: return fail(PISA_ERR_UNSUPPORTED, "routing supports head_dim 16/32/64/128 (got %d)", a.D);
+    default: return launch_route_lds<T>(a, items, threads, stream);
   }
 }
 
@@ -1223,7 +1344,7 @@ static bool route_mfma_path(const RouteArgs& a, int64_t items, int es) {
   const bool base = dim && a.G <= 16 && a.branching <= 8 && ptrs && strides;
   if (!a.fused) return base;
   const bool keys = ((uintptr_t)a.key & 15) == 0 && ((a.key_batch | a.key_token) * es) % 16 == 0;
-  const bool leaf = a.method == PISA_METHOD_PISA1 || (es == 2 && a.D >= 32 && keys);
+  const bool leaf = a.method == PISA_METHOD_PISA1 || (es == 2 && a.D >= 32 && a.C <= 128 && keys);
   return base && leaf && items >= kFusedWaveItems;
 }
 
@@ -1260,10 +1381,11 @@ int launch_route(int dtype, const RouteArgs& a, int64_t items, int threads, hipS
 // rows outweighs the saving (measured), so dense levels need P >= 2; a wave's
 // 4 P items fit its 16 staging rows for P <= 4, i.e. Gp in {4, 8}.
 constexpr int kDenseFactor = 16;
-bool route_level_dense(int G, int level, int top, int first_width, int branching, int topk,
-                       int nodes) {
+bool route_level_dense(int G, int head_dim, int level, int top, int first_width, int branching,
+                       int topk, int nodes) {
   const int gp = next_pow2(G);
-  if (level < 1 || level > top || gp < 4 || gp > 8 || branching > 8) return false;
+  const bool mfma_dim = head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128;
+  if (!mfma_dim || level < 1 || level > top || gp < 4 || gp > 8 || branching > 8) return false;
   const int width = level == top ? first_width : branching * topk;
   return (int64_t)nodes <= (int64_t)(kDenseFactor / gp) * width;
 }

@@ -174,8 +174,8 @@ def _select_params(method, block_size, branching, topk, force_first, force_recen
 def _check_gpu_shape(q, k, block_size, topk, branching, force_first, force_recent):
     if q.dtype not in (torch.float16, torch.bfloat16, torch.float32):
         raise ValueError("GPU routing supports FP16, BF16 and FP32")
-    if block_size & (block_size - 1) or not 16 <= block_size <= 128 or not 1 <= topk <= 64:
-        raise ValueError("GPU routing requires power-of-two block_size in [16, 128] and "
+    if block_size & (block_size - 1) or not 16 <= block_size <= 512 or not 1 <= topk <= 64:
+        raise ValueError("GPU routing requires power-of-two block_size >= 16 (up to 512) and "
                          "topk in [1, 64]")
     if branching * topk > 512:
         raise ValueError("branching * topk must not exceed 512")

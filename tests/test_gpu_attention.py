@@ -76,6 +76,12 @@ CASES = [
     # (the online merge), G = 3 above takes the online merge too
     ("bf16-g16-k16", 1, 300, 1024, 16, 1, 64, 32, 16, "bf16", True, None),
     ("bf16-g16-k17", 1, 300, 1024, 16, 1, 64, 32, 17, "bf16", True, None),
+    # blocks over 128 keys run as their 128-key halves; head dim 96 (forward on the general
+    # kernels, backward on zero-padded 128-wide rows); 32 query heads per kv head
+    ("bf16-c256", 1, 700, 1500, 8, 2, 64, 256, 4, "bf16", True, None),
+    ("fp32-c512-d32", 1, 300, 2100, 4, 2, 32, 512, 3, "fp32", True, None),
+    ("bf16-d96", 1, 400, 400, 8, 2, 96, 64, 4, "bf16", True, None),
+    ("bf16-g32", 1, 256, 512, 64, 2, 64, 64, 4, "bf16", True, None),
 ]
 
 

@@ -126,6 +126,17 @@ CONFIGS = [
     # (at least 16384 (token, kv head) items, where pairs are used)
     ("c128-pisa2-ragged", 1, 9072, 8, 2, 128, 128, 4, 8, "pisa2", True, 1, "bf16", 0.0, None),
     ("c128-lse-fp16-d64", 2, 5048, 16, 2, 64, 128, 2, 8, "pisa", True, 2, "fp16", 0.0, None),
+    # shapes outside the fast kernels (top_k_pyramid_triton.py:327-335, :362 pads any head
+    # dim and head group): blocks of 256 keys (the leaf in 128-key chunks), head dims 96 and
+    # 256 and 32 query heads per kv head (query rows in LDS)
+    ("c256", 1, 9000, 8, 2, 64, 256, 4, 8, "pisa", True, 1, "bf16", 0.0, None),
+    ("c256-pisa2-fp32", 1, 6000, 4, 2, 32, 256, 2, 8, "pisa2", True, 2, "fp32", 0.0, None),
+    ("d96", 1, 4096, 8, 2, 96, 64, 4, 8, "pisa2", True, 2, "bf16", 0.01, None),
+    ("d96-lse-fp16", 1, 3000, 4, 1, 96, 32, 2, 8, "pisa", True, 1, "fp16", 0.0, None),
+    ("d256", 1, 2048, 8, 2, 256, 64, 2, 8, "pisa", True, 1, "bf16", 0.0, None),
+    ("g32", 1, 2048, 64, 2, 64, 64, 4, 8, "pisa", True, 1, "bf16", 0.0, None),
+    ("g32-pisa2-d128", 1, 2048, 64, 2, 128, 32, 2, 16, "pisa2", True, 2, "bf16", 0.0, None),
+    ("g24-pisa1", 1, 1500, 48, 2, 64, 64, 2, 8, "pisa1", True, 1, "bf16", 0.0, None),
 ]
 
 
