@@ -108,8 +108,9 @@ __device__ void stage_kv(const AttnArgs& a, int b, int h, int64_t blk, int rows,
 }
 
 // One 16-row unit: rows unit*16 .. +15 of the request list (row = request x Gp + head).
-// P enters the P V product as a pair of 16-bit values hi + lo (lo = P - hi),
-// so the product keeps ~16 significant bits of P; fp32 needs no split.
+// In the general kernels and the backward, P (and dS) enter their products as a
+// pair of 16-bit values hi + lo (lo = P - hi), keeping ~16 significant bits; the
+// forward tile kernel rounds P once, as the reference does.  fp32 needs no split.
 template <typename T>
 constexpr bool kSplit = sizeof(T) == 2;
 
@@ -569,27 +570,25 @@ __device__ void fwd_tile_units(const AttnArgs& a, const TileLds& L, const T* ks,
       }
     }
     l = xor32_sum(xor16_sum(l));
-    // O^T = V^T P^T, P entering as hi + lo for 16-bit types
+    // O^T = V^T P^T, P rounded once to the input type as the reference's kernels do
+    // (P.to(v.dtype) @ V); the statistics m, l stay in float32
     f4 o[NDT];
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) o[dt] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < S::MAXK; ++kk) {
       if (kk < NK) {
-        frag ph, pl;
+        frag ph;
 #pragma unroll
         for (int e = 0; e < E; ++e) {
           const int lam = kk * E + e;
-          const float x = s[lam >> 2][lam & 3];
-          const float r = Op::set(ph, e, x);
-          if constexpr (kSplit<T>) Op::set(pl, e, x - r);
+          Op::set(ph, e, s[lam >> 2][lam & 3]);
         }
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
           const T* vrow = vt + (16 * dt + col) * L.ldv;  // vt_row of this lane's A row
           const frag vf = load_vt<T, E>(vrow, kk, grp);
           o[dt] = Op::mma(vf, ph, o[dt]);
-          if constexpr (kSplit<T>) o[dt] = Op::mma(vf, pl, o[dt]);
         }
       }
     }
