@@ -55,6 +55,11 @@ __device__ __forceinline__ bool slot_visible(const AttnArgs& a, int64_t blk, int
   return blk >= 0 && blk < a.M0 && (!a.causal || blk * a.C <= pos);
 }
 
+// A slot whose partial the combine merges: a visible one.
+__device__ __forceinline__ bool slot_active(const AttnArgs& a, int64_t slot, int64_t pos) {
+  return slot_visible(a, slot_block(a, slot), pos);
+}
+
 // Row bookkeeping of one request slot.
 struct RowInfo {
   int64_t slot;
@@ -820,9 +825,8 @@ __global__ void __launch_bounds__(256) attn_combine2_kernel(AttnArgs a, int64_t 
   for (int j = 0; j < kCombinePairs / 64; ++j) {
     const int idx = lane + 64 * j;
     const int ic = min(idx, pairs - 1);  // every lane loads; pairs past the row are masked
-    const int64_t blk = slot_block(a, slot0 + (ic >> gl));
     lse[j] = stream_load(a.part_lse + slot0 * G + ic);
-    vis[j] = idx < pairs && slot_visible(a, blk, ri.pos);
+    vis[j] = idx < pairs && slot_active(a, slot0 + (ic >> gl), ri.pos);
     if (vis[j]) m = fmaxf(m, lse[j]);
   }
   for (int off = G; off < 64; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
@@ -850,22 +854,30 @@ __global__ void __launch_bounds__(256) attn_combine2_kernel(AttnArgs a, int64_t 
     for (int v = 0; v < V; ++v) acc[v] = 0.f;
     for (int s0 = 0; s0 < a.K; s0 += 64) {
       const int n = min(64, a.K - s0);
-      const bool vis_l = lane < n && slot_visible(a, slot_block(a, slot0 + s0 + lane), ri.pos);
-      const uint64_t vmask = __ballot(vis_l);
-      for (int s = 0; s < n; s += U) {
+      uint64_t rest = __ballot(lane < n && slot_active(a, slot0 + s0 + lane, ri.pos));
+      // the active slots in slot order, U partial chunks in flight
+      while (rest) {
+        int sl[U];
+        bool on[U];
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+          on[j] = rest != 0;
+          sl[j] = on[j] ? __ffsll((long long)rest) - 1 : sl[0];
+          rest &= rest - 1;
+        }
         union {
           uint4 u;
           PT e[V];
         } x[U];
 #pragma unroll
         for (int j = 0; j < U; ++j) {
-          const int64_t row = (slot0 + s0 + min(s + j, n - 1)) * G + g;
+          const int64_t row = (slot0 + s0 + sl[j]) * G + g;
           x[j].u = stream_load16(part + row * a.Dv + c * V);
         }
 #pragma unroll
         for (int j = 0; j < U; ++j) {
-          if (s + j < n && ((vmask >> (s + j)) & 1)) {
-            const float w = wl[(s0 + s + j) * G + g];
+          if (on[j]) {
+            const float w = wl[(s0 + sl[j]) * G + g];
 #pragma unroll
             for (int v = 0; v < V; ++v) acc[v] = fmaf(w, (float)x[j].e[v], acc[v]);
           }
