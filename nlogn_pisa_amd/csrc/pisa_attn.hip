@@ -1134,7 +1134,7 @@ __global__ void __launch_bounds__(512) attn_bwd_grouped_kernel(AttnArgs a) {
         for (int i = 0; i < 4; ++i) {
           const int r = 4 * grp + i;
           if (rslot[r] >= 0)
-            a.part_dq[(rslot[r] * a.G + rgh[r]) * HD + dt * 16 + col] = q[i] * a.scale;
+            static_cast<float*>(a.part_dq)[(rslot[r] * a.G + rgh[r]) * HD + dt * 16 + col] = q[i] * a.scale;
         }
       }
     }
@@ -1275,6 +1275,177 @@ __global__ void __launch_bounds__(256) attn_dq_combine_kernel(AttnArgs a, int64_
         o[1] = from_f<T>(acc[j].y);
         o[2] = from_f<T>(acc[j].z);
         o[3] = from_f<T>(acc[j].w);
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ compact dQ partials
+//
+// The 16-bit register-tile backward kernels store each (row, slot) dQ partial
+// as fp16 values with one power-of-two exponent per group of 8 consecutive
+// values (int8, row order: values 8 f .. 8 f + 7 of a row take its byte f):
+// the group's values are multiplied by 2^s before rounding, s chosen so that
+// its largest magnitude m lands in [2^14, 2^15].  Rounding to fp16's 11-bit
+// significand then costs at most 2^-11 relative per value (down to 2^-28 m,
+// where fp16 turns subnormal), the scaling is exact both ways, and a partial
+// takes 2 D + D / 8 bytes instead of 4 D.  Infinities and NaNs are left out of
+// m and pass through.
+//
+// A dQ^T tile leaves 4 values of a row per lane (d = 16 dt + 4 grp + i).  When
+// a wave owns an even number of tiles, tiles 2p and 2p + 1 take the K^T rows
+// of their A operand interleaved in fours (dq_tile_row), so a lane holds the 8
+// consecutive values d = 32 p + 8 grp .. + 7 and writes one 16-byte piece
+// (64 bytes per row across its 4 lanes, as the fp32 form writes) and one byte.
+// With one tile per wave the lane pair grp, grp ^ 1 shares a group.
+
+// The K^T row (head-dim index) that A row `col` of dQ^T tile dt takes.
+template <int NQ>
+__device__ __forceinline__ int dq_tile_row(int dt, int col) {
+  if constexpr (NQ % 2 == 0) return 32 * (dt >> 1) + 8 * (col >> 2) + 4 * (dt & 1) + (col & 3);
+  else return 16 * dt + col;
+}
+
+// Largest magnitude of the finite values among n (v_max drops NaNs; an
+// infinity sends it to the slow path).
+template <int N>
+__device__ __forceinline__ float dq_group_max(const float (&v)[N]) {
+  float m = 0.f;
+#pragma unroll
+  for (int i = 0; i < N; ++i) m = fmaxf(m, fabsf(v[i]));
+  if (!(m <= 3.402823466e38f)) {
+    m = 0.f;
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      if (fabsf(v[i]) <= 3.402823466e38f) m = fmaxf(m, fabsf(v[i]));
+  }
+  return m;
+}
+
+// Shift of a group whose largest magnitude (before the softmax scale) is m, and
+// the exact multiplier scale 2^s: x (scale 2^s) is x scale rounded once, times 2^s.
+__device__ __forceinline__ int dq_group_shift(float m, float scale, float& mult) {
+  // m scale = f 2^e with f in [0.5, 1) (e = 0 for 0): s = 14 - (e - 1)
+  const int s = min(127, 15 - __builtin_amdgcn_frexp_expf(m * scale));
+  mult = __builtin_amdgcn_ldexpf(scale, s);
+  return s;
+}
+
+__device__ __forceinline__ uint32_t pack_h2(float x, float y) {
+  typedef float f2v __attribute__((ext_vector_type(2)));
+  typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2v){x, y}, h2v));
+}
+
+// A wave's dQ^T tiles first .. first + NQ - 1 (first even when NQ is) of the
+// compact partial row `prow` (row = slot x G + head) at head dim HD, lane col's
+// row.  Every lane calls it; lanes whose row is a request (`ok`) store.
+template <int NQ>
+__device__ __forceinline__ void store_dq_row(const AttnArgs& a, int64_t prow, int HD, int first, int grp,
+                                             const f4 (&dq)[NQ], bool ok) {
+  uint16_t* row = static_cast<uint16_t*>(a.part_dq) + prow * HD;
+  int8_t* ex = a.part_dq_exp + prow * (HD / 8);
+  if constexpr (NQ % 2 == 0) {
+    if (ok) {
+#pragma unroll
+      for (int t = 0; t < NQ; t += 2) {
+        const float v[8] = {dq[t][0], dq[t][1], dq[t][2], dq[t][3],
+                            dq[t + 1][0], dq[t + 1][1], dq[t + 1][2], dq[t + 1][3]};
+        float mult;
+        const int s = dq_group_shift(dq_group_max(v), a.scale, mult);
+        const int p = (first + t) >> 1;
+        stream_store16(row + 32 * p + 8 * grp,
+                       make_uint4(pack_h2(v[0] * mult, v[1] * mult), pack_h2(v[2] * mult, v[3] * mult),
+                                  pack_h2(v[4] * mult, v[5] * mult), pack_h2(v[6] * mult, v[7] * mult)));
+        ex[4 * p + grp] = (int8_t)s;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < NQ; ++t) {
+      const float v[4] = {dq[t][0], dq[t][1], dq[t][2], dq[t][3]};
+      float mult;
+      const int s = dq_group_shift(xor16_max(dq_group_max(v)), a.scale, mult);  // with lane grp ^ 1
+      if (ok) {
+        const int dt = first + t;
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 w = {pack_h2(v[0] * mult, v[1] * mult), pack_h2(v[2] * mult, v[3] * mult)};
+        __builtin_nontemporal_store(w, reinterpret_cast<u32x2*>(row + 16 * dt + 4 * grp));
+        if (!(grp & 1)) ex[2 * dt + (grp >> 1)] = (int8_t)s;
+      }
+    }
+  }
+}
+
+// dQ = the sum of a row's compact partials over its visible slots, one wave per
+// (batch, token, kv head) item: 16-byte chunks of 8 values (one exponent
+// group), up to four slots' chunks in flight per lane.
+template <typename T>
+__global__ void __launch_bounds__(256) attn_dq_combine_compact_kernel(AttnArgs a, int64_t items) {
+  const int lane = threadIdx.x & 63;
+  const int64_t item = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (item >= items) return;
+  const RowInfo ri = row_info(a, item * a.K);
+  const int chunks = a.G * a.D / 8;
+  const uint16_t* part = static_cast<const uint16_t*>(a.part_dq);
+  T* out = static_cast<T*>(a.dq) + item * a.G * a.D;
+  for (int c0 = 0; c0 < chunks; c0 += 128) {
+    float acc[2][8];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[j][e] = 0.f;
+    for (int s0 = 0; s0 < a.K; s0 += 64) {
+      const int sl = s0 + lane;
+      const bool vis = sl < a.K && slot_visible(a, slot_block(a, item * a.K + sl), ri.pos);
+      uint64_t mask = __ballot(vis);
+      while (mask) {
+        int64_t sidx[4];
+        int cnt = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          sidx[k] = -1;
+          if (mask) {
+            const int bit = __ffsll((unsigned long long)mask) - 1;
+            mask &= mask - 1;
+            sidx[k] = item * a.K + s0 + bit;
+            ++cnt;
+          }
+        }
+        uint4 hv[4][2];
+        int sh[4][2];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const int c = c0 + lane + 64 * j;
+            hv[k][j] = make_uint4(0u, 0u, 0u, 0u);
+            sh[k][j] = 0;
+            if (k < cnt && c < chunks) {
+              hv[k][j] = stream_load16(part + (sidx[k] * chunks + c) * 8);
+              sh[k][j] = a.part_dq_exp[sidx[k] * chunks + c];  // the chunk is one group
+            }
+          }
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const uint32_t w4[4] = {hv[k][j].x, hv[k][j].y, hv[k][j].z, hv[k][j].w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)(w4[e >> 1] >> (16 * (e & 1))));
+              acc[j][e] += __builtin_amdgcn_ldexpf((float)h, -sh[k][j]);
+            }
+          }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int c = c0 + lane + 64 * j;
+      if (c < chunks) {
+        T* o = out + 8 * c;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = from_f<T>(acc[j][e]);
       }
     }
   }
@@ -1511,22 +1682,16 @@ __global__ void __launch_bounds__(64 * W, W == 4 ? 2 : 1) attn_bwd_tile_kernel(A
 #pragma unroll
         for (int t = 0; t < NQ; ++t) {
           const int dt = w * NQ + t;
-          const uint2 k4 = *reinterpret_cast<const uint2*>(kt + (16 * dt + col) * L.ldt + 16 * m + 4 * grp);
+          const uint2 k4 = *reinterpret_cast<const uint2*>(kt + dq_tile_row<NQ>(dt, col) * L.ldt + 16 * m + 4 * grp);
           dq[t] = Op::mma(as_frag<frag>(make_uint4(k4.x, k4.y, k4.x, k4.y)), db, dq[t]);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
       // dQ^T tile dt holds d = 16 dt + 4 grp + i of row `col` (K^T rows are
-      // d): a wave writes whole 64-byte runs of the row, its d in one piece
+      // d): a wave writes the compact runs w NQ .. w NQ + NQ - 1 of the row
       const int rho = (u << 4) + col, rq = rho >> gl, gh = rho & (Gp - 1);
-      if (rq < nreq && gh < a.G) {
-        float* dst = a.part_dq + ((int64_t)mslot[rq] * a.G + gh) * HD + 4 * grp;
-#pragma unroll
-        for (int t = 0; t < NQ; ++t)
-          stream_store_f4(dst + 16 * (w * NQ + t),
-                          make_float4(dq[t][0] * a.scale, dq[t][1] * a.scale, dq[t][2] * a.scale,
-                                      dq[t][3] * a.scale));
-      }
+      const bool ok = rq < nreq && gh < a.G;
+      store_dq_row<NQ>(a, ok ? (int64_t)mslot[rq] * a.G + gh : 0, HD, w * NQ, grp, dq, ok);
     };
     Rows buf[2];
     fetch(0, buf[0]);
@@ -1778,19 +1943,13 @@ __global__ void __launch_bounds__(256, NT <= 4 ? 2 : 1) attn_bwd_share_kernel(At
 #pragma unroll
         for (int t = 0; t < NQ; ++t) {
           const int dt = w * NQ + t;
-          const uint2 k4 = *reinterpret_cast<const uint2*>(kt + (16 * dt + col) * L.ldt + 16 * m + 4 * grp);
+          const uint2 k4 = *reinterpret_cast<const uint2*>(kt + dq_tile_row<NQ>(dt, col) * L.ldt + 16 * m + 4 * grp);
           dq[t] = Op::mma(as_frag<frag>(make_uint4(k4.x, k4.y, k4.x, k4.y)), db, dq[t]);
         }
       }
       const int rho = (u << 4) + col, rq = rho >> gl, gh = rho & (Gp - 1);
-      if (rq < nreq && gh < a.G) {
-        float* dst = a.part_dq + ((int64_t)mslot[rq] * a.G + gh) * HD + 4 * grp;
-#pragma unroll
-        for (int t = 0; t < NQ; ++t)
-          stream_store_f4(dst + 16 * (w * NQ + t),
-                          make_float4(dq[t][0] * a.scale, dq[t][1] * a.scale, dq[t][2] * a.scale,
-                                      dq[t][3] * a.scale));
-      }
+      const bool ok = rq < nreq && gh < a.G;
+      store_dq_row<NQ>(a, ok ? (int64_t)mslot[rq] * a.G + gh : 0, HD, w * NQ, grp, dq, ok);
       __syncthreads();  // the exchange is free and the next unit's rows are in LDS
     };
     typedef std::integral_constant<int, 0> P0;
@@ -1996,9 +2155,12 @@ static bool launch_bwd_tiles(const AttnArgs& a, hipStream_t stream) {
   }
 }
 
+// The register-tile kernels write compact dQ partials, the LDS-staged kernel
+// fp32 ones (it clears a.part_dq_exp for the combine).
 template <typename T, int HD>
-static void launch_bwd_kernel(const AttnArgs& a, hipStream_t stream) {
+static void launch_bwd_kernel(AttnArgs& a, hipStream_t stream) {
   if (tile_path(a) && launch_bwd_tiles<T, HD>(a, stream)) return;
+  a.part_dq_exp = nullptr;
   const int Cp = (a.C + 15) / 16 * 16;
   const size_t lds = bwd_lds(a, sizeof(T));
   allow_lds((const void*)attn_bwd_grouped_kernel<T, HD>, lds);
@@ -2007,7 +2169,8 @@ static void launch_bwd_kernel(const AttnArgs& a, hipStream_t stream) {
 }
 
 template <typename T>
-static int attn_bwd_t(const AttnArgs& a, int64_t groups, int64_t items, hipStream_t stream) {
+static int attn_bwd_t(const AttnArgs& args, int64_t groups, int64_t items, hipStream_t stream) {
+  AttnArgs a = args;
   const int64_t rows = items * a.G;
   if (rows > 0)
     PISA_TIMED("attn_delta", stream, hipLaunchKernelGGL(attn_delta_kernel<T>, dim3((rows + 3) / 4), dim3(256), 0, stream, a, rows));
@@ -2020,8 +2183,12 @@ static int attn_bwd_t(const AttnArgs& a, int64_t groups, int64_t items, hipStrea
   }
   if (groups > 0)
     PISA_TIMED("attn_dkv_reduce", stream, hipLaunchKernelGGL(attn_dkv_reduce_kernel<T>, dim3(groups), dim3(256), 0, stream, a, groups));
-  if (items > 0)
-    PISA_TIMED("attn_dq_combine", stream, hipLaunchKernelGGL(attn_dq_combine_kernel<T>, dim3((items + 3) / 4), dim3(256), 0, stream, a, items));
+  if (items > 0) {
+    if (a.part_dq_exp)
+      PISA_TIMED("attn_dq_combine", stream, hipLaunchKernelGGL(attn_dq_combine_compact_kernel<T>, dim3((items + 3) / 4), dim3(256), 0, stream, a, items));
+    else
+      PISA_TIMED("attn_dq_combine", stream, hipLaunchKernelGGL(attn_dq_combine_kernel<T>, dim3((items + 3) / 4), dim3(256), 0, stream, a, items));
+  }
   return check_launch("attention backward");
 }
 

@@ -489,7 +489,10 @@ void carve_attn(const pisa_attn_desc* d, const AttnPlan& pl, bool backward, Carv
     if (pl.grouped) carve_buckets(c, b, pl.window_slots, pl.groups, kAttnFwdTile);
   } else {
     a.delta = c.take<float>(pl.items * pl.G);
+    // room for fp32 dQ partials (the compact form takes the first half) and the
+    // compact form's exponents (one per 8 values)
     a.part_dq = c.take<float>(pl.slots * pl.G * d->head_dim);
+    a.part_dq_exp = c.take<int8_t>(pl.slots * pl.G * (d->head_dim / 8));
     carve_buckets(c, b, pl.slots, pl.groups, kAttnTile);
     a.part_dkv = c.take<float>(b.max_tiles * pl.Cp * (d->head_dim + d->value_dim));
   }

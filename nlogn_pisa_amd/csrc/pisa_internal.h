@@ -226,7 +226,10 @@ struct AttnArgs {
   const float* lse;
   const void* dout;
   float* delta;     // [B,T,Hq]
-  float* part_dq;   // [slots * G, D]
+  // dQ partials [slots * G, D]: fp32, or (part_dq_exp set) the compact fp16
+  // form with one int8 power-of-two exponent per 8 values [slots * G, D / 8]
+  void* part_dq;
+  int8_t* part_dq_exp;
   float* part_dkv;  // [tiles, Cp, D + Dv]
   void* dq;
   void* dk;

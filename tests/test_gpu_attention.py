@@ -129,9 +129,44 @@ def test_backward_matches_oracle(P, case):
     dq, dk, dv = O.sparse_attention_backward(q, k, v, idx, dout, block, positions=pos,
                                              causal=causal)
     for name_, mine, ref in (("dq", qg.grad, dq), ("dk", kg.grad, dk), ("dv", vg.grad, dv)):
-        err = excess_error(mine.float().cpu().numpy(), ref, dtype)
-        print(f"{name_} excess max-abs error {err:.3e}")
+        mine = mine.float().cpu().numpy()
+        err = excess_error(mine, ref, dtype)
+        print(f"{name_} max-abs error {np.abs(mine - ref).max():.3e}, "
+              f"beyond half an output ulp {err:.3e}")
         assert err <= TOL[dtype], f"{name_} max-abs error {err}"
+
+
+@pytest.mark.parametrize("case", [CASES[2], CASES[16]], ids=[CASES[2][0], CASES[16][0]])
+@pytest.mark.parametrize("shift", [20, -30])
+def test_backward_scales_exactly(P, case, shift):
+    """Gradients are linear in dO: scaling dO by 2^shift scales them by exactly
+    2^shift (bf16 keeps fp32's exponent range).  dQ, a slot-ordered sum of
+    per-request partials, must match bit for bit, which holds only if its
+    partials carry the scale through their exponents (no fp16 overflow at
+    2^20, none of fp16's subnormals at 2^-30).  dK and dV sum a tile's requests
+    in bucketing order, which varies between runs, so they are held to a
+    bf16-level bound.  Head dims 128 and 64 cover both register-tile backward
+    kernels."""
+    name, batch, tq, n, qh, kh, dim, block, topk, dtype, causal, offset = case
+    print(f"attention backward scale 2^{shift} {name}", flush=True)
+    q, k, v, idx = _inputs(case)
+    dout = np.random.default_rng(7).standard_normal((batch, tq, qh, dim)).astype(np.float32)
+    ids = torch.from_numpy(idx).cuda()
+
+    def grads(scale):
+        qg, kg, vg = (to_gpu(x, dtype).requires_grad_(True) for x in (q, k, v))
+        out = P.sparse_attention(qg, kg, vg, ids, block, query_offset=offset, causal=causal)
+        out.backward(to_gpu(dout, dtype) * scale)
+        return [g.grad.float() for g in (qg, kg, vg)]
+
+    base = grads(1.0)
+    scaled = grads(2.0 ** shift)
+    assert torch.equal(base[0] * 2.0 ** shift, scaled[0]), "dq is not scaled exactly"
+    for name_, a, b in zip(("dk", "dv"), base[1:], scaled[1:]):
+        a = a * 2.0 ** shift
+        err = ((a - b).abs().max() / a.abs().max()).item()
+        print(f"{name_} relative difference {err:.3e}")
+        assert err <= 2 ** -7, f"{name_} relative difference {err}"
 
 
 def test_selected_blocks_end_to_end(P):
