@@ -548,29 +548,67 @@ __device__ void fwd_tile_units(const AttnArgs& a, const TileLds& L, const T* ks,
       const int64_t last = a.causal ? mpos[rq] - blk * a.C + 1 : (int64_t)rows;  // keys <= pos
       lim = (int)min((int64_t)rows, last) - 4 * grp;
     }
-    float m = -INFINITY;
+    float m = -INFINITY, l = 0.f;
+    if (a.scale > 0.f) {
+      // The softmax in base 2 with the scale folded into one fma, c = scale
+      // log2(e): p = 2^(c s - c max s), m = scale max s.  Hidden keys enter as
+      // -inf; a wave whose existing rows all see every key of the block
+      // (padding rows are never stored) skips that masking, with the same
+      // arithmetic, so a row's result does not depend on its unit-mates.
+      float mx = -INFINITY;
+      if (__all(!valid || lim > 16 * NT - 13)) {
 #pragma unroll
-    for (int mt = 0; mt < NTM; ++mt) {
-      if (mt < NT) {
+        for (int mt = 0; mt < NTM; ++mt)
+          if (mt < NT)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float z = mt * 16 + i < lim ? s[mt][i] * a.scale : -INFINITY;
-          s[mt][i] = z;
-          m = fmaxf(m, z);
+            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[mt][i]);
+      } else {
+#pragma unroll
+        for (int mt = 0; mt < NTM; ++mt)
+          if (mt < NT)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float z = mt * 16 + i < lim ? s[mt][i] : -INFINITY;
+              s[mt][i] = z;
+              mx = fmaxf(mx, z);
+            }
+      }
+      mx = xor32_max(xor16_max(mx));
+      const float c = a.scale * 1.44269504088896340736f;
+      const float mc = mx == -INFINITY ? 0.f : mx * c;
+#pragma unroll
+      for (int mt = 0; mt < NTM; ++mt)
+        if (mt < NT)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float p = __builtin_amdgcn_exp2f(fmaf(s[mt][i], c, -mc));
+            s[mt][i] = p;
+            l += p;
+          }
+      m = mx * a.scale;
+    } else {
+#pragma unroll
+      for (int mt = 0; mt < NTM; ++mt) {
+        if (mt < NT) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float z = mt * 16 + i < lim ? s[mt][i] * a.scale : -INFINITY;
+            s[mt][i] = z;
+            m = fmaxf(m, z);
+          }
         }
       }
-    }
-    m = xor32_max(xor16_max(m));
-    const float safe = m == -INFINITY ? 0.f : m;
-    float l = 0.f;
+      m = xor32_max(xor16_max(m));
+      const float safe = m == -INFINITY ? 0.f : m;
 #pragma unroll
-    for (int mt = 0; mt < NTM; ++mt) {
-      if (mt < NT) {
+      for (int mt = 0; mt < NTM; ++mt) {
+        if (mt < NT) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float p = __expf(s[mt][i] - safe);
-          s[mt][i] = p;
-          l += p;
+          for (int i = 0; i < 4; ++i) {
+            const float p = __expf(s[mt][i] - safe);
+            s[mt][i] = p;
+            l += p;
+          }
         }
       }
     }

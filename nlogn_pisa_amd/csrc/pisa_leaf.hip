@@ -439,6 +439,12 @@ leaf_tile_kernel(LeafArgs a) {
   }
 }
 
+// Sum over the Gp heads of a request (aligned lane groups of a DPP row), with
+// the common four heads per kv head unrolled (no uniform branches per step).
+__device__ __forceinline__ float head_sum(float v, int Gp) {
+  return Gp == 4 ? group_sum(v, 4) : group_sum(v, Gp);
+}
+
 // ------------------------------------------------------------------ split spans
 //
 // Spans of SPAN sibling blocks of at most 64 keys (or two blocks of 128 keys),
@@ -659,7 +665,7 @@ leaf_split_kernel(LeafArgs a) {
       const int rho = u * 16 + col;
       const int rq = rho >> gl;
       const bool real = rq < nreq && (rho & (Gp - 1)) < a.G;
-      const float v = group_sum(real ? head : 0.f, Gp);
+      const float v = head_sum(real ? head : 0.f, Gp);
       if (grp == 0 && (col & (Gp - 1)) == 0 && rq < nreq && ((mmask[rq] >> c) & 1))
         a.scores[mslot[rq] + c] = v;
     };
@@ -715,7 +721,7 @@ leaf_split_kernel(LeafArgs a) {
         const int rho = u * 16 + col;
         const int rq = rho >> gl;
         const bool real = rq < nreq && (rho & (Gp - 1)) < a.G;
-        const float v = group_sum(real ? head : 0.f, Gp);
+        const float v = head_sum(real ? head : 0.f, Gp);
         if (grp == 0 && (col & (Gp - 1)) == 0 && rq < nreq && ((mmask[rq] >> c) & 1))
           a.scores[mslot[rq] + c] = v;
       }
