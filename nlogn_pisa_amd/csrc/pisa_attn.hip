@@ -855,6 +855,30 @@ __global__ void __launch_bounds__(256) attn_combine2_kernel(AttnArgs a, int64_t 
   const RowInfo ri = row_info(a, slot0);
   const int G = a.G, pairs = a.K * G;
   const int gl = 31 - __clz(G);
+  // pass 2's first U active slots (they depend on the ids only): their chunks
+  // are loaded before pass 1, so the two passes' first loads overlap
+  const int chunks = a.Dv / V;
+  const int work = G * chunks;
+  const PT* part = static_cast<const PT*>(a.part_o);
+  const bool early = work <= 64;  // one pass-2 round per row
+  uint64_t rest0 = __ballot(lane < min(64, a.K) && slot_active(a, slot0 + lane, ri.pos));
+  int sl0[U];
+  bool on0[U];
+  union Chunk {
+    uint4 u;
+    PT e[V];
+  } x0[U];
+  if (early) {
+    const int idx = min(lane, work - 1);
+    const int g = idx / chunks, c = idx % chunks;
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      on0[j] = rest0 != 0;
+      sl0[j] = on0[j] ? __ffsll((long long)rest0) - 1 : 0;
+      rest0 &= rest0 - 1;
+      x0[j].u = stream_load16(part + ((slot0 + sl0[j]) * G + g) * a.Dv + c * V);
+    }
+  }
   // pass 1: this lane's pairs lane + 64 j, all of head lane & (G - 1)
   float m = -INFINITY;
   float lse[kCombinePairs / 64];
@@ -879,9 +903,6 @@ __global__ void __launch_bounds__(256) attn_combine2_kernel(AttnArgs a, int64_t 
   for (int off = G; off < 64; off <<= 1) l += __shfl_xor(l, off);
   wave_lds_sync();
   // pass 2: lane (g, c) owns 16-byte chunk c of head g's row
-  const int chunks = a.Dv / V;
-  const int work = G * chunks;
-  const PT* part = static_cast<const PT*>(a.part_o);
   for (int base = 0; base < work; base += 64) {
     const int idx = min(base + lane, work - 1);
     const bool writer = base + lane < work;
@@ -890,9 +911,20 @@ __global__ void __launch_bounds__(256) attn_combine2_kernel(AttnArgs a, int64_t 
     float acc[V];
 #pragma unroll
     for (int v = 0; v < V; ++v) acc[v] = 0.f;
+    if (early) {
+#pragma unroll
+      for (int j = 0; j < U; ++j) {
+        if (on0[j]) {
+          const float w = wl[sl0[j] * G + g];
+#pragma unroll
+          for (int v = 0; v < V; ++v) acc[v] = fmaf(w, (float)x0[j].e[v], acc[v]);
+        }
+      }
+    }
     for (int s0 = 0; s0 < a.K; s0 += 64) {
       const int n = min(64, a.K - s0);
       uint64_t rest = __ballot(lane < n && slot_active(a, slot0 + s0 + lane, ri.pos));
+      if (early && s0 == 0) rest = rest0;  // the slots after the first U
       // the active slots in slot order, U partial chunks in flight
       while (rest) {
         int sl[U];
@@ -903,10 +935,7 @@ __global__ void __launch_bounds__(256) attn_combine2_kernel(AttnArgs a, int64_t 
           sl[j] = on[j] ? __ffsll((long long)rest) - 1 : sl[0];
           rest &= rest - 1;
         }
-        union {
-          uint4 u;
-          PT e[V];
-        } x[U];
+        Chunk x[U];
 #pragma unroll
         for (int j = 0; j < U; ++j) {
           const int64_t row = (slot0 + s0 + sl[j]) * G + g;
