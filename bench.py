@@ -66,6 +66,26 @@ def copy_probe():
     return 0
 
 
+def copy_rate():
+    """Bytes per second (read + written) of a plain 1 GiB device copy: the
+    practical ceiling of a kernel that reads and writes HBM in equal parts."""
+    import torch
+    src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(5):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    rate = 5 * 2 * src.numel() * 4 / (e0.elapsed_time(e1) * 1e-3)
+    del src, dst
+    torch.cuda.empty_cache()
+    return rate
+
+
 # ---------------------------------------------------------------- work counts
 
 def query_window(tokens, row_bytes):
@@ -481,6 +501,13 @@ def main():
             comp = attn_compulsory / n_launch
             roofline["compulsory_bytes_per_launch"] = int(comp)
             roofline["traffic_over_compulsory"] = round(traffic / comp, 2) if traffic else None
+            # the kernel's counted HBM traffic per second beside a plain copy's rate
+            # (it reads q rows and writes its partial rows in about equal parts)
+            copy = copy_rate()
+            roofline["copy_rate_gbps"] = round(copy / 1e9, 1)
+            if traffic:
+                roofline["traffic_rate_gbps"] = round(traffic / (dom_ms * 1e-3) / 1e9, 1)
+                roofline["traffic_frac_copy_rate"] = round(traffic / (dom_ms * 1e-3) / copy, 3)
     else:
         achieved = info["bytes"] / n_launch / (dom_ms * 1e-3)
         roofline = {"kernel": dominant, "bound": "hbm", "achieved": round(achieved / 1e9, 1),
