@@ -980,6 +980,44 @@ __global__ void __launch_bounds__(256) attn_delta_kernel(AttnArgs a, int64_t row
   if (lane == 0) a.delta[row] = s;
 }
 
+// rowsum(dO * O) with Dv / 4 lanes per row (Dv in {16, 32, 64, 128, 256}, 16-byte
+// aligned rows): each lane reads 4 consecutive values of O (float32 O when the
+// forward kept it) and of dO with one load each, 64 / (Dv / 4) rows per wave.
+template <typename T, int DV>
+__global__ void __launch_bounds__(256) attn_delta_vec_kernel(AttnArgs a, int64_t rows) {
+  constexpr int L = DV / 4 < 64 ? DV / 4 : 64;  // lanes per row
+  constexpr int R = 64 / L;                     // rows per wave
+  constexpr int PER = DV / (4 * L);             // quads per lane
+  const int lane = threadIdx.x & 63;
+  const int64_t row = ((int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * R + lane / L;
+  const int q = lane % L;
+  float s = 0.f;
+  if (row < rows) {
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int i = 4 * (q + L * k);
+      float ov[4], dv[4];
+      if (a.out_f32) {
+        const float4 x = *reinterpret_cast<const float4*>(a.out_f32 + row * DV + i);
+        ov[0] = x.x; ov[1] = x.y; ov[2] = x.z; ov[3] = x.w;
+      } else {
+        load_f<4>(static_cast<const T*>(a.out) + row * DV + i, ov);
+      }
+      load_f<4>(static_cast<const T*>(a.dout) + row * DV + i, dv);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s = fmaf(ov[e], dv[e], s);
+    }
+  }
+  // sum over the row's L lanes (aligned groups within the wave)
+  if constexpr (L >= 2) s += __shfl_xor(s, 1);
+  if constexpr (L >= 4) s += __shfl_xor(s, 2);
+  if constexpr (L >= 8) s += __shfl_xor(s, 4);
+  if constexpr (L >= 16) s += __shfl_xor(s, 8);
+  if constexpr (L >= 32) s += __shfl_xor(s, 16);
+  if constexpr (L >= 64) s += __shfl_xor(s, 32);
+  if (q == 0 && row < rows) a.delta[row] = s;
+}
+
 // LDS carve of the backward kernel (byte offsets, 16-byte aligned regions).
 struct BwdLds {
   size_t kt, qt, dot, dsa, pw, lse, delta, pos, slot, gh, total;
@@ -1220,9 +1258,11 @@ __global__ void __launch_bounds__(512) attn_bwd_grouped_kernel(AttnArgs a) {
 }
 
 // dK/dV of every key: the sum of its block's tile partials in tile order
-// (zero for blocks no row selected).  One workgroup per (batch, head, block);
-// a thread owns 4 consecutive columns of a key row and has four tiles' loads
-// in flight at a time.
+// (zero for blocks no row selected).  Workgroups (group blockIdx.x, chunk
+// blockIdx.y) give each thread one quad (4 consecutive columns of one key
+// row), eight tiles' loads in flight: a group with many tiles (the first
+// block, which every row selects) spreads over workgroups instead of
+// serialising in one.
 template <typename T>
 __global__ void __launch_bounds__(256) attn_dkv_reduce_kernel(AttnArgs a, int64_t groups) {
   const int64_t g = blockIdx.x;
@@ -1238,18 +1278,19 @@ __global__ void __launch_bounds__(256) attn_dkv_reduce_kernel(AttnArgs a, int64_
   const int quads = width / 4;
   const int64_t tile_stride = (int64_t)Cp * width / 4;
   const float4* part = reinterpret_cast<const float4*>(a.part_dkv) + (int64_t)first * tile_stride;
-  for (int idx = threadIdx.x; idx < rows * quads; idx += blockDim.x) {
+  const int idx = blockIdx.y * blockDim.x + threadIdx.x;
+  if (idx < rows * quads) {
     const int r = idx / quads, c = (idx % quads) * 4;
     const float4* src = part + (int64_t)r * quads + c / 4;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     int j = 0;
-    for (; j + 4 <= n; j += 4) {
-      float4 v[4];
+    for (; j + 8 <= n; j += 8) {  // eight tiles' loads in flight, summed in tile order
+      float4 v[8];
 #pragma unroll
-      for (int k = 0; k < 4; ++k)
+      for (int k = 0; k < 8; ++k)
         v[k] = stream_load_f4(reinterpret_cast<const float*>(src + (int64_t)(j + k) * tile_stride));
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
+      for (int k = 0; k < 8; ++k) {
         acc.x += v[k].x;
         acc.y += v[k].y;
         acc.z += v[k].z;
@@ -1265,14 +1306,19 @@ __global__ void __launch_bounds__(256) attn_dkv_reduce_kernel(AttnArgs a, int64_
     }
     const int64_t tok = block_key(a, blk) + r;
     const float vals[4] = {acc.x, acc.y, acc.z, acc.w};
+    // the quad lies wholly in dK or in dV (D is a multiple of 4): one store of
+    // its four values where aligned
+    T* dst = c < a.D ? static_cast<T*>(a.dk) + (int64_t)b * a.dk_batch + tok * a.dk_token + (int64_t)h * a.D + c
+                     : static_cast<T*>(a.dv) + (int64_t)b * a.dv_batch + tok * a.dv_token + (int64_t)h * a.Dv +
+                           (c - a.D);
+    T out4[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int cc = c + e;
-      if (cc < a.D)
-        static_cast<T*>(a.dk)[(int64_t)b * a.dk_batch + tok * a.dk_token + (int64_t)h * a.D + cc] = from_f<T>(vals[e]);
-      else
-        static_cast<T*>(a.dv)[(int64_t)b * a.dv_batch + tok * a.dv_token + (int64_t)h * a.Dv + (cc - a.D)] =
-            from_f<T>(vals[e]);
+    for (int e = 0; e < 4; ++e) out4[e] = from_f<T>(vals[e]);
+    if (((uintptr_t)dst & (4 * sizeof(T) - 1)) == 0) {
+      store_vals(dst, out4);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dst[e] = out4[e];
     }
   }
 }
@@ -2239,8 +2285,19 @@ template <typename T>
 static int attn_bwd_t(const AttnArgs& args, int64_t groups, int64_t items, hipStream_t stream) {
   AttnArgs a = args;
   const int64_t rows = items * a.G;
-  if (rows > 0)
-    PISA_TIMED("attn_delta", stream, hipLaunchKernelGGL(attn_delta_kernel<T>, dim3((rows + 3) / 4), dim3(256), 0, stream, a, rows));
+  if (rows > 0) {
+    const bool vec = sizeof(T) == 2 && ((uintptr_t)a.out & 15) == 0 && ((uintptr_t)a.dout & 15) == 0 &&
+                     (!a.out_f32 || ((uintptr_t)a.out_f32 & 15) == 0);
+    auto delta_vec = [&](auto kernel, int dv) {
+      const int64_t per_block = 4 * (int64_t)(64 / (dv / 4 < 64 ? dv / 4 : 64));  // rows per 256 threads
+      PISA_TIMED("attn_delta", stream, hipLaunchKernelGGL(kernel, dim3((rows + per_block - 1) / per_block), dim3(256), 0, stream, a, rows));
+    };
+    if (vec && a.Dv == 128) delta_vec(attn_delta_vec_kernel<T, 128>, 128);
+    else if (vec && a.Dv == 64) delta_vec(attn_delta_vec_kernel<T, 64>, 64);
+    else if (vec && a.Dv == 32) delta_vec(attn_delta_vec_kernel<T, 32>, 32);
+    else
+      PISA_TIMED("attn_delta", stream, hipLaunchKernelGGL(attn_delta_kernel<T>, dim3((rows + 3) / 4), dim3(256), 0, stream, a, rows));
+  }
   switch (a.D) {
     case 16: launch_bwd_kernel<T, 16>(a, stream); break;
     case 32: launch_bwd_kernel<T, 32>(a, stream); break;
@@ -2249,7 +2306,10 @@ static int attn_bwd_t(const AttnArgs& args, int64_t groups, int64_t items, hipSt
     default: return fail(PISA_ERR_UNSUPPORTED, "attention backward head_dim %d", a.D);
   }
   if (groups > 0)
-    PISA_TIMED("attn_dkv_reduce", stream, hipLaunchKernelGGL(attn_dkv_reduce_kernel<T>, dim3(groups), dim3(256), 0, stream, a, groups));
+    PISA_TIMED("attn_dkv_reduce", stream,
+               hipLaunchKernelGGL(attn_dkv_reduce_kernel<T>,
+                                  dim3(groups, ((a.C + 15) / 16 * 16 * ((a.D + a.Dv) / 4) + 255) / 256), dim3(256),
+                                  0, stream, a, groups));
   if (items > 0) {
     if (a.part_dq_exp)
       PISA_TIMED("attn_dq_combine", stream, hipLaunchKernelGGL(attn_dq_combine_compact_kernel<T>, dim3((items + 3) / 4), dim3(256), 0, stream, a, items));
