@@ -189,6 +189,13 @@ __device__ __forceinline__ float group_sum(float v, int n) {
   return v;
 }
 
+// Sum over the Gp heads of a request (aligned groups of Gp lanes, Gp a power of
+// two <= 16), with the common four heads per kv head unrolled (no uniform
+// branches per step).
+__device__ __forceinline__ float head_sum(float v, int Gp) {
+  return Gp == 4 ? group_sum(v, 4) : group_sum(v, Gp);
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
   v = row_sum16(v);
   v += __shfl_xor(v, 16);

@@ -388,7 +388,7 @@ leaf_tile_kernel(LeafArgs a) {
           const float v = group_sum(tot[c], 16);
           if (lane == 0 && r < nreq && ((mmask[r] >> c) & 1)) a.scores[mslot[r] + c] = v;
         } else {
-          const float v = group_sum(tot[c], Gp);
+          const float v = head_sum(tot[c], Gp);
           const int rq = ((r << 4) + col) >> gl;
           if (grp == 0 && (col & (Gp - 1)) == 0 && rq < nreq && ((mmask[rq] >> c) & 1))
             a.scores[mslot[rq] + c] = v;
@@ -437,12 +437,6 @@ leaf_tile_kernel(LeafArgs a) {
     if (full) run(std::true_type{});
     else run(std::false_type{});
   }
-}
-
-// Sum over the Gp heads of a request (aligned lane groups of a DPP row), with
-// the common four heads per kv head unrolled (no uniform branches per step).
-__device__ __forceinline__ float head_sum(float v, int Gp) {
-  return Gp == 4 ? group_sum(v, 4) : group_sum(v, Gp);
 }
 
 // ------------------------------------------------------------------ split spans

@@ -601,9 +601,11 @@ __device__ __forceinline__ float support_final(SupportAcc r, const float* v, flo
     const float d = z0 - z1;
     return r.n == 2 ? 0.5f * (z0 + z1) + 0.125f * d * d : z0;
   } else {
-    const float count = (float)max(r.n, 1);
-    const float mean = r.a0 / count;
-    const float var = fmaxf(r.a1 / count - mean * mean, 0.f);
+    // 1 / count by v_rcp_f32: exact for the power-of-two counts of full nodes,
+    // within an ulp for the partial last node of a level
+    const float inv = __builtin_amdgcn_rcpf((float)max(r.n, 1));
+    const float mean = r.a0 * inv;
+    const float var = fmaxf(r.a1 * inv - mean * mean, 0.f);
     return scale * mean + (float)(0.5 * (double)scale * (double)scale) * var;
   }
 }
@@ -926,7 +928,7 @@ __global__ void __launch_bounds__(256) route_dense_kernel(RouteArgs a) {
   // valid support rows of node n (0 past the level)
   auto count = [&](int n) { return n >= M ? 0 : own ? 1 : max(0, min(R, len - n * R)); };
   auto store = [&](int c, int n, float head) {
-    const float tot = group_sum(hd < a.G ? head : 0.f, Gp);
+    const float tot = head_sum(hd < a.G ? head : 0.f, Gp);
     if (hd == 0) sw[c * P + col / Gp][n % kDenseChunk] = tot;
   };
   // the staged nodes [64 k, 64 k + 64) of the wave's items -> their rows
@@ -1082,7 +1084,7 @@ __global__ void __launch_bounds__(256) route_dense_lds_kernel(RouteArgs a) {
   // valid support rows of node n (0 past the level)
   auto count = [&](int n) __attribute__((always_inline)) { return n >= M ? 0 : own ? 1 : max(0, min(R, len - n * R)); };
   auto store = [&](int c, int n, float head) __attribute__((always_inline)) {
-    const float tot = group_sum(hd < a.G ? head : 0.f, Gp);
+    const float tot = head_sum(hd < a.G ? head : 0.f, Gp);
     if (hd == 0) sw[c * P + col / Gp][n % kDenseChunk] = tot;
   };
   // the staged nodes [64 k, 64 k + 64) of the wave's items -> their rows
