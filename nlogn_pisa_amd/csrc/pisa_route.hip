@@ -1103,7 +1103,10 @@ __global__ void __launch_bounds__(256) route_dense_lds_kernel(RouteArgs a) {
     wave_lds_sync();
   };
   const int tiles_per_chunk = kDenseChunk * (own ? 1 : R) / 16;
-  auto tile = [&](int mt, const frag (&xf)[DS]) __attribute__((always_inline)) {
+  // WH: every node of tile mt has all R support rows (all but a level's last
+  // tile), so the counts are the constant R and no row is masked
+  auto tile_body = [&](int mt, const frag (&xf)[DS], auto wh_tag) __attribute__((always_inline)) {
+    constexpr bool WH = decltype(wh_tag)::value;
 #pragma unroll
     for (int c = 0; c < NCT; ++c) {
       f4 sv = f4{0.f, 0.f, 0.f, 0.f};
@@ -1118,7 +1121,7 @@ __global__ void __launch_bounds__(256) route_dense_lds_kernel(RouteArgs a) {
           if constexpr (own) {
             head = v[j];
           } else {
-            const SupportAcc acc = support_acc<LSE>(v + j * R, R, count(n), a.scale);
+            const SupportAcc acc = support_acc<LSE>(v + j * R, R, WH ? R : count(n), a.scale);
             head = support_final<MODE>(acc, v + j * R, a.scale);
           }
           store(c, n, head);
@@ -1126,7 +1129,7 @@ __global__ void __launch_bounds__(256) route_dense_lds_kernel(RouteArgs a) {
       } else {
         // R = 8: lane groups 2k (children 0-3) and 2k + 1 (children 4-7) of node 2 mt + k
         const int n = mt * 2 + (grp >> 1);
-        const int cnt = count(n) - 4 * (grp & 1);
+        const int cnt = (WH ? R : count(n)) - 4 * (grp & 1);
         SupportAcc acc = support_acc<LSE>(v, 4, cnt, a.scale);
         SupportAcc other;
         other.a0 = __shfl_xor(acc.a0, 16);
@@ -1137,6 +1140,11 @@ __global__ void __launch_bounds__(256) route_dense_lds_kernel(RouteArgs a) {
         store(c, n, head);
       }
     }
+  };
+  auto tile = [&](int mt, const frag (&xf)[DS]) __attribute__((always_inline)) {
+    const bool whole = own ? (mt + 1) * 16 <= M : ((mt + 1) * 16 <= len && (mt + 1) * 16 / R <= M);
+    if (whole) tile_body(mt, xf, std::true_type{});
+    else tile_body(mt, xf, std::false_type{});
   };
   auto done = [&](int mt) __attribute__((always_inline)) {
     if ((mt + 1) % tiles_per_chunk == 0 || mt + 1 == ntile) flush(mt / tiles_per_chunk);
