@@ -190,10 +190,10 @@ __device__ __forceinline__ float group_sum(float v, int n) {
 }
 
 // Sum over the Gp heads of a request (aligned groups of Gp lanes, Gp a power of
-// two <= 16), with the common four heads per kv head unrolled (no uniform
-// branches per step).
+// two <= 16), with the common four and eight heads per kv head unrolled (no
+// uniform branches per step).
 __device__ __forceinline__ float head_sum(float v, int Gp) {
-  return Gp == 4 ? group_sum(v, 4) : group_sum(v, Gp);
+  return Gp == 4 ? group_sum(v, 4) : Gp == 8 ? group_sum(v, 8) : group_sum(v, Gp);
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
