@@ -170,6 +170,7 @@ LeafArgs leaf_args(const pisa_qk_desc* qk, int method, int block_size, int W, in
   a.tile_off = b.tile_off;
   a.counts = b.counts;
   a.num_tiles = b.num_tiles;
+  a.tile_cursor = b.num_tiles ? b.num_tiles + 1 : nullptr;
   a.tile = b.tile;
   a.scores = scores;
   (void)block_size;

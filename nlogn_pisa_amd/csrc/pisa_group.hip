@@ -224,6 +224,7 @@ __global__ void __launch_bounds__(1024) bucket_scan_kernel(const int32_t* counts
     run += (counts[g] + tile - 1) / tile;
   }
   if (tid == 1023) *num_tiles = (int32_t)part[1023];
+  if (tid < 8) num_tiles[1 + tid] = 0;  // per-XCD tile cursors
 }
 
 // The same exclusive scan of tiles per group for many groups, in three passes:
@@ -284,6 +285,7 @@ __global__ void __launch_bounds__(1024) scan_blocks_kernel(int32_t* block_sum, i
     __syncthreads();
   }
   if (tid == 0) *num_tiles = (int32_t)carry;
+  if (tid < 8) num_tiles[1 + tid] = 0;  // per-XCD tile cursors
 }
 
 __global__ void __launch_bounds__(256) scan_add_kernel(int32_t* tile_off, int64_t groups,
@@ -317,7 +319,7 @@ void carve_buckets(Carve& c, Buckets& b, int64_t slots, int64_t groups, int tile
   b.groups = groups;
   b.tile = tile;
   b.max_tiles = (slots + tile - 1) / tile + groups;
-  b.counts = c.take<int32_t>(2 * groups + 1);  // counts, cursors, tile count: one fill
+  b.counts = c.take<int32_t>(2 * groups + 9);  // counts, cursors, tile count, tile cursors: one fill
   b.cursors = b.counts ? b.counts + groups : nullptr;
   b.num_tiles = b.counts ? b.counts + 2 * groups : nullptr;
   b.tile_off = c.take<int32_t>(groups);
@@ -350,7 +352,7 @@ static int run_buckets(const Src& src, int64_t slot_begin, int64_t slot_end, Buc
                 (long long)(slot_end - slot_begin));
   const int64_t range = slot_end - slot_begin;
   if (range <= 0) {
-    fill_i32(b.counts, 2 * b.groups + 1, 0, stream);  // counts, cursors, tile count
+    fill_i32(b.counts, 2 * b.groups + 9, 0, stream);  // counts, cursors, tile count, tile cursors
     return check_launch("bucket fill");
   }
   if (b.hist) {
@@ -372,7 +374,7 @@ static int run_buckets(const Src& src, int64_t slot_begin, int64_t slot_end, Buc
     return check_launch("bucket");
   }
   // global atomics on counts and cursors
-  fill_i32(b.counts, 2 * b.groups + 1, 0, stream);  // counts, cursors, tile count
+  fill_i32(b.counts, 2 * b.groups + 9, 0, stream);  // counts, cursors, tile count, tile cursors
   const int64_t chunk = kSmallChunk;
   const int64_t grid = (range + chunk - 1) / chunk;
   PISA_TIMED("bucket_count", stream, hipLaunchKernelGGL((bucket_count_kernel<Src>), dim3(grid), dim3(kBucketThreads), 0, stream,

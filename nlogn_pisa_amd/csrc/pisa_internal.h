@@ -58,7 +58,7 @@ struct Buckets {
   int32_t* tile_off;    // [groups]
   int32_t* tile_group;  // [max_tiles]
   int32_t* tile_req;    // [max_tiles * tile]
-  int32_t* num_tiles;   // [1]
+  int32_t* num_tiles;   // [1 + 8]: the tile count, then per-XCD tile cursors (zeroed with it)
   int32_t* hist;        // [kMaxBucketGroups rows][groups]: per-workgroup histograms, then offsets
   int32_t* block_sum;   // [groups / 4096]: block totals of the many-group scan, then bases
   int64_t groups;
@@ -188,6 +188,7 @@ struct LeafArgs {
   const int32_t* tile_off;
   const int32_t* counts;
   const int32_t* num_tiles;
+  int32_t* tile_cursor;  // [8] per-XCD cursors of the dynamic tile walk (zero before the launch)
   int tile;
   float* scores;
 };
