@@ -279,7 +279,11 @@ __global__ void __launch_bounds__(256) attn_fwd_grouped_kernel(AttnArgs a) {
   char* wave_lds = smem + (size_t)(Cp * ldk + a.Dv * ldv) * sizeof(T) +
                    wave * FwdWaveLds<T>(Cp, a.Dv).bytes;
   const int ntiles = *a.num_tiles;
-  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+  __shared__ int tile_slot;
+  const TileQueue queue = xcd_queue(ntiles);  // the dynamic XCD walk
+  for (;;) {
+    const int tile = next_tile(queue, a.tile_cursor, &tile_slot);
+    if (tile >= queue.end) break;
     const int g = a.tile_group[tile];
     const int64_t blk = g % a.M0;
     const int bh = g / a.M0;
@@ -703,7 +707,11 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_tile_kernel(AttnArgs a) {
   typedef typename PartialT<T>::type PT;
   PT* so = STAGE ? reinterpret_cast<PT*>(smem + L.o_off) + wave * kStageRows * L.ldo : nullptr;
   const int ntiles = *a.num_tiles;
-  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+  __shared__ int tile_slot;
+  const TileQueue queue = xcd_queue(ntiles);  // the dynamic XCD walk
+  for (;;) {
+    const int tile = next_tile(queue, a.tile_cursor, &tile_slot);
+    if (tile >= queue.end) break;
     const int g = a.tile_group[tile];
     const int64_t blk = g % a.M0;
     const int bh = g / a.M0;
@@ -1079,7 +1087,11 @@ __global__ void __launch_bounds__(512) attn_bwd_grouped_kernel(AttnArgs a) {
   const int ntiles = *a.num_tiles;
   const int Hq = a.Hkv * a.G;
 
-  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+  __shared__ int tile_slot;
+  const TileQueue queue = xcd_queue(ntiles);  // the dynamic XCD walk
+  for (;;) {
+    const int tile = next_tile(queue, a.tile_cursor, &tile_slot);
+    if (tile >= queue.end) break;
     const int g = a.tile_group[tile];
     const int64_t blk = g % a.M0;
     const int bh = g / a.M0;
@@ -1675,7 +1687,11 @@ __global__ void __launch_bounds__(64 * W, W == 4 ? 2 : 1) attn_bwd_tile_kernel(A
   };
 
   const int ntiles = *a.num_tiles;
-  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+  __shared__ int tile_slot;
+  const TileQueue queue = xcd_queue(ntiles);  // the dynamic XCD walk
+  for (;;) {
+    const int tile = next_tile(queue, a.tile_cursor, &tile_slot);
+    if (tile >= queue.end) break;
     const int g = a.tile_group[tile];
     const int64_t blk = g % a.M0;
     const int bh = g / a.M0;
@@ -1901,7 +1917,11 @@ __global__ void __launch_bounds__(256, NT <= 4 ? 2 : 1) attn_bwd_share_kernel(At
   static_assert(HD == 128, "rows of 16 lanes x 16 bytes");
 
   const int ntiles = *a.num_tiles;
-  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+  __shared__ int tile_slot;
+  const TileQueue queue = xcd_queue(ntiles);  // the dynamic XCD walk
+  for (;;) {
+    const int tile = next_tile(queue, a.tile_cursor, &tile_slot);
+    if (tile >= queue.end) break;
     const int g = a.tile_group[tile];
     const int64_t blk = g % a.M0;
     const int bh = g / a.M0;

@@ -521,6 +521,7 @@ void bind_buckets(AttnArgs& a, const Buckets& b) {
   a.tile_off = b.tile_off;
   a.counts = b.counts;
   a.num_tiles = b.num_tiles;
+  a.tile_cursor = b.num_tiles ? b.num_tiles + 1 : nullptr;
   a.tile = b.tile;
 }
 

@@ -84,6 +84,28 @@ __device__ __forceinline__ XcdTiles xcd_tiles(int ntiles) {
                   (int)((int64_t)ntiles * (x + 1) / 8), (int)(gridDim.x >> 3)};
 }
 
+// The dynamic form of that walk: XCD x takes the tiles of its eighth one at a
+// time from its cursor (Buckets::num_tiles[1 + x], zeroed by the bucketing), so
+// tiles of unequal size balance out within the XCD.  next_tile() is called by
+// every thread of the workgroup (two barriers) and returns the same tile to all;
+// a tile at or past `end` means the workgroup is done (every workgroup gets
+// there: the cursor only grows).  `slot` is a __shared__ int of the kernel.
+struct TileQueue {
+  int first, end, xcd;
+};
+
+__device__ __forceinline__ TileQueue xcd_queue(int ntiles) {
+  const int x = (int)(blockIdx.x & 7);
+  return TileQueue{(int)((int64_t)ntiles * x / 8), (int)((int64_t)ntiles * (x + 1) / 8), x};
+}
+
+__device__ __forceinline__ int next_tile(const TileQueue& q, int32_t* cursors, int* slot) {
+  __syncthreads();  // every thread has read the previous tile
+  if (threadIdx.x == 0) *slot = q.first + atomicAdd(cursors + q.xcd, 1);
+  __syncthreads();
+  return *slot;
+}
+
 // Sources of bucketed requests.
 // Leaf requests: request i is the `span` consecutive slots i*span .. i*span+span-1
 // of one item, whose candidates are consecutive blocks (siblings under one
@@ -216,6 +238,7 @@ struct AttnArgs {
   const int32_t* tile_off;
   const int32_t* counts;
   const int32_t* num_tiles;
+  int32_t* tile_cursor;  // [8] per-XCD cursors of the dynamic tile walk (zero before the launch)
   int tile;
   // forward
   void* part_o;     // [slots * G, Dv] normalized partial rows (fp16, or fp32 for fp32 inputs)

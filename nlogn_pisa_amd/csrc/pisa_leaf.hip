@@ -499,20 +499,12 @@ leaf_split_kernel(LeafArgs a) {
   const T* q = static_cast<const T*>(a.q);
   const int ntiles = *a.num_tiles;
 
-  // XCD x = blockIdx.x % 8 takes the tiles of its eighth of the (batch, kv
-  // head, block)-ordered list one at a time from its cursor, so its workgroups
-  // share query rows in its L2 and tiles of unequal size balance out.  Every
-  // workgroup leaves once its cursor passes the eighth's end.
-  __shared__ int next_tile;
-  const int xcd = (int)(blockIdx.x & 7);
-  const int first_tile = (int)((int64_t)ntiles * xcd / 8);
-  const int end_tile = (int)((int64_t)ntiles * (xcd + 1) / 8);
+  // the dynamic XCD walk: an XCD's workgroups share query rows in its L2
+  __shared__ int tile_slot;
+  const TileQueue queue = xcd_queue(ntiles);
   for (;;) {
-    __syncthreads();  // every thread has read next_tile
-    if (threadIdx.x == 0) next_tile = first_tile + atomicAdd(a.tile_cursor + xcd, 1);
-    __syncthreads();
-    const int tile = next_tile;
-    if (tile >= end_tile) break;
+    const int tile = next_tile(queue, a.tile_cursor, &tile_slot);
+    if (tile >= queue.end) break;
     const int g = a.tile_group[tile];
     const int blk0 = (g % a.spans) * SPAN;
     const int bh = g / a.spans;
