@@ -68,28 +68,18 @@ struct Buckets {
 
 void carve_buckets(Carve& c, Buckets& b, int64_t slots, int64_t groups, int tile);
 
-// The tiles a consumer workgroup walks when workgroups are dealt round-robin
-// to the 8 XCDs: XCD x = blockIdx.x % 8 takes the contiguous eighth
+// The tiles a consumer workgroup takes when workgroups are dealt round-robin
+// to the 8 XCDs: XCD x = blockIdx.x % 8 works through the contiguous eighth
 // [ntiles x / 8, ntiles (x + 1) / 8) of the (batch, kv head, block)-ordered
-// tile list, its workgroups striding by gridDim.x / 8, so the tiles an XCD runs
-// together come from few kv heads and share their query rows in its L2.  The
-// eighths partition the list for any placement; gridDim.x must be a multiple of 8.
-struct XcdTiles {
-  int begin, end, step;
-};
-
-__device__ __forceinline__ XcdTiles xcd_tiles(int ntiles) {
-  const int x = (int)(blockIdx.x & 7);
-  return XcdTiles{(int)((int64_t)ntiles * x / 8) + (int)(blockIdx.x >> 3),
-                  (int)((int64_t)ntiles * (x + 1) / 8), (int)(gridDim.x >> 3)};
-}
-
-// The dynamic form of that walk: XCD x takes the tiles of its eighth one at a
-// time from its cursor (Buckets::num_tiles[1 + x], zeroed by the bucketing), so
-// tiles of unequal size balance out within the XCD.  next_tile() is called by
-// every thread of the workgroup (two barriers) and returns the same tile to all;
-// a tile at or past `end` means the workgroup is done (every workgroup gets
-// there: the cursor only grows).  `slot` is a __shared__ int of the kernel.
+// tile list, so the tiles an XCD runs together come from few kv heads and share
+// their query rows in its L2 (the eighths partition the list for any placement;
+// gridDim.x must be a multiple of 8).  Its workgroups take the eighth's tiles
+// one at a time from the XCD's cursor (Buckets::num_tiles[1 + x], zeroed by the
+// bucketing), so tiles of unequal size balance out within the XCD.
+// next_tile() is called by every thread of the workgroup (two barriers) and
+// returns the same tile to all; a tile at or past `end` means the workgroup is
+// done (every workgroup gets there: the cursor only grows).  `slot` is a
+// __shared__ int of the kernel.
 struct TileQueue {
   int first, end, xcd;
 };

@@ -262,8 +262,11 @@ leaf_tile_kernel(LeafArgs a) {
   constexpr int vpr = HD / vec;
   const int ntiles = *a.num_tiles;
 
-  const XcdTiles walk = xcd_tiles(ntiles);
-  for (int tile = walk.begin; tile < walk.end; tile += walk.step) {
+  __shared__ int tile_slot;
+  const TileQueue queue = xcd_queue(ntiles);  // the dynamic XCD walk
+  for (;;) {
+    const int tile = next_tile(queue, a.tile_cursor, &tile_slot);
+    if (tile >= queue.end) break;
     const int g = a.tile_group[tile];
     const int blk0 = (g % a.spans) * span;  // first block of the tile's span
     const int bh = g / a.spans;
