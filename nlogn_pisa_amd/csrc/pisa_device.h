@@ -134,9 +134,12 @@ __device__ __forceinline__ void load_f(const f16_t* p, float* out) {
 
 // ------------------------------------------------------------------ lane reductions
 
+// v of the lane a DPP pattern names.  Every pattern used here (quad permutes,
+// row mirrors, row rotations) gives each lane a valid source with all rows and
+// banks enabled, so no old value is needed (v_mov_b32_dpp, no register to clear).
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
 }
 
 // All-reduce over each DPP row of 16 lanes with row rotations 8, 4, 2, 1.  Every
@@ -517,15 +520,15 @@ struct QkShape {
 template <int D>
 __device__ __forceinline__ int xor_row(int v) {
   if constexpr (D == 1) {
-    return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
+    return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
   } else if constexpr (D == 2) {
-    return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
+    return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
   } else if constexpr (D == 4) {
     // row_half_mirror (j <- j ^ 7 within 8 lanes), then quad_perm [3,2,1,0] (j <- j ^ 3)
-    const int m = __builtin_amdgcn_update_dpp(0, v, 0x141, 0xf, 0xf, false);
-    return __builtin_amdgcn_update_dpp(0, m, 0x1B, 0xf, 0xf, false);
+    const int m = __builtin_amdgcn_mov_dpp(v, 0x141, 0xf, 0xf, false);
+    return __builtin_amdgcn_mov_dpp(m, 0x1B, 0xf, 0xf, false);
   } else {
-    return __builtin_amdgcn_update_dpp(0, v, 0x128, 0xf, 0xf, false);  // row_ror 8
+    return __builtin_amdgcn_mov_dpp(v, 0x128, 0xf, 0xf, false);  // row_ror 8
   }
 }
 
