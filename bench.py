@@ -122,12 +122,19 @@ def leaf_span(w, elem):
     return span
 
 
+def grouped_schedule(w):
+    """Whether the automatic schedule routes grouped (top_k_pyramid.py:64-72): pisa
+    or pisa2 with more than one query token; otherwise the fused route scores
+    every level, the leaf included, by gathering."""
+    return w.method != "pisa1" and w.tokens > 1
+
+
 def dense_levels(w, top, first):
     """Routing levels scored densely, {level: nodes} (mirrors route_level_dense in
     csrc/pisa_route.hip: padded head groups of 4 or 8, branching <= 8, a level whose
     nodes are at most (16 / Gp) x its candidate width)."""
     gp = 1 << (w.query_heads // w.key_heads - 1).bit_length()
-    if not 4 <= gp <= 8 or w.branching > 8 or w.method == "pisa1":   # pisa1 routes fused
+    if not 4 <= gp <= 8 or w.branching > 8 or not grouped_schedule(w):   # fused routes gather
         return {}
     out, nodes = {}, math.ceil(w.keys / w.block_size)
     sizes = [nodes]
@@ -449,10 +456,14 @@ def main():
     span = counts.get("leaf_span", 1)
     r_span = counts.get("leaf_requests", r_leaf)
     # algorithmic bytes / flops per launch of each hot kernel
+    # the fused route (decode, pisa1) also scores the leaf: raw key rows of each
+    # scored candidate (leaf means for pisa1)
+    fused_leaf = 0 if grouped_schedule(w) else r_leaf * (D * e if w.method == "pisa1"
+                                                          else w.block_size * D * e)
     algo = {
         "route": {"bound": "hbm",
                   "bytes": w.batch * w.tokens * w.query_heads * D * e + r_int * w.branching * D * e
-                  + r_dense * 4 + items * width * 5},
+                  + r_dense * 4 + items * width * 5 + fused_leaf},
         # per dense level: the query rows, each wave's pass over the level's support
         # rows (16 items per wave), the score rows written
         "route_dense": {"bound": "mfma",
