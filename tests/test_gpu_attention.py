@@ -197,6 +197,29 @@ def test_forward_value_dim_differs(P, dv):
     assert np.abs(lse.cpu().numpy()[fin] - ref_lse[fin]).max() <= TOL[dtype]
 
 
+@pytest.mark.parametrize("kind", ["padding", "out-of-range"])
+@pytest.mark.parametrize("tq", [1, 700])
+def test_no_visible_key_anywhere(P, kind, tq):
+    """Every id -1, or every id past the last block: no request reaches a tile
+    (the tile walks start on an empty list), O = 0 and LSE = -inf for every row
+    and every gradient is 0, as the reference's masked softmax gives
+    (sparse_attn_torch.py:28-31)."""
+    print(f"attention without visible keys {kind} tq={tq}", flush=True)
+    n, block = 700, 64
+    q, k, v = structured_qkv(31, 2, n, 8, 2, 128, "bf16")
+    q = np.ascontiguousarray(q[:, n - tq:])
+    fill = -1 if kind == "padding" else -(-n // block) + 2
+    idx = torch.full((2, tq, 2, 8), fill, dtype=torch.int64, device="cuda")
+    qg, kg, vg = (to_gpu(x, "bf16").requires_grad_(True) for x in (q, k, v))
+    out, lse = P.sparse_attention_with_lse(qg.detach(), kg.detach(), vg.detach(), idx, block)
+    assert torch.count_nonzero(out).item() == 0
+    assert torch.isneginf(lse).all()
+    out = P.sparse_attention(qg, kg, vg, idx, block)
+    out.backward(torch.ones_like(out))
+    for g in (qg.grad, kg.grad, vg.grad):
+        assert torch.count_nonzero(g).item() == 0
+
+
 def test_int32_indices_and_determinism(P):
     q, k, v, idx = _inputs(CASES[2])
     qg, kg, vg = (to_gpu(x, "bf16") for x in (q, k, v))

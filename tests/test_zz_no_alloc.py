@@ -93,6 +93,26 @@ def test_noalloc_equals_workspace_entry(P, pair):
         assert excess_error(o_na.float().cpu().numpy(), ref_o, "bf16") <= 2e-2
 
 
+def test_noalloc_around_a_call_without_visible_keys(P):
+    """The scratch keeps the previous call's buckets and tile cursors: a prefill with
+    real ids, one whose ids are all padding (no request reaches a tile), then the
+    first again, each bit-identical to the workspace entry point, the second
+    with O = 0 and LSE = -inf."""
+    name, batch, tq, n, qh, kh, dim, block, topk = CALLS[3]
+    q, k, v = structured_qkv(77, batch, n, qh, kh, dim, "bf16")
+    q = q[:, n - tq:]
+    real = torch.from_numpy(_ids(9, batch, tq, kh, topk, n, block)).cuda()
+    empty = torch.full_like(real, -1)
+    qg, kg, vg = (to_gpu(x, "bf16") for x in (q, k, v))
+    for step, ig in enumerate((real, empty, real)):
+        print(f"no-alloc attention sequence step {step}", flush=True)
+        (o_ws, l_ws), (o_na, l_na) = _both(P, qg, kg, vg, ig, block)
+        assert torch.equal(o_ws, o_na) and torch.equal(l_ws, l_na), f"step {step} differs"
+        if step == 1:
+            assert torch.count_nonzero(o_na).item() == 0
+            assert torch.isneginf(l_na).all()
+
+
 def test_noalloc_rejects_oversized(P):
     """A shape whose workspace exceeds the static scratch is refused before any launch."""
     from nlogn_pisa_amd import _lib
