@@ -196,6 +196,16 @@ int pisa_bsa_select(const pisa_qk_desc* qk, int32_t block_size, int32_t topk, in
 /* Workspace bytes for the attention entry points. */
 size_t pisa_attention_workspace_size(const pisa_attn_desc* a, int32_t backward);
 
+/* The largest key block (128, 64, 32 or 16) the attention entry points take
+ * for this dtype and these head dims on the current device (the key block and
+ * its tile rows must fit its LDS; with backward != 0, the backward's too); 0 if
+ * none.  A caller attends larger blocks as their consecutive sub-blocks of that
+ * size, the same key set.  No counterpart in the reference, whose Triton and
+ * FLA kernels choose their own tiles (sparse_attn_fla.py:42-45 rejects the
+ * shapes it cannot tile). */
+int32_t pisa_attention_block_limit(int32_t dtype, int32_t head_dim, int32_t value_dim,
+                                   int32_t backward);
+
 /* Attention over the selected blocks: O [B, Tq, Hq, Dv] (dtype) and the
  * natural-log LSE float32 [B, Tq, Hq] (-inf, O = 0 for rows without a
  * visible key).  Replaces selected_attention,

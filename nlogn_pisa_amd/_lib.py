@@ -28,7 +28,7 @@ MAX_LEVELS = 32
 EXPORTS = (
     "pisa_last_error", "pisa_abi_version", "pisa_routing_geometry", "pisa_pyramid_layout",
     "pisa_mean_pool", "pisa_build_pyramid", "pisa_pyramid_append", "pisa_rotary", "pisa_select_workspace_size", "pisa_select",
-    "pisa_leaf_workspace_size", "pisa_leaf_scores", "pisa_bsa_workspace_size", "pisa_bsa_select", "pisa_attention_workspace_size", "pisa_sparse_attention_fwd",
+    "pisa_leaf_workspace_size", "pisa_leaf_scores", "pisa_bsa_workspace_size", "pisa_bsa_select", "pisa_attention_workspace_size", "pisa_attention_block_limit", "pisa_sparse_attention_fwd",
     "pisa_sparse_attention_bwd", "pisa_noalloc_scratch_bytes", "pisa_sparse_attention_fwd_noalloc",
     "pisa_profile_begin", "pisa_profile_end",
 )
@@ -115,6 +115,7 @@ def _declare(lib):
         "pisa_leaf_scores": (I32, [ctypes.POINTER(QkDesc), ctypes.POINTER(SelectParams), P, P, P,
                                    I64, P, I32, P, I64, P, P, SZ, P]),
         "pisa_attention_workspace_size": (SZ, [ctypes.POINTER(AttnDesc), I32]),
+        "pisa_attention_block_limit": (I32, [I32, I32, I32, I32]),
         "pisa_sparse_attention_fwd": (I32, [ctypes.POINTER(AttnDesc), P, P, P, P, P, I64, P, P, P,
                                             P, SZ, P]),
         "pisa_sparse_attention_bwd": (I32, [ctypes.POINTER(AttnDesc), P, P, P, P, P, I64, P, P, P,

@@ -164,21 +164,35 @@ def _check(q, k, v, indices, block_size, backend):
         raise ValueError("invalid block_size or attention backend")
 
 
-# Largest key block the attention kernels stage (keys of a block in LDS).
+# Largest key block the attention kernels stage (keys of a block in LDS); wide
+# fp32 rows take less (kernel_block).
 MAX_KERNEL_BLOCK = 128
 
 
-def split_blocks(indices, block_size):
-    """Ids of blocks over MAX_KERNEL_BLOCK keys as ids of their sub-blocks.
+def kernel_block(q, v, backward):
+    """The largest key block the kernels take for q's dtype and the head dims on
+    q's device (``pisa_attention_block_limit``: its tiles must fit the LDS), the
+    backward's too when gradients will be asked for."""
+    lib = _lib.library()
+    code = dtype_code(q, "CUDA attention supports FP16, BF16 and FP32")
+    with torch.cuda.device(q.device):
+        limit = lib.pisa_attention_block_limit(code, q.shape[-1], v.shape[-1], int(backward))
+    if limit <= 0:
+        raise ValueError("attention head dims too wide for the GPU's LDS")
+    return limit
+
+
+def split_blocks(indices, block_size, limit=MAX_KERNEL_BLOCK):
+    """Ids of blocks over `limit` keys as ids of their sub-blocks.
 
     A block of C keys is f consecutive sub-blocks of C / f keys (the largest divisor
-    of C that is at most MAX_KERNEL_BLOCK); block j becomes sub-blocks j f .. j f + f - 1
+    of C that is at most `limit`); block j becomes sub-blocks j f .. j f + f - 1
     and -1 stays -1.  The keys a row attends are the same set, so O, LSE and the
     gradients are those of the original blocks.  Returns (ids, sub-block size).
     """
-    if block_size <= MAX_KERNEL_BLOCK:
+    if block_size <= limit:
         return indices, block_size
-    sub = max(d for d in range(1, MAX_KERNEL_BLOCK + 1) if block_size % d == 0)
+    sub = max(d for d in range(1, limit + 1) if block_size % d == 0)
     f = block_size // sub
     ids = indices.long()
     parts = ids[..., None] * f + torch.arange(f, device=ids.device)
@@ -198,8 +212,14 @@ def _launch(q, k, v, indices, positions, block_size, scale, causal, packed=None)
                                   scale, causal, packed)
 
 
+def _needs_grad(q, k, v):
+    return torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad)
+
+
 def _unpacked(q, k, v, indices, block_size, scale, query_offset, causal):
-    indices, block_size = split_blocks(indices, block_size)
+    require_gpu(q, "sparse_attention")
+    indices, block_size = split_blocks(indices, block_size,
+                                       kernel_block(q, v, _needs_grad(q, k, v)))
     return _launch(q, k, v, indices, query_positions(q, k, query_offset), block_size, scale,
                    causal)
 
@@ -208,7 +228,8 @@ def _packed(q, k, v, indices, block_size, scale, cu_seqlens, query_offset, causa
     """Every document of a packed batch in one launch sequence (``sparse_attn.py:29-54``
     semantics: document-local ids and positions, keys of the row's own document)."""
     require_gpu(q, "sparse_attention")
-    indices, block_size = split_blocks(indices, block_size)
+    indices, block_size = split_blocks(indices, block_size,
+                                       kernel_block(q, v, _needs_grad(q, k, v)))
     layout = PackedKeys(packed_queries(q, k, cu_seqlens, query_offset), q.shape[1], block_size,
                         q.device)
     return _launch(q, k, v, layout.block_ids(indices), layout.positions, block_size, scale,

@@ -2143,6 +2143,22 @@ int attn_check(const AttnArgs& a, int dtype, bool backward) {
   return PISA_OK;
 }
 
+// The largest key block (128, 64, 32 or 16) whose tiles fit the device's LDS at
+// these head dims (the forward's, and the backward's when asked); 0 if none does.
+int attn_block_limit(int dtype, int head_dim, int value_dim, bool backward) {
+  const int es = dtype_size(dtype);
+  if (!es) return 0;
+  const size_t limit = (size_t)device_lds_limit();
+  AttnArgs a{};
+  a.D = head_dim;
+  a.Dv = value_dim;
+  for (int c = 128; c >= 16; c >>= 1) {
+    a.C = c;
+    if (fwd_lds(a, es, 4) <= limit && (!backward || bwd_lds(a, es) <= limit)) return c;
+  }
+  return 0;
+}
+
 static int grid_size() {
   const int cus = device_cus();
   return cus * 8;

@@ -527,6 +527,11 @@ void bind_buckets(AttnArgs& a, const Buckets& b) {
 
 }  // namespace
 
+extern "C" int32_t pisa_attention_block_limit(int32_t dtype, int32_t head_dim, int32_t value_dim,
+                                              int32_t backward) {
+  return attn_block_limit(dtype, head_dim, value_dim, backward != 0);
+}
+
 extern "C" size_t pisa_attention_workspace_size(const pisa_attn_desc* d, int32_t backward) {
   AttnPlan pl;
   if (plan_attn(d, pl)) return 0;

@@ -269,6 +269,7 @@ constexpr int kLeafTile = 256;
 int leaf_span(int dtype, int head_dim, int block_size, int branching, int group, int method,
               int64_t items);
 int attn_check(const AttnArgs& a, int dtype, bool backward);
+int attn_block_limit(int dtype, int head_dim, int value_dim, bool backward);
 // Forward partials (grouped tiles or one workgroup per slot), then the combine.
 int launch_attn_partials(int dtype, const AttnArgs& a, bool grouped, int64_t slots, hipStream_t stream);
 int launch_attn_combine(int dtype, const AttnArgs& a, int64_t items, hipStream_t stream);
