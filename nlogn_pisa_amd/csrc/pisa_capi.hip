@@ -348,8 +348,8 @@ extern "C" int pisa_leaf_scores(const pisa_qk_desc* qk, const pisa_select_params
   if (width < 1 || width > 512) return fail(PISA_ERR_UNSUPPORTED, "candidate width must be in [1, 512]");
   if (p->method == PISA_METHOD_PISA1 && !leaf_means)
     return fail(PISA_ERR_INVALID, "pisa1 leaf scoring needs the leaf means");
-  if (p->block_size < 1 || p->block_size > 128)
-    return fail(PISA_ERR_UNSUPPORTED, "leaf scoring supports block_size <= 128");
+  if (p->block_size < 1 || p->block_size > 512)
+    return fail(PISA_ERR_UNSUPPORTED, "leaf scoring supports block_size <= 512");
   if (qk->head_dim % 16 || qk->head_dim > 256)
     return fail(PISA_ERR_UNSUPPORTED, "leaf scoring needs head_dim % 16 == 0 and <= 256");
   const int G = qk->query_heads / qk->key_heads;

@@ -10,6 +10,9 @@
 // per-head support score (LogSumExp of s*S, or s*mean + s^2/2*var for pisa2,
 // top_k_pyramid_torch.py:62-79), summed over the G heads and scattered to the
 // request's slot.  PISA1 reuses the path with one support row (the leaf mean).
+// A key block too large for the LDS (512 fp32 keys of head dim 96 and up) is
+// read by the MFMA B loads straight from the key rows, which the tile's waves
+// share through L2.
 
 #include "pisa_device.h"
 #include "pisa_internal.h"
@@ -19,12 +22,12 @@
 namespace pisa {
 
 
-template <typename T>
+template <typename T, bool kStaged>
 __global__ void __launch_bounds__(256) leaf_kernel(LeafArgs a) {
   using M = Mfma<T>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   T* ks = reinterpret_cast<T*>(smem);
-  const int ldk = a.D + 16 / (int)sizeof(T);
+  const int ldk = kStaged ? a.D + 16 / (int)sizeof(T) : a.src_row;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 15, grp = lane >> 4;
   const int NT = (a.C + 15) / 16;  // key column tiles
@@ -48,16 +51,21 @@ __global__ void __launch_bounds__(256) leaf_kernel(LeafArgs a) {
     const int rows_valid = min(a.C, a.src_rows - blk * a.C);
     const int32_t* reqs = a.tile_req + (int64_t)tile * a.tile;
 
-    __syncthreads();
     const T* kb = static_cast<const T*>(a.src) + b * a.src_batch + (int64_t)blk * a.C * a.src_row +
                   (int64_t)h * a.D;
-    for (int idx = tid; idx < NT * 16 * vpr; idx += blockDim.x) {
-      const int r = idx / vpr, c = (idx % vpr) * vec;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (r < rows_valid) v = *reinterpret_cast<const uint4*>(kb + (int64_t)r * a.src_row + c);
-      *reinterpret_cast<uint4*>(ks + r * ldk + c) = v;
+    const T* kbase = kb;
+    const int last_row = max(rows_valid - 1, 0);
+    if constexpr (kStaged) {
+      __syncthreads();
+      for (int idx = tid; idx < NT * 16 * vpr; idx += blockDim.x) {
+        const int r = idx / vpr, c = (idx % vpr) * vec;
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (r < rows_valid) v = *reinterpret_cast<const uint4*>(kb + (int64_t)r * a.src_row + c);
+        *reinterpret_cast<uint4*>(ks + r * ldk + c) = v;
+      }
+      __syncthreads();
+      kbase = ks;
     }
-    __syncthreads();
 
     const int nunits = (nreq + rpu - 1) / rpu;
     for (int u = wave; u < nunits; u += 4) {
@@ -98,7 +106,10 @@ __global__ void __launch_bounds__(256) leaf_kernel(LeafArgs a) {
 #pragma unroll
             for (int nt = 0; nt < 8; ++nt) {
               if (kc + nt < NT) {
-                const typename M::frag fb = M::load(ks + ((kc + nt) * 16 + col) * ldk + k0 + M::E * grp);
+                // unstaged: rows past the block's end read its last row, and the
+                // statistics below skip those columns
+                const int kr = kStaged ? (kc + nt) * 16 + col : min((kc + nt) * 16 + col, last_row);
+                const typename M::frag fb = M::load(kbase + (int64_t)kr * ldk + k0 + M::E * grp);
                 acc[nt] = M::mma(fa, fb, acc[nt]);
               }
             }
@@ -909,14 +920,24 @@ static bool leaf_tile_path(const LeafArgs& a, int es) {
   return dim && ptrs && strides;
 }
 
+template <typename T>
+static void launch_leaf_general(const LeafArgs& a, bool staged, int grid, size_t lds, hipStream_t stream) {
+  if (staged) {
+    allow_lds((const void*)leaf_kernel<T, true>, lds);
+    PISA_TIMED("leaf", stream, hipLaunchKernelGGL((leaf_kernel<T, true>), dim3(grid), dim3(256), lds, stream, a));
+  } else {
+    PISA_TIMED("leaf", stream, hipLaunchKernelGGL((leaf_kernel<T, false>), dim3(grid), dim3(256), 0, stream, a));
+  }
+}
+
 int launch_leaf(int dtype, const LeafArgs& a, hipStream_t stream) {
   const int es = dtype_size(dtype);
   const int ldk = a.D + 16 / es;
-  const size_t lds = (size_t)((a.C + 15) / 16 * 16) * ldk * es;
+  size_t lds = (size_t)((a.C + 15) / 16 * 16) * ldk * es;
   if (a.D % 16 != 0 || a.D > 256) return fail(PISA_ERR_UNSUPPORTED, "leaf scoring needs head_dim % 16 == 0, <= 256");
   if (a.C > 512) return fail(PISA_ERR_UNSUPPORTED, "leaf scoring supports block_size <= 512");
-  if (lds > (size_t)device_lds_limit())
-    return fail(PISA_ERR_UNSUPPORTED, "key block of %zu bytes exceeds LDS", lds);
+  const bool staged = lds <= (size_t)device_lds_limit();
+  if (!staged) lds = 0;
   if (a.span > 1 && a.C > 64 &&
       !(a.span == 2 && a.scale > 0.f && span128(es, a.D, a.C, 2, a.G, a.method)))
     return fail(PISA_ERR_UNSUPPORTED, "sibling spans of blocks over 64 keys need 16-bit keys, pisa or pisa2 and two blocks");
@@ -933,20 +954,10 @@ int launch_leaf(int dtype, const LeafArgs& a, hipStream_t stream) {
   }
   if (a.span != 1) return fail(PISA_ERR_UNSUPPORTED, "sibling leaf requests need the tile kernel");
   switch (dtype) {
-    case PISA_F32:
-      allow_lds((const void*)leaf_kernel<float>, lds);
-      PISA_TIMED("leaf", stream, hipLaunchKernelGGL(leaf_kernel<float>, dim3(grid), dim3(256), lds, stream, a));
-      break;
-    case PISA_F16:
-      allow_lds((const void*)leaf_kernel<f16_t>, lds);
-      PISA_TIMED("leaf", stream, hipLaunchKernelGGL(leaf_kernel<f16_t>, dim3(grid), dim3(256), lds, stream, a));
-      break;
-    case PISA_BF16:
-      allow_lds((const void*)leaf_kernel<bf16_t>, lds);
-      PISA_TIMED("leaf", stream, hipLaunchKernelGGL(leaf_kernel<bf16_t>, dim3(grid), dim3(256), lds, stream, a));
-      break;
-    default:
-      return fail(PISA_ERR_INVALID, "unknown dtype %d", dtype);
+    case PISA_F32: launch_leaf_general<float>(a, staged, grid, lds, stream); break;
+    case PISA_F16: launch_leaf_general<f16_t>(a, staged, grid, lds, stream); break;
+    case PISA_BF16: launch_leaf_general<bf16_t>(a, staged, grid, lds, stream); break;
+    default: return fail(PISA_ERR_INVALID, "unknown dtype %d", dtype);
   }
   return check_launch("leaf");
 }

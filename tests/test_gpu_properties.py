@@ -1,7 +1,9 @@
 """Property tests on the GPU path: random supported shapes and settings, each
 example checked against the CPU oracle to the same bars as the fixed cases
 (selection ids bit-exact with tie adjudication, ``tests/parity.py``; attention
-within half an output ulp + 2e-2 for 16-bit and 1e-5 for fp32 of float64).
+within half an output ulp + 2e-2 for 16-bit and 1e-5 for fp32 of float64).  The
+attention backward is drawn for head dims up to 128 (the reference's GPU path,
+FLA, stops at 128: sparse_attn_fla.py:42-45).
 
 Examples are derandomized, so every run checks the same set.
 """
@@ -33,33 +35,35 @@ def P():
 
 @st.composite
 def selection_cases(draw):
-    block = draw(st.sampled_from([16, 32, 64, 128]))
+    block = draw(st.sampled_from([16, 32, 64, 128, 256, 512]))
     # up to 400 blocks (routing three or four levels deep at b = 2), the last one ragged
-    blocks = draw(st.one_of(st.integers(1, 40), st.integers(41, 400)))
+    blocks = draw(st.one_of(st.integers(1, 40), st.integers(41, 400 if block <= 128 else 100)))
     length = max(1, blocks * block - draw(st.integers(0, block - 1)))
     decode = draw(st.booleans())
     tq = 1 if decode else draw(st.sampled_from([None, max(1, length // 3)]))
+    ff = draw(st.booleans())
+    fr = draw(st.integers(1, 2))
     return dict(
         seed=draw(st.integers(0, 10_000)),
         batch=draw(st.integers(1, 2)),
         length=length,
         tq=tq,
         kh=draw(st.integers(1, 2)),
-        group=draw(st.sampled_from([1, 2, 3, 4, 8])),
-        dim=draw(st.sampled_from([16, 32, 64, 128])),
+        group=draw(st.sampled_from([1, 2, 3, 4, 8, 16, 32])),
+        dim=draw(st.sampled_from([16, 32, 48, 64, 96, 128, 256])),
         block=block,
-        branching=draw(st.sampled_from([2, 4])),
-        topk=draw(st.sampled_from([4, 8, 16])),
+        branching=draw(st.sampled_from([2, 4, 8])),
+        topk=draw(st.sampled_from([k for k in (2, 4, 8, 16, 32, 64) if k >= int(ff) + fr])),
         method=draw(st.sampled_from(["pisa", "pisa2", "pisa1"])),
-        ff=draw(st.booleans()),
-        fr=draw(st.integers(1, 2)),
+        ff=ff,
+        fr=fr,
         dtype=draw(st.sampled_from(["fp32", "bf16", "fp16"])),
         schedule=draw(st.sampled_from(["auto", "grouped", "fused"])),
         needles=draw(st.sampled_from([0.0, 0.05])),
     )
 
 
-@settings(max_examples=40, **SETTINGS)
+@settings(max_examples=60, **SETTINGS)
 @given(case=selection_cases())
 def test_selection_random_shapes(P, case):
     c = case
@@ -77,23 +81,28 @@ def test_selection_random_shapes(P, case):
 
 @st.composite
 def attention_cases(draw):
-    block = draw(st.sampled_from([16, 32, 64, 128]))
+    block = draw(st.sampled_from([16, 32, 48, 64, 96, 128, 256]))
     length = draw(st.integers(min_value=1, max_value=12 * block))
     decode = draw(st.booleans())
+    dim = draw(st.sampled_from([16, 32, 48, 64, 96, 128, 256]))
+    backward = draw(st.booleans()) and dim <= 128
+    # value rows of another width (forward only, and the backward's padded rows)
+    value_dim = draw(st.sampled_from([dim, dim, 32, 64])) if dim <= 128 else dim
     return dict(
         seed=draw(st.integers(0, 10_000)),
         batch=draw(st.integers(1, 2)),
         length=length,
         tq=1 if decode else draw(st.integers(1, length)),
         kh=draw(st.integers(1, 2)),
-        group=draw(st.sampled_from([1, 2, 3, 4, 8])),
-        dim=draw(st.sampled_from([16, 32, 64, 128])),
+        group=draw(st.sampled_from([1, 2, 3, 4, 8, 16])),
+        dim=dim,
+        value_dim=value_dim,
         block=block,
         topk=draw(st.integers(1, 8)),
         causal=draw(st.booleans()),
         dtype=draw(st.sampled_from(["fp32", "bf16", "fp16"])),
         duplicates=draw(st.booleans()),
-        backward=draw(st.booleans()),
+        backward=backward,
     )
 
 
@@ -107,7 +116,7 @@ def _random_ids(rng, batch, tq, kh, topk, blocks, duplicates):
     return ids
 
 
-@settings(max_examples=40, **SETTINGS)
+@settings(max_examples=60, **SETTINGS)
 @given(case=attention_cases())
 def test_attention_random_shapes(P, case):
     c = case
@@ -116,6 +125,9 @@ def test_attention_random_shapes(P, case):
     q, k, v = structured_qkv(c["seed"], c["batch"], c["length"], c["group"] * c["kh"], c["kh"], c["dim"],
                              dt, offset_block=c["block"])
     q = np.ascontiguousarray(q[:, c["length"] - c["tq"]:])
+    if c["value_dim"] != c["dim"]:
+        v = O.round_storage(np.random.default_rng(c["seed"] + 2).standard_normal(
+            (c["batch"], c["length"], c["kh"], c["value_dim"])).astype(np.float32), dt)
     rng = np.random.default_rng(c["seed"] + 1)
     blocks = -(-c["length"] // c["block"])
     ids = _random_ids(rng, c["batch"], c["tq"], c["kh"], c["topk"], blocks, c["duplicates"])

@@ -179,6 +179,10 @@ LEAF_SHAPES = [
     (1, 1024, 64, 2, 32, 32, "bf16"),     # 32 query heads per kv head: a request spans two units
     (1, 1000, 4, 2, 16, 16, "fp32"),
     (1, 700, 6, 2, 128, 128, "fp16"),     # 3 heads per kv head (padded to 4), tail block
+    # key blocks larger than the LDS (200-270 KB): MFMA B loads from the key rows
+    (1, 1500, 4, 2, 96, 512, "fp32"),
+    (1, 1100, 2, 1, 128, 512, "fp32"),
+    (1, 600, 8, 2, 256, 256, "fp32"),
 ]
 
 
