@@ -154,3 +154,214 @@ def test_attention_random_shapes(P, case):
     for name, mine, ref in zip(("dq", "dk", "dv"), (qg.grad, kg.grad, vg.grad), grads):
         err = excess_error(mine.float().cpu().numpy(), ref, dt)
         assert err <= TOL[dt], f"{name} excess error {err}"
+
+
+# ---------------------------------------------------------------- packed documents
+
+def _bounds(lengths):
+    return np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64).tolist()
+
+
+@st.composite
+def packed_selection_cases(draw):
+    block = draw(st.sampled_from([16, 32, 64, 128]))
+    docs = draw(st.integers(1, 6))
+    lengths = draw(st.lists(st.one_of(st.integers(1, 2 * block), st.integers(2 * block, 30 * block)),
+                            min_size=docs, max_size=docs))
+    ff = draw(st.booleans())
+    fr = draw(st.integers(1, 2))
+    topk = draw(st.sampled_from([k for k in (2, 4, 8, 16) if k >= int(ff) + fr]))
+    return dict(
+        seed=draw(st.integers(0, 10_000)),
+        lengths=lengths,
+        decode=draw(st.booleans()),        # one query per document
+        kh=draw(st.integers(1, 2)),
+        group=draw(st.sampled_from([1, 2, 4, 8])),
+        dim=draw(st.sampled_from([16, 32, 64, 128])),
+        block=block,
+        branching=draw(st.sampled_from([b for b in (2, 4, 8) if b * topk <= 512])),
+        topk=topk,
+        method=draw(st.sampled_from(["pisa", "pisa2", "pisa1"])),
+        ff=ff,
+        fr=fr,
+        dtype=draw(st.sampled_from(["fp32", "bf16", "fp16"])),
+        schedule=draw(st.sampled_from(["auto", "grouped", "fused"])),
+        index_dtype=draw(st.sampled_from([torch.int32, torch.int64])),
+    )
+
+
+@settings(max_examples=30, **SETTINGS)
+@given(case=packed_selection_cases())
+def test_packed_selection_random_documents(P, case):
+    """cu_seqlens selection (``top_k_pyramid.py:73-86``): every document's ids equal
+    its selection alone (own depth, or the longest document's for fused routing),
+    and that selection meets the oracle bar."""
+    import parity
+    c = case
+    print(f"packed select property {c}", flush=True)
+    dt, block, b = c["dtype"], c["block"], c["branching"]
+    bounds = _bounds(c["lengths"])
+    docs = list(zip(bounds[:-1], bounds[1:]))
+    q, k = structured_qkv(c["seed"], 1, bounds[-1], c["group"] * c["kh"], c["kh"], c["dim"], dt,
+                          offset_block=block, value=False)
+    if c["decode"]:
+        q = np.ascontiguousarray(q[:, :len(docs)])
+    qg, kg = to_gpu(q, dt), to_gpu(k, dt)
+    cu = torch.tensor(bounds, dtype=c["index_dtype"], device="cuda")
+    kw = dict(force_first=c["ff"], force_recent=c["fr"], branching=b)
+    out = P.select_blocks(qg, kg, c["method"], block, c["topk"], cu_seqlens=cu,
+                          routing_schedule=c["schedule"], **kw).cpu().numpy()
+    decode = q.shape[1] != k.shape[1]
+    grouped = c["schedule"] == "grouped" or (c["schedule"] == "auto" and c["method"] != "pisa1"
+                                             and not decode)
+    longest = max(-(-(e - s) // block) for s, e in docs)
+    geometry = None if grouped else O.routing_geometry(longest, c["topk"], b)
+    for d, (s, e) in enumerate(docs):
+        rows = slice(d, d + 1) if decode else slice(s, e)
+        qd, kd = q[:, rows], k[:, s:e]
+        ids, trace = P.selection.select_blocks_traced(
+            qg[:, rows], kg[:, s:e], c["method"], block, c["topk"],
+            routing_schedule="grouped" if grouped else "fused", geometry=geometry, **kw)
+        ids, trace = ids.cpu().numpy(), trace.cpu().numpy()
+        assert np.array_equal(out[:, rows], ids), f"document {d} [{s}, {e})"
+        tq = qd.shape[1]
+        tokens = np.unique(np.linspace(0, tq - 1, min(tq, 48)).astype(np.int64))
+        levels = O.build_pyramid(kd, block, b, None, dt)
+        pos = O.query_positions(1, tq, e - s)
+        res = parity.selection_parity(qd, kd, ids, trace, tokens, c["method"], block, c["topk"],
+                                      c["ff"], c["fr"], b, levels, pos, geometry=geometry)
+        assert not res["failures"], f"document {d}: {res['failures'][:3]}"
+
+
+@st.composite
+def packed_attention_cases(draw):
+    block = draw(st.sampled_from([16, 32, 64, 128]))
+    docs = draw(st.integers(1, 5))
+    lengths = draw(st.lists(st.integers(1, 10 * block), min_size=docs, max_size=docs))
+    dim = draw(st.sampled_from([16, 32, 64, 128, 256]))
+    return dict(
+        seed=draw(st.integers(0, 10_000)),
+        lengths=lengths,
+        decode=draw(st.booleans()),
+        kh=draw(st.integers(1, 2)),
+        group=draw(st.sampled_from([1, 2, 4, 8])),
+        dim=dim,
+        block=block,
+        topk=draw(st.integers(1, 8)),
+        causal=draw(st.booleans()),
+        dtype=draw(st.sampled_from(["fp32", "bf16", "fp16"])),
+        duplicates=draw(st.booleans()),
+        backward=draw(st.booleans()) and dim <= 128,
+    )
+
+
+@settings(max_examples=30, **SETTINGS)
+@given(case=packed_attention_cases())
+def test_packed_attention_random_documents(P, case):
+    """cu_seqlens attention (``sparse_attn.py:29-54``): document-local ids (padding,
+    past the document's blocks, repeated) and positions; O, LSE and the gradients
+    equal the per-document oracle, concatenated."""
+    c = case
+    print(f"packed attention property {c}", flush=True)
+    dt, block = c["dtype"], c["block"]
+    bounds = _bounds(c["lengths"])
+    docs = list(zip(bounds[:-1], bounds[1:]))
+    qh = c["group"] * c["kh"]
+    q, k, v = structured_qkv(c["seed"], 1, bounds[-1], qh, c["kh"], c["dim"], dt, offset_block=block)
+    if c["decode"]:
+        q = np.ascontiguousarray(q[:, :len(docs)])
+    decode = q.shape[1] != k.shape[1]
+    rng = np.random.default_rng(c["seed"] + 3)
+    parts = []
+    for s, e in docs:
+        tq = 1 if decode else e - s
+        parts.append(_random_ids(rng, 1, tq, c["kh"], c["topk"], -(-(e - s) // block), c["duplicates"]))
+    ids = np.concatenate(parts, 1)
+    cu = torch.tensor(bounds, dtype=torch.int32, device="cuda")
+    ref_o, ref_l, ref_g = [], [], [[], [], []]
+    dout = O.round_storage(rng.standard_normal(q.shape).astype(np.float32), dt)
+    for d, (s, e) in enumerate(docs):
+        rows = slice(d, d + 1) if decode else slice(s, e)
+        pos = O.query_positions(1, rows.stop - rows.start, e - s, None)
+        o_, l_ = O.sparse_attention(q[:, rows], k[:, s:e], v[:, s:e], ids[:, rows], block,
+                                    positions=pos, causal=c["causal"])
+        ref_o.append(o_)
+        ref_l.append(l_)
+        if c["backward"]:
+            g_ = O.sparse_attention_backward(q[:, rows], k[:, s:e], v[:, s:e], ids[:, rows],
+                                             dout[:, rows], block, positions=pos, causal=c["causal"])
+            for j in range(3):
+                ref_g[j].append(g_[j])
+    ref_o, ref_l = np.concatenate(ref_o, 1), np.concatenate(ref_l, 1)
+    ids_gpu = torch.from_numpy(ids).cuda()
+    qg, kg, vg = (to_gpu(x, dt).requires_grad_(c["backward"]) for x in (q, k, v))
+    out, lse = P.sparse_attention_with_lse(qg, kg, vg, ids_gpu, block, cu_seqlens=cu,
+                                           causal=c["causal"])
+    assert excess_error(out.detach().float().cpu().numpy(), ref_o, dt) <= TOL[dt]
+    lse = lse.cpu().numpy()
+    fin = np.isfinite(ref_l)
+    assert np.array_equal(np.isneginf(lse), ~fin)
+    if fin.any():
+        assert np.abs(lse[fin] - ref_l[fin]).max() <= max(TOL[dt], 1e-5)
+    if c["backward"]:
+        out.backward(to_gpu(dout, dt))
+        for name, mine, ref in zip(("dq", "dk", "dv"), (qg.grad, kg.grad, vg.grad), ref_g):
+            err = excess_error(mine.float().cpu().numpy(), np.concatenate(ref, 1), dt)
+            assert err <= TOL[dt], f"{name} excess error {err}"
+
+
+# ---------------------------------------------------------------- decode cache
+
+@st.composite
+def cache_cases(draw):
+    block = draw(st.sampled_from([16, 32, 64, 128]))
+    return dict(
+        seed=draw(st.integers(0, 10_000)),
+        prefill=draw(st.integers(1, 40 * block)),
+        chunks=draw(st.lists(st.one_of(st.just(1), st.integers(1, 3 * block)), min_size=1, max_size=8)),
+        kh=draw(st.integers(1, 2)),
+        group=draw(st.sampled_from([1, 2, 4, 8])),
+        dim=draw(st.sampled_from([16, 32, 64, 128])),
+        block=block,
+        branching=draw(st.sampled_from([2, 4, 8])),
+        topk=draw(st.sampled_from([4, 8, 16])),
+        method=draw(st.sampled_from(["pisa", "pisa2", "pisa1"])),
+        dtype=draw(st.sampled_from(["fp32", "bf16", "fp16"])),
+        batch=draw(st.integers(1, 2)),
+    )
+
+
+@settings(max_examples=30, **SETTINGS)
+@given(case=cache_cases())
+def test_cache_random_appends(P, case):
+    """``PyramidCache`` (``attention_cache.py:50-140``) under a random prefill and
+    append sequence: every level bit-exact against a rebuild after each append, and
+    a decode selection through the cache equal to one that builds its own pyramid,
+    which meets the oracle bar."""
+    c = case
+    print(f"cache property {c}", flush=True)
+    dt, block, b = c["dtype"], c["block"], c["branching"]
+    total = c["prefill"] + sum(c["chunks"])
+    q, k = structured_qkv(c["seed"], c["batch"], total, c["group"] * c["kh"], c["kh"], c["dim"], dt,
+                          offset_block=block, value=False, tq=1)
+    kg, qg = to_gpu(k, dt), to_gpu(q, dt)
+    cache = P.PyramidCache.from_keys(kg[:, :c["prefill"]], block_size=block, branching=b)
+    end = c["prefill"]
+    for chunk in c["chunks"]:
+        cache.append(kg[:, end:end + chunk])
+        end += chunk
+        assert cache.length == end
+        want = O.build_pyramid(k[:, :end], block, b, None, dt)
+        assert cache.lengths.tolist() == [x.shape[1] for x in want]
+        for level, (mine, ref) in enumerate(zip(cache.levels, want)):
+            np.testing.assert_array_equal(mine.float().cpu().numpy(), ref,
+                                          err_msg=f"after {end} tokens, level {level}")
+    kw = dict(method=c["method"], block_size=block, topk=c["topk"], query_offset=total - 1,
+              force_first=True, force_recent=1, branching=b)
+    ids = P.select_blocks(qg, cache.keys, pyramid=cache, **kw)
+    alone = P.select_blocks(qg, kg, **kw)
+    assert torch.equal(ids, alone)
+    traced, trace = _run_select(P, q, k, dt, c["method"], block, c["topk"], True, 1, total - 1,
+                                "auto", b)
+    assert np.array_equal(traced, ids.cpu().numpy())
+    _check_against(q, k, dt, c["method"], block, c["topk"], True, 1, total - 1, b, traced, trace)
