@@ -32,6 +32,7 @@ struct BsaArgs {
   const int64_t* positions;
   int64_t pos_batch;
   int T, M, Hkv, G, C, K, W, log_w, force_first, force_recent;
+  int D;  // head dim: q's head stride and the means' row width (<= the kernel's HD)
   float scale;
   int64_t* out;  // [B, T, Hkv, K]
 };
@@ -144,7 +145,9 @@ __device__ __forceinline__ int pick4(const int (&a)[4], int t) {
   return t == 0 ? a[0] : t == 1 ? a[1] : t == 2 ? a[2] : a[3];
 }
 
-template <typename T, int HD, int GP, int NC>
+// PAD: head dims below HD (a multiple of 16); the dimensions past a.D are zero
+// in both MFMA operands (their chunks load the row's first chunk, then clear).
+template <typename T, int HD, int GP, int NC, bool PAD>
 __global__ void __launch_bounds__(256) bsa_kernel(BsaArgs a) {
   constexpr int E = sizeof(T) == 4 ? 1 : (HD % 32 == 0 ? 8 : 4);
   typedef MfmaOp<T, E> Op;
@@ -173,6 +176,10 @@ __global__ void __launch_bounds__(256) bsa_kernel(BsaArgs a) {
     max_cmp = max(max_cmp, cmp[tt]);
   }
 
+  const int D = PAD ? a.D : HD;
+  // dimension chunk s of this lane group lies inside the head dim
+  auto inside = [&](int s) { return !PAD || 4 * E * s + E * grp < D; };
+
   // scaled query rows, rounded to the storage dtype (bsa_torch.py:80-81)
   frag qf[RT][DS];
 #pragma unroll
@@ -181,22 +188,32 @@ __global__ void __launch_bounds__(256) bsa_kernel(BsaArgs a) {
     const bool live = tok < 4 && hd < a.G;
     const T* row = static_cast<const T*>(a.q) + (int64_t)b * a.q_batch +
                    (int64_t)min(t0 + tok, a.T - 1) * a.q_token +
-                   (int64_t)(h * a.G + min(hd, a.G - 1)) * HD + E * grp;
+                   (int64_t)(h * a.G + min(hd, a.G - 1)) * D + E * grp;
 #pragma unroll
     for (int s = 0; s < DS; ++s) {
       float x[E];
-      load_f<E>(row + 4 * E * s, x);
+      load_f<E>(row + (inside(s) ? 4 * E * s : 0), x);
 #pragma unroll
-      for (int e = 0; e < E; ++e) Op::set(qf[rt][s], e, live ? x[e] * a.scale : 0.f);
+      for (int e = 0; e < E; ++e) Op::set(qf[rt][s], e, live && inside(s) ? x[e] * a.scale : 0.f);
     }
   }
 
-  const T* means = static_cast<const T*>(a.means) + (int64_t)b * a.M * a.Hkv * HD + (int64_t)h * HD +
+  const T* means = static_cast<const T*>(a.means) + (int64_t)b * a.M * a.Hkv * D + (int64_t)h * D +
                    E * grp;
-  const int64_t mrow = (int64_t)a.Hkv * HD;
+  const int64_t mrow = (int64_t)a.Hkv * D;
   auto logits = [&](int block, f4 (&acc)[RT]) {
     frag bf[DS];
-    load_row_frags<E>(means + (int64_t)min(block, a.M - 1) * mrow, bf);
+    if constexpr (PAD) {
+      const T* mr = means + (int64_t)min(block, a.M - 1) * mrow;
+#pragma unroll
+      for (int s = 0; s < DS; ++s) {
+        frag f;
+        load_frags(mr + (inside(s) ? 4 * E * s : 0), *reinterpret_cast<frag(*)[1]>(&f));
+        bf[s] = inside(s) ? f : frag{};
+      }
+    } else {
+      load_row_frags<E>(means + (int64_t)min(block, a.M - 1) * mrow, bf);
+    }
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
       acc[rt] = f4{0.f, 0.f, 0.f, 0.f};
@@ -328,34 +345,42 @@ __global__ void __launch_bounds__(256) bsa_kernel(BsaArgs a) {
   }
 }
 
-template <typename T, int HD, int GP>
+template <typename T, int HD, int GP, bool PAD>
 static void launch_bsa_w(const BsaArgs& a, dim3 grid, hipStream_t stream) {
   if (a.W <= 16) {
-    PISA_TIMED("bsa", stream, hipLaunchKernelGGL((bsa_kernel<T, HD, GP, 1>), grid, dim3(256), 0, stream, a));
+    PISA_TIMED("bsa", stream, hipLaunchKernelGGL((bsa_kernel<T, HD, GP, 1, PAD>), grid, dim3(256), 0, stream, a));
   } else if (a.W == 32) {
-    PISA_TIMED("bsa", stream, hipLaunchKernelGGL((bsa_kernel<T, HD, GP, 2>), grid, dim3(256), 0, stream, a));
+    PISA_TIMED("bsa", stream, hipLaunchKernelGGL((bsa_kernel<T, HD, GP, 2, PAD>), grid, dim3(256), 0, stream, a));
   } else if (a.W == 64) {
-    PISA_TIMED("bsa", stream, hipLaunchKernelGGL((bsa_kernel<T, HD, GP, 4>), grid, dim3(256), 0, stream, a));
+    PISA_TIMED("bsa", stream, hipLaunchKernelGGL((bsa_kernel<T, HD, GP, 4, PAD>), grid, dim3(256), 0, stream, a));
   } else {
-    PISA_TIMED("bsa", stream, hipLaunchKernelGGL((bsa_kernel<T, HD, GP, 8>), grid, dim3(256), 0, stream, a));
+    PISA_TIMED("bsa", stream, hipLaunchKernelGGL((bsa_kernel<T, HD, GP, 8, PAD>), grid, dim3(256), 0, stream, a));
   }
 }
 
-template <typename T, int HD>
+template <typename T, int HD, bool PAD>
 static void launch_bsa_g(const BsaArgs& a, dim3 grid, hipStream_t stream) {
-  if (a.G <= 4) launch_bsa_w<T, HD, 4>(a, grid, stream);
-  else if (a.G <= 16) launch_bsa_w<T, HD, 16>(a, grid, stream);
-  else launch_bsa_w<T, HD, 32>(a, grid, stream);
+  if (a.G <= 4) launch_bsa_w<T, HD, 4, PAD>(a, grid, stream);
+  else if (a.G <= 16) launch_bsa_w<T, HD, 16, PAD>(a, grid, stream);
+  else launch_bsa_w<T, HD, 32, PAD>(a, grid, stream);
 }
 
+// Head dims 16, 32, 64 and 128 run exact; other multiples of 16 up to 256 run
+// in the next of 64, 128 and 256 with zero dimensions (bsa_triton.py:108 pads to
+// a power of two as well).
 template <typename T>
 static int launch_bsa(const BsaArgs& a, int D, dim3 grid, hipStream_t stream) {
   switch (D) {
-    case 16: launch_bsa_g<T, 16>(a, grid, stream); break;
-    case 32: launch_bsa_g<T, 32>(a, grid, stream); break;
-    case 64: launch_bsa_g<T, 64>(a, grid, stream); break;
-    case 128: launch_bsa_g<T, 128>(a, grid, stream); break;
-    default: return fail(PISA_ERR_UNSUPPORTED, "BSA routing supports head_dim 16, 32, 64 or 128");
+    case 16: launch_bsa_g<T, 16, false>(a, grid, stream); break;
+    case 32: launch_bsa_g<T, 32, false>(a, grid, stream); break;
+    case 64: launch_bsa_g<T, 64, false>(a, grid, stream); break;
+    case 128: launch_bsa_g<T, 128, false>(a, grid, stream); break;
+    default:
+      if (D % 16 != 0 || D > 256)
+        return fail(PISA_ERR_UNSUPPORTED, "BSA routing supports head dims that are multiples of 16, up to 256");
+      if (D < 64) launch_bsa_g<T, 64, true>(a, grid, stream);
+      else if (D < 128) launch_bsa_g<T, 128, true>(a, grid, stream);
+      else launch_bsa_g<T, 256, true>(a, grid, stream);
   }
   return check_launch("bsa");
 }
@@ -421,6 +446,7 @@ extern "C" int pisa_bsa_select(const pisa_qk_desc* qk, int32_t block_size, int32
   while ((1 << a.log_w) < a.W) ++a.log_w;
   a.force_first = force_first ? 1 : 0;
   a.force_recent = force_recent;
+  a.D = qk->head_dim;
   a.scale = (float)(1.0 / sqrt((double)qk->head_dim));
   a.out = out;
   const int units = (qk->query_tokens + 3) / 4;

@@ -92,6 +92,12 @@ CASES = [
     ("w8", "fp32", 1, 200, None, 2, 1, 32, 8, 4, False, 2, None),
     ("decode", "bf16", 3, 20000, 1, 32, 2, 64, 64, 8, True, 2, None),
     ("suffix", "bf16", 2, 5000, 77, 4, 2, 128, 64, 8, True, 2, 4000),
+    # head dims outside 16/32/64/128: zero-padded products
+    ("d48", "bf16", 1, 2000, None, 8, 2, 48, 32, 8, True, 2, None),
+    ("d96-fp32", "fp32", 1, 1500, None, 4, 1, 96, 64, 8, True, 1, None),
+    ("d80-g32", "fp16", 1, 1200, None, 32, 1, 80, 16, 16, True, 2, None),
+    ("d256", "bf16", 2, 3000, None, 16, 2, 256, 64, 16, True, 2, None),
+    ("d160-fp32-decode", "fp32", 2, 5000, 1, 8, 2, 160, 64, 8, False, 2, None),
 ]
 
 
@@ -142,6 +148,6 @@ def test_bsa_errors(P):
         P.bsa_fn(q, k, 8, 2, force_first=True, force_recent=3)
     with pytest.raises(ValueError, match="block_size <= 128"):
         P.bsa_fn(q, k, 256, 8)
-    with pytest.raises(P._lib.PisaError, match="head_dim"):
-        P.bsa_fn(torch.zeros(1, 64, 4, 48, device="cuda", dtype=torch.bfloat16),
-                 torch.zeros(1, 64, 2, 48, device="cuda", dtype=torch.bfloat16), 16, 4)
+    with pytest.raises(P._lib.PisaError, match="multiples of 16"):
+        P.bsa_fn(torch.zeros(1, 64, 4, 40, device="cuda", dtype=torch.bfloat16),
+                 torch.zeros(1, 64, 2, 40, device="cuda", dtype=torch.bfloat16), 16, 4)

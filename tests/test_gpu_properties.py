@@ -365,3 +365,59 @@ def test_cache_random_appends(P, case):
                                 "auto", b)
     assert np.array_equal(traced, ids.cpu().numpy())
     _check_against(q, k, dt, c["method"], block, c["topk"], True, 1, total - 1, b, traced, trace)
+
+
+# ---------------------------------------------------------------- flat BSA selection
+
+@st.composite
+def bsa_cases(draw):
+    block = draw(st.sampled_from([4, 8, 16, 32, 64, 128]))
+    blocks = draw(st.one_of(st.integers(1, 40), st.integers(41, 300)))
+    length = max(1, blocks * block - draw(st.integers(0, block - 1)))
+    kind = draw(st.sampled_from(["prefill", "decode", "suffix"]))
+    ff = draw(st.booleans())
+    fr = draw(st.integers(1, 3))
+    return dict(
+        seed=draw(st.integers(0, 10_000)),
+        batch=draw(st.integers(1, 2)),
+        length=length,
+        kind=kind,
+        kh=draw(st.integers(1, 2)),
+        group=draw(st.sampled_from([1, 2, 3, 4, 8, 16, 32])),
+        dim=draw(st.sampled_from([16, 32, 48, 64, 96, 128, 160, 256])),
+        block=block,
+        topk=draw(st.sampled_from([k for k in (2, 4, 8, 16, 32, 64) if k >= int(ff) + fr])),
+        ff=ff,
+        fr=fr,
+        dtype=draw(st.sampled_from(["fp32", "bf16", "fp16"])),
+    )
+
+
+@settings(max_examples=40, **SETTINGS)
+@given(case=bsa_cases())
+def test_bsa_random_shapes(P, case):
+    """``bsa_fn`` (``bsa_torch.py:8-106``) on random supported shapes against the
+    oracle: ids bit-exact including slot order, ties within 1e-4 adjudicated."""
+    from parity import adjudicate_flat
+    c = case
+    print(f"bsa property {c}", flush=True)
+    dt, n = c["dtype"], c["length"]
+    q, k = structured_qkv(c["seed"], c["batch"], n, c["group"] * c["kh"], c["kh"], c["dim"], dt,
+                          offset_block=c["block"], value=False)
+    offset = None
+    if c["kind"] == "decode":
+        q = np.ascontiguousarray(q[:, n - 1:])
+    elif c["kind"] == "suffix" and n > 2:
+        offset = n // 3
+        q = np.ascontiguousarray(q[:, offset:offset + max(1, n // 3)])
+    got = P.bsa_fn(to_gpu(q, dt), to_gpu(k, dt), c["block"], c["topk"], query_offset=offset,
+                   force_first=c["ff"], force_recent=c["fr"]).cpu().numpy()
+    assert got.shape == (c["batch"], q.shape[1], c["kh"], c["topk"])
+    tokens = np.unique(np.linspace(0, q.shape[1] - 1, min(q.shape[1], 128)).astype(np.int64))
+    pos = O.query_positions(c["batch"], q.shape[1], n, offset)[:, tokens]
+    qs, got = q[:, tokens], got[:, tokens]
+    want = O.bsa_select(qs, k, c["block"], c["topk"], pos, c["ff"], c["fr"], dt)
+    if not np.array_equal(got, want):
+        scores, ids, _ = O.bsa_scores(qs, k, c["block"], pos, c["ff"], c["fr"], dt)
+        differ, exempt, failures = adjudicate_flat(got, want, scores, ids)
+        assert not failures, f"{len(failures)} of {differ} differing rows, e.g. {failures[:3]}"
