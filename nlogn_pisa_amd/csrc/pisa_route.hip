@@ -856,9 +856,10 @@ __global__ void __launch_bounds__(64) route_grouped_kernel(RouteArgs a) {
 
 // ------------------------------------------------------------------ dense routing levels
 //
-// route_dense_kernel: one routing level scored for every node and every item,
-// for levels with few nodes compared with the candidates a row scores there
-// (the top levels of a prefill).  Support scores are the same as
+// route_dense_kernel: one routing level scored for every visible node and every
+// item, for levels with few nodes compared with the candidates a row scores
+// there (the top levels of a prefill); a wave stops after the last node its
+// latest query can see (nodes past it are left unwritten and never read).  Support scores are the same as
 // route_grouped_kernel's (block_scores, top_k_pyramid_torch.py:48-80) but a
 // wave owns 4 P items of one (batch, kv head) - P = 16 / Gp items of Gp padded
 // heads fill the 16 columns of one query tile, four tiles side by side - and
@@ -871,6 +872,22 @@ __global__ void __launch_bounds__(64) route_grouped_kernel(RouteArgs a) {
 // Scores of one wave wait in LDS for 64 nodes of its 16 items, then go out as
 // whole 256-byte pieces of the items' rows (rows padded to 64 nodes).
 constexpr int kDenseChunk = 64;
+
+// Nodes of dense level `level` that any of tokens [t0, t1) of batch b can see:
+// the route reads a node's score only when the node is scoreable, so visible
+// (it starts at or before the query's position, n * span <= pos), and nodes past
+// the latest position's last visible one need no score.  Every lane of the wave
+// returns the same count.
+__device__ __forceinline__ int dense_visible(const RouteArgs& a, int b, int t0, int t1, int level,
+                                             int M) {
+  long long p = -1;
+  for (int t = t0 + (int)(threadIdx.x & 63); t < min(t1, a.T); t += 64)
+    p = max(p, (long long)a.positions[(int64_t)b * a.pos_batch + t]);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) p = max(p, __shfl_xor(p, o));
+  const int64_t span = ipow(a.branching, level) * a.C;
+  return p < 0 ? 0 : (int)min<int64_t>(M, p / span + 1);
+}
 
 template <typename T, int HD, int RR, int MODE>
 __global__ void __launch_bounds__(256) route_dense_kernel(RouteArgs a) {
@@ -914,7 +931,8 @@ __global__ void __launch_bounds__(256) route_dense_kernel(RouteArgs a) {
                   ((int64_t)a.offsets[src_level] * a.Hkv + h) * HD;
   const int64_t rstride = (int64_t)a.Hkv * HD;
   const int len = a.lengths[src_level];
-  const int nrows = own ? M : M * R;
+  const int visible = dense_visible(a, b, t0, t0 + NCT * P, level, M);  // the causal cut
+  const int nrows = own ? visible : visible * R;
   const int ntile = (nrows + 15) / 16;
   float* out = a.dense[level];
   const int64_t item0 = ((int64_t)b * a.T + t0) * a.Hkv + h;  // item of token t0
@@ -1059,7 +1077,10 @@ __global__ void __launch_bounds__(256) route_dense_lds_kernel(RouteArgs a) {
                   ((int64_t)a.offsets[src_level] * a.Hkv + h) * HD;
   const int64_t rstride = (int64_t)a.Hkv * HD;
   const int len = a.lengths[src_level];
-  const int nrows = own ? M : M * R;
+  // the causal cut, over the workgroup's tokens (the same count in every wave)
+  const int tw = (blockIdx.x - bh * per_bh) * 4 * NCT * P;
+  const int visible = dense_visible(a, b, tw, tw + 4 * NCT * P, level, M);
+  const int nrows = own ? visible : visible * R;
   const int ntile = (nrows + 15) / 16;
   const int nchunk = (ntile + kDenseCT - 1) / kDenseCT;
   float* out = a.dense[level];
