@@ -453,6 +453,10 @@ def main():
     r_int = sum(v for lvl, v in counts.items() if isinstance(lvl, int) and lvl > 0
                 and lvl not in dense)
     r_dense = sum(v for lvl, v in counts.items() if isinstance(lvl, int) and lvl in dense)
+    # nodes of each dense level the items can see (the dense kernels stop after the
+    # node visible to their latest query): the sum over items of min(nodes, pos // span + 1)
+    visible = {lvl: int(torch.clamp(positions // (w.branching ** lvl * w.block_size) + 1,
+                                    max=n).sum()) * w.key_heads for lvl, n in dense.items()}
     span = counts.get("leaf_span", 1)
     r_span = counts.get("leaf_requests", r_leaf)
     # algorithmic bytes / flops per launch of each hot kernel
@@ -464,13 +468,13 @@ def main():
         "route": {"bound": "hbm",
                   "bytes": w.batch * w.tokens * w.query_heads * D * e + r_int * w.branching * D * e
                   + r_dense * 4 + items * width * 5 + fused_leaf},
-        # per dense level: the query rows, each wave's pass over the level's support
-        # rows (16 items per wave), the score rows written
+        # per dense level: the query rows, each wave's pass over the visible support
+        # rows (16 items per wave), the visible nodes' scores written
         "route_dense": {"bound": "mfma",
                         "bytes": sum(w.batch * w.tokens * w.query_heads * D * e
-                                     + items / 16 * n * w.branching * D * e
-                                     + items * (-(-n // 64) * 64) * 4 for n in dense.values()),
-                        "flops": sum(2 * items * G * n * w.branching * D for n in dense.values())},
+                                     + v / 16 * w.branching * D * e + v * 4
+                                     for v in visible.values()),
+                        "flops": sum(2 * G * v * w.branching * D for v in visible.values())},
         "leaf": {"bound": "hbm",   # key spans per tile, q rows once per span request, scores
                  "bytes": leaf_tiles * span * w.block_size * D * e + r_span * (G * D * e + 4)
                  + r_leaf * 4,
