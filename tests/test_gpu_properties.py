@@ -26,6 +26,20 @@ SETTINGS = dict(deadline=None, derandomize=True, database=None,
                                        HealthCheck.function_scoped_fixture])
 
 
+def _offsets(kind, seed, batch, tq, length):
+    """query_offset forms (``validation.py:38-56``): None (the queries end at the
+    keys' end), a scalar, or one offset per batch element; (numpy form for the
+    oracle, the form passed to the GPU operators)."""
+    if kind == "none" or tq is None:
+        return None, None
+    rng = np.random.default_rng(seed + 7)
+    if kind == "scalar":
+        off = int(rng.integers(0, length - tq + 1))
+        return off, off
+    off = rng.integers(0, length - tq + 1, size=batch).astype(np.int64)
+    return off, torch.from_numpy(off).cuda()
+
+
 @pytest.fixture(scope="module")
 def P():
     import nlogn_pisa_amd
@@ -60,6 +74,7 @@ def selection_cases(draw):
         dtype=draw(st.sampled_from(["fp32", "bf16", "fp16"])),
         schedule=draw(st.sampled_from(["auto", "grouped", "fused"])),
         needles=draw(st.sampled_from([0.0, 0.05])),
+        offset=draw(st.sampled_from(["none", "scalar", "per_batch"])),
     )
 
 
@@ -71,11 +86,13 @@ def test_selection_random_shapes(P, case):
     q, k = structured_qkv(c["seed"], c["batch"], c["length"], c["group"] * c["kh"], c["kh"], c["dim"],
                           c["dtype"], offset_block=c["block"], needles=c["needles"], value=False,
                           tq=c["tq"])
+    tq = q.shape[1] if c["tq"] is not None else None
+    off_np, off_gpu = _offsets(c["offset"], c["seed"], c["batch"], tq, c["length"])
     ids, trace = _run_select(P, q, k, c["dtype"], c["method"], c["block"], c["topk"], c["ff"],
-                             c["fr"], None, c["schedule"], c["branching"])
+                             c["fr"], off_gpu, c["schedule"], c["branching"])
     assert ids.shape == (c["batch"], q.shape[1], c["kh"], c["topk"])
     tokens = np.unique(np.linspace(0, q.shape[1] - 1, min(q.shape[1], 96)).astype(np.int64))
-    _check_against(q, k, c["dtype"], c["method"], c["block"], c["topk"], c["ff"], c["fr"], None,
+    _check_against(q, k, c["dtype"], c["method"], c["block"], c["topk"], c["ff"], c["fr"], off_np,
                    c["branching"], ids, trace, tokens=tokens)
 
 
@@ -103,6 +120,7 @@ def attention_cases(draw):
         dtype=draw(st.sampled_from(["fp32", "bf16", "fp16"])),
         duplicates=draw(st.booleans()),
         backward=backward,
+        offset=draw(st.sampled_from(["none", "scalar", "per_batch"])),
     )
 
 
@@ -131,12 +149,13 @@ def test_attention_random_shapes(P, case):
     rng = np.random.default_rng(c["seed"] + 1)
     blocks = -(-c["length"] // c["block"])
     ids = _random_ids(rng, c["batch"], c["tq"], c["kh"], c["topk"], blocks, c["duplicates"])
-    pos = O.query_positions(c["batch"], c["tq"], c["length"], None)
+    off_np, off_gpu = _offsets(c["offset"], c["seed"], c["batch"], c["tq"], c["length"])
+    pos = O.query_positions(c["batch"], c["tq"], c["length"], off_np)
     ref_o, ref_lse = O.sparse_attention(q, k, v, ids, c["block"], positions=pos, causal=c["causal"])
     ids_gpu = torch.from_numpy(ids).cuda()
     if not c["backward"]:
         out, lse = P.sparse_attention_with_lse(to_gpu(q, dt), to_gpu(k, dt), to_gpu(v, dt), ids_gpu,
-                                               c["block"], causal=c["causal"])
+                                               c["block"], causal=c["causal"], query_offset=off_gpu)
         assert excess_error(out.float().cpu().numpy(), ref_o, dt) <= TOL[dt]
         lse = lse.cpu().numpy()
         fin = np.isfinite(ref_lse)
@@ -146,7 +165,7 @@ def test_attention_random_shapes(P, case):
         return
     dout = O.round_storage(rng.standard_normal(ref_o.shape).astype(np.float32), dt)
     qg, kg, vg = (to_gpu(x, dt).requires_grad_(True) for x in (q, k, v))
-    out = P.sparse_attention(qg, kg, vg, ids_gpu, c["block"], causal=c["causal"])
+    out = P.sparse_attention(qg, kg, vg, ids_gpu, c["block"], causal=c["causal"], query_offset=off_gpu)
     out.backward(to_gpu(dout, dt))
     assert excess_error(out.detach().float().cpu().numpy(), ref_o, dt) <= TOL[dt]
     grads = O.sparse_attention_backward(q, k, v, ids, dout, c["block"], positions=pos,
@@ -160,6 +179,20 @@ def test_attention_random_shapes(P, case):
 
 def _bounds(lengths):
     return np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64).tolist()
+
+
+def _doc_offsets(kind, seed, docs):
+    """Packed decode offsets (``validation.py:70-79``): none (each document's last
+    position), one scalar for every document, or one per document; returns the
+    per-document local offsets (None: the default) and the query_offset argument."""
+    if kind == "none":
+        return [None] * len(docs), None
+    rng = np.random.default_rng(seed + 11)
+    if kind == "scalar":
+        off = int(rng.integers(0, min(e - s for s, e in docs)))
+        return [off] * len(docs), off
+    offs = [int(rng.integers(0, e - s)) for s, e in docs]
+    return offs, torch.tensor(offs, dtype=torch.int64, device="cuda")
 
 
 @st.composite
@@ -187,6 +220,7 @@ def packed_selection_cases(draw):
         dtype=draw(st.sampled_from(["fp32", "bf16", "fp16"])),
         schedule=draw(st.sampled_from(["auto", "grouped", "fused"])),
         index_dtype=draw(st.sampled_from([torch.int32, torch.int64])),
+        doc_offsets=draw(st.sampled_from(["none", "scalar", "per_document"])),
     )
 
 
@@ -209,9 +243,10 @@ def test_packed_selection_random_documents(P, case):
     qg, kg = to_gpu(q, dt), to_gpu(k, dt)
     cu = torch.tensor(bounds, dtype=c["index_dtype"], device="cuda")
     kw = dict(force_first=c["ff"], force_recent=c["fr"], branching=b)
-    out = P.select_blocks(qg, kg, c["method"], block, c["topk"], cu_seqlens=cu,
-                          routing_schedule=c["schedule"], **kw).cpu().numpy()
     decode = q.shape[1] != k.shape[1]
+    local, offset = _doc_offsets(c["doc_offsets"] if decode else "none", c["seed"], docs)
+    out = P.select_blocks(qg, kg, c["method"], block, c["topk"], cu_seqlens=cu, query_offset=offset,
+                          routing_schedule=c["schedule"], **kw).cpu().numpy()
     grouped = c["schedule"] == "grouped" or (c["schedule"] == "auto" and c["method"] != "pisa1"
                                              and not decode)
     longest = max(-(-(e - s) // block) for s, e in docs)
@@ -220,14 +255,14 @@ def test_packed_selection_random_documents(P, case):
         rows = slice(d, d + 1) if decode else slice(s, e)
         qd, kd = q[:, rows], k[:, s:e]
         ids, trace = P.selection.select_blocks_traced(
-            qg[:, rows], kg[:, s:e], c["method"], block, c["topk"],
+            qg[:, rows], kg[:, s:e], c["method"], block, c["topk"], query_offset=local[d],
             routing_schedule="grouped" if grouped else "fused", geometry=geometry, **kw)
         ids, trace = ids.cpu().numpy(), trace.cpu().numpy()
         assert np.array_equal(out[:, rows], ids), f"document {d} [{s}, {e})"
         tq = qd.shape[1]
         tokens = np.unique(np.linspace(0, tq - 1, min(tq, 48)).astype(np.int64))
         levels = O.build_pyramid(kd, block, b, None, dt)
-        pos = O.query_positions(1, tq, e - s)
+        pos = O.query_positions(1, tq, e - s, local[d])
         res = parity.selection_parity(qd, kd, ids, trace, tokens, c["method"], block, c["topk"],
                                       c["ff"], c["fr"], b, levels, pos, geometry=geometry)
         assert not res["failures"], f"document {d}: {res['failures'][:3]}"
@@ -252,6 +287,7 @@ def packed_attention_cases(draw):
         dtype=draw(st.sampled_from(["fp32", "bf16", "fp16"])),
         duplicates=draw(st.booleans()),
         backward=draw(st.booleans()) and dim <= 128,
+        doc_offsets=draw(st.sampled_from(["none", "scalar", "per_document"])),
     )
 
 
@@ -271,6 +307,7 @@ def test_packed_attention_random_documents(P, case):
     if c["decode"]:
         q = np.ascontiguousarray(q[:, :len(docs)])
     decode = q.shape[1] != k.shape[1]
+    local, offset = _doc_offsets(c["doc_offsets"] if decode else "none", c["seed"], docs)
     rng = np.random.default_rng(c["seed"] + 3)
     parts = []
     for s, e in docs:
@@ -282,7 +319,7 @@ def test_packed_attention_random_documents(P, case):
     dout = O.round_storage(rng.standard_normal(q.shape).astype(np.float32), dt)
     for d, (s, e) in enumerate(docs):
         rows = slice(d, d + 1) if decode else slice(s, e)
-        pos = O.query_positions(1, rows.stop - rows.start, e - s, None)
+        pos = O.query_positions(1, rows.stop - rows.start, e - s, local[d])
         o_, l_ = O.sparse_attention(q[:, rows], k[:, s:e], v[:, s:e], ids[:, rows], block,
                                     positions=pos, causal=c["causal"])
         ref_o.append(o_)
@@ -296,7 +333,7 @@ def test_packed_attention_random_documents(P, case):
     ids_gpu = torch.from_numpy(ids).cuda()
     qg, kg, vg = (to_gpu(x, dt).requires_grad_(c["backward"]) for x in (q, k, v))
     out, lse = P.sparse_attention_with_lse(qg, kg, vg, ids_gpu, block, cu_seqlens=cu,
-                                           causal=c["causal"])
+                                           causal=c["causal"], query_offset=offset)
     assert excess_error(out.detach().float().cpu().numpy(), ref_o, dt) <= TOL[dt]
     lse = lse.cpu().numpy()
     fin = np.isfinite(ref_l)
@@ -390,6 +427,7 @@ def bsa_cases(draw):
         ff=ff,
         fr=fr,
         dtype=draw(st.sampled_from(["fp32", "bf16", "fp16"])),
+        per_batch=draw(st.booleans()),
     )
 
 
@@ -404,13 +442,15 @@ def test_bsa_random_shapes(P, case):
     dt, n = c["dtype"], c["length"]
     q, k = structured_qkv(c["seed"], c["batch"], n, c["group"] * c["kh"], c["kh"], c["dim"], dt,
                           offset_block=c["block"], value=False)
-    offset = None
+    offset = off_gpu = None
     if c["kind"] == "decode":
         q = np.ascontiguousarray(q[:, n - 1:])
     elif c["kind"] == "suffix" and n > 2:
-        offset = n // 3
+        offset = off_gpu = n // 3
         q = np.ascontiguousarray(q[:, offset:offset + max(1, n // 3)])
-    got = P.bsa_fn(to_gpu(q, dt), to_gpu(k, dt), c["block"], c["topk"], query_offset=offset,
+    if c["per_batch"] and c["kind"] != "prefill":
+        offset, off_gpu = _offsets("per_batch", c["seed"], c["batch"], q.shape[1], n)
+    got = P.bsa_fn(to_gpu(q, dt), to_gpu(k, dt), c["block"], c["topk"], query_offset=off_gpu,
                    force_first=c["ff"], force_recent=c["fr"]).cpu().numpy()
     assert got.shape == (c["batch"], q.shape[1], c["kh"], c["topk"])
     tokens = np.unique(np.linspace(0, q.shape[1] - 1, min(q.shape[1], 128)).astype(np.int64))
