@@ -10,7 +10,7 @@ and the ``PyramidSparseAttention`` layer, computed by hand-written gfx950 HIP ke
 
 from .cache import PyramidCache, TensorCache
 from .layer import (PisaLayerConfig, PyramidSparseAttention, RotaryEmbedding, full_attention,
-                    rotary, token_positions)
+                    rotary, rotary_fn, token_positions)
 from .bsa import bsa_fn
 from .attention import sparse_attention, sparse_attention_with_lse, sparse_attn_fn
 from .pooling import build_pyramid, mean_pool, mean_pooling_fn
@@ -23,5 +23,5 @@ __all__ = [
     "sparse_attention_with_lse", "mean_pool", "mean_pooling_fn", "build_pyramid",
     "routing_geometry", "leaf_scores", "validate_qkv", "query_positions", "packed_queries",
     "sequence_slices", "PyramidCache", "TensorCache", "PisaLayerConfig", "PyramidSparseAttention",
-    "RotaryEmbedding", "rotary", "token_positions", "full_attention", "bsa_fn",
+    "RotaryEmbedding", "rotary", "rotary_fn", "token_positions", "full_attention", "bsa_fn",
 ]

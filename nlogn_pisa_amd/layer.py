@@ -124,6 +124,13 @@ def rotary(x, frequency, positions):
     return _RotaryFn.apply(x, frequency.reshape(-1), positions)
 
 
+def rotary_fn(x, frequency, positions, *, use_triton=True):
+    """``rotary_fn`` (``pisa/pisa/ops/lrpe/rotary.py:9-15``): the HIP rotary for either
+    ``use_triton`` choice (the reference's eager and Triton paths compute the same
+    float32 rotation); a CPU tensor raises."""
+    return rotary(x, frequency.flatten().to(device=x.device, dtype=torch.float32), positions)
+
+
 def rotary_frequency(head_dim, base, fraction):
     """Float32 frequencies base^(-2 i / head_dim) for i < head_dim // 2 * fraction,
     zero after (``lrpe.py:20-28``, type 3).  Both the exponent and the power are

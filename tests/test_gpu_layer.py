@@ -54,6 +54,22 @@ def test_rotary_matches_oracle(P, dtype):
         assert excess_error(got_g, ref_g, dtype) <= 1e-4
 
 
+def test_rotary_fn_is_the_reference_operator(P):
+    """``rotary_fn(x, frequency, positions, use_triton=...)`` (``lrpe/rotary.py:9-15``):
+    any frequency shape and one position row per token (``[T]``) or per batch
+    (``[B, T]``); equal to ``rotary`` and to the oracle."""
+    rng = np.random.default_rng(22)
+    x = O.round_storage(rng.standard_normal((2, 19, 4, 32)).astype(np.float32), "bf16")
+    theta = O.rotary_frequency(32, 10000.0, 1.0).astype(np.float64)   # a float64 table
+    xg = torch.from_numpy(x).to(torch.bfloat16).cuda()
+    steps = torch.arange(19, device="cuda") + 3
+    for use_triton in (True, False):
+        got = P.rotary_fn(xg, torch.from_numpy(theta)[None], steps, use_triton=use_triton)
+        assert torch.equal(got, P.rotary(xg, torch.from_numpy(theta).float().cuda(), steps[None]))
+        ref = O.rotary(x, theta.astype(np.float32), np.broadcast_to(steps.cpu().numpy(), (2, 19)))
+        assert excess_error(got.float().cpu().numpy(), ref, "bf16") <= 1e-4
+
+
 def _layer(P, dtype, method="pisa", seed=0, **kw):
     torch.manual_seed(seed)
     cfg = dict(hidden_size=128, num_attention_heads=8, num_key_value_heads=2, head_dim=32,
