@@ -476,6 +476,31 @@ __host__ __device__ inline size_t leaf_split_lds(int nu, int tile) {
 // Units (16 rows each) per staged batch of query rows at four waves.
 constexpr int kLeafBatchUnits = 4;
 
+// Query rows of head dim 128 (16-bit, one wave per block) reach LDS by LDS DMA
+// (global_load_lds_dwordx4: no staging registers), three batches deep.
+template <typename T, int HD, int BW>
+__host__ __device__ constexpr bool leaf_dma() {
+  return sizeof(T) == 2 && HD == 128 && BW == 1;
+}
+
+// One of the three DMA batch buffers (a distinct LDS object per K).
+template <typename T, int N, int K>
+__device__ __forceinline__ T* leaf_dma_buffer() {
+  __shared__ __attribute__((aligned(16))) T buf[N];
+  return buf;
+}
+
+// 16 bytes per lane from global memory into LDS at lds_base + 16 * lane
+// (global_load_lds_dwordx4; M0 holds the wave's LDS byte address).  Issued as
+// inline assembly so that the compiler's waits do not track it: the kernel waits
+// for it itself (vmcnt, before a barrier).  Memory operations the compiler does
+// not count only make its own counted waits stricter.
+__device__ __forceinline__ void lds_dma16(const void* src, const void* lds_base) {
+  const unsigned lds = (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void*)lds_base;
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(src), "s"(lds) : "memory");
+}
+
 // NTM: key tiles a wave holds (2: up to 32 keys, 4: up to 64); LSE: log-sum-exp
 // support scores, else the moment form (pisa2).  BW: waves per block - with two,
 // the waves of a pair hold keys [0, 64) and [64, 128) of a 128-key block; after
@@ -496,9 +521,10 @@ leaf_split_kernel(LeafArgs a) {
   constexpr int LPT = NU * 16 * vpr / THREADS;  // staging loads per thread and batch
   static_assert(sizeof(T) == 2 && LPT * THREADS == NU * 16 * vpr, "query staging layout");
   constexpr int LDQ = HD + vec;               // LDS query row, 16 bytes of padding
+  constexpr bool DMA = leaf_dma<T, HD, BW>();
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  T* qs = reinterpret_cast<T*>(smem);         // [2][NU * 16][LDQ]
-  int64_t* mq = reinterpret_cast<int64_t*>(smem + (size_t)2 * NU * 16 * LDQ * sizeof(T));
+  T* qs = reinterpret_cast<T*>(smem);         // [2][NU * 16][LDQ] (register staging)
+  int64_t* mq = reinterpret_cast<int64_t*>(smem + (DMA ? 0 : (size_t)2 * NU * 16 * LDQ * sizeof(T)));
   int32_t* mslot = reinterpret_cast<int32_t*>(mq + a.tile);
   int32_t* mmask = mslot + a.tile;
   // partial statistics of the odd waves: [2 batches][SPAN blocks][NU units][16 rows] x 2
@@ -546,7 +572,7 @@ leaf_split_kernel(LeafArgs a) {
     }
     // this wave's block: A fragments of its key rows (zero past the valid rows)
     frag kreg[NTM][DS];
-    {
+    auto load_keys = [&]() __attribute__((always_inline)) {
       const T* kb = static_cast<const T*>(a.src) + b * a.src_batch +
                     (int64_t)(blk0 + c) * a.C * a.src_row + (int64_t)h * HD;
 #pragma unroll
@@ -559,7 +585,8 @@ leaf_split_kernel(LeafArgs a) {
           for (int d = 0; d < DS; ++d) kreg[mt][d] = frag{};
         }
       }
-    }
+    };
+    if constexpr (!DMA) load_keys();  // with LDS DMA: after the first batches' DMA
     const int nunits = (nreq + (16 >> gl) - 1) >> (4 - gl);
     const int nb = (nunits + NU - 1) / NU;
     __syncthreads();  // bookkeeping visible
@@ -767,8 +794,106 @@ leaf_split_kernel(LeafArgs a) {
         if (rows_valid > 0) join_batch(i);
       }
     };
+    // LDS DMA, three buffers: batch b lands in buffer b % 3 as rows of HD
+    // elements whose 16-byte chunk c sits at chunk position c ^ (row & 15)
+    // (conflict-free fragment reads without padding).  Step i issues batch i + 2,
+    // scores batch i from its buffer into registers and stores batch i - 1's
+    // scores first, so the only memory operations issued after batch i + 1's
+    // DMA are those stores and batch i + 2's DMA: vmcnt(LPT) (loads complete in
+    // order) then means batch i + 1 has landed.  The barrier is s_barrier with
+    // compiler memory barriers around it.
+    auto run_dma = [&](auto full_tag) __attribute__((always_inline)) {
+      constexpr int W = SPAN * BW;  // waves per workgroup
+      constexpr int BUF = NU * 16 * HD;
+      T* const b0 = leaf_dma_buffer<T, BUF, 0>();
+      T* const b1 = leaf_dma_buffer<T, BUF, 1>();
+      T* const b2 = leaf_dma_buffer<T, BUF, 2>();
+      const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+      // batch `batch` into `buf`: instruction j of wave w fills 64 chunks (4 rows);
+      // rows that do not exist load request 0's first head (never scored)
+      auto issue = [&](int batch, T* buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < LPT; ++j) {
+          const int blk = j * W + wave_u;
+          const int row = blk * 4 + (lane >> 4);
+          const int chunk = (lane & 15) ^ (row & 15);
+          const int rho = batch * NU * 16 + row;
+          const int rq = rho >> gl, gh = rho & (Gp - 1);
+          const bool ok = rq < nreq && gh < a.G;
+          const T* src = q + mq[ok ? rq : 0] + (int64_t)(ok ? gh : 0) * HD + chunk * vec;
+          lds_dma16(src, buf + blk * 64 * vec);
+        }
+      };
+      auto sync = [&](bool pending) __attribute__((always_inline)) {
+        if (pending) __builtin_amdgcn_s_waitcnt(0x70 | LPT);  // vmcnt(LPT) lgkmcnt(0)
+        else __builtin_amdgcn_s_waitcnt(0x70);                // vmcnt(0) lgkmcnt(0)
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+      };
+      float held[NU];
+      auto score = [&](int batch, const T* buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int p = 0; p < NU; ++p) {
+          const int u = batch * NU + p;
+          if (u >= nunits) break;
+          const T* row = buf + (p * 16 + col) * HD;
+          frag qf[DS];
+#pragma unroll
+          for (int d = 0; d < DS; ++d)
+            qf[d] = *reinterpret_cast<const frag*>(row + ((grp + 4 * d) ^ col) * vec);
+          f4 sv[NTM];
+#pragma unroll
+          for (int mt = 0; mt < NTM; ++mt) {
+            sv[mt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int d = 0; d < DS; ++d) sv[mt] = Op::mma(kreg[mt][d], qf[d], sv[mt]);
+          }
+          const float head = head_of(full_tag, sv);
+          const int rq = (u * 16 + col) >> gl;
+          const bool real = rq < nreq && ((u * 16 + col) & (Gp - 1)) < a.G;
+          held[p] = head_sum(real ? head : 0.f, Gp);
+        }
+      };
+      auto store = [&](int batch) __attribute__((always_inline)) {
+#pragma unroll
+        for (int p = 0; p < NU; ++p) {
+          const int u = batch * NU + p;
+          if (u >= nunits) break;
+          const int rq = (u * 16 + col) >> gl;
+          if (grp == 0 && (col & (Gp - 1)) == 0 && rq < nreq && ((mmask[rq] >> c) & 1))
+            a.scores[mslot[rq] + c] = held[p];
+        }
+      };
+      auto step = [&](int i, const T* cur, T* nxt) __attribute__((always_inline)) {
+        if (i > 0 && rows_valid > 0) store(i - 1);
+        if (i + 2 < nb) issue(i + 2, nxt);
+        if (rows_valid > 0) score(i, cur);
+        sync(i + 2 < nb);
+      };
+      // the first two batches, then the key fragments, all waited for here: the
+      // compiler counts only the key loads, so it must see them complete before
+      // any scoring (a counted wait there would also drain DMAs in flight)
+      issue(0, b0);
+      if (nb > 1) issue(1, b1);
+      load_keys();
+      sync(false);
+      // whole rounds of three steps (the loop is entered and left with only b1's
+      // DMA possibly in flight, so its reads of b0 need no wait), then the last
+      // one or two batches
+      int i = 0;
+      for (; i + 2 < nb; i += 3) {
+        step(i, b0, b2);
+        step(i + 1, b1, b0);
+        step(i + 2, b2, b1);
+      }
+      if (i < nb) step(i, b0, b2);
+      if (i + 1 < nb) step(i + 1, b1, b0);
+      if (rows_valid > 0) store(nb - 1);
+    };
     auto run = [&](auto full_tag) __attribute__((always_inline)) {
-      if constexpr (BW == 2) run1h(full_tag);
+      if constexpr (DMA) run_dma(full_tag);
+      else if constexpr (BW == 2) run1h(full_tag);
       else run1(full_tag);
     };
     // FULL: every key of every block of the span is valid (uniform over the workgroup)
@@ -793,8 +918,10 @@ static void launch_leaf_split(const LeafArgs& a, int cus, hipStream_t stream) {
   constexpr int NU0 = kLeafBatchUnits * W / 4 > 0 ? kLeafBatchUnits * W / 4 : 1;
   constexpr int NU = NU0 * 16 * vpr >= 64 * W ? NU0 : 64 * W / (16 * vpr);
   const void* kernel = (const void*)leaf_split_kernel<T, HD, SPAN, NU, NTM, LSE, BW>;
-  // two waves per block: the odd waves' statistics, two batches of NU units of 16 rows per block
-  const size_t lds = leaf_split_lds<T, HD>(NU, a.tile) + (BW == 2 ? (size_t)2 * SPAN * NU * 16 * sizeof(float2) : 0);
+  // two waves per block: the odd waves' statistics, two batches of NU units of 16 rows per block;
+  // with LDS DMA the three query buffers are static, the dynamic part the bookkeeping only
+  const size_t lds = leaf_dma<T, HD, BW>() ? (size_t)a.tile * 16
+                     : leaf_split_lds<T, HD>(NU, a.tile) + (BW == 2 ? (size_t)2 * SPAN * NU * 16 * sizeof(float2) : 0);
   allow_lds(kernel, lds);
   static int per_cu = 0;  // per instance
   if (per_cu == 0) {
