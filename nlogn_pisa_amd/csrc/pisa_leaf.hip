@@ -476,11 +476,13 @@ __host__ __device__ inline size_t leaf_split_lds(int nu, int tile) {
 // Units (16 rows each) per staged batch of query rows at four waves.
 constexpr int kLeafBatchUnits = 4;
 
-// Query rows of head dim 128 (16-bit, one wave per block) reach LDS by LDS DMA
-// (global_load_lds_dwordx4: no staging registers), three batches deep.
+// Query rows of head dim 128 (16-bit) reach LDS by LDS DMA (global_load_lds_dwordx4:
+// no staging registers), three batches deep with one wave per block, two with two
+// (whose statistics exchange leaves no LDS for a third buffer at three workgroups
+// per CU).
 template <typename T, int HD, int BW>
 __host__ __device__ constexpr bool leaf_dma() {
-  return sizeof(T) == 2 && HD == 128 && BW == 1;
+  return sizeof(T) == 2 && HD == 128;
 }
 
 // One of the three DMA batch buffers (a distinct LDS object per K).
@@ -794,20 +796,23 @@ leaf_split_kernel(LeafArgs a) {
         if (rows_valid > 0) join_batch(i);
       }
     };
-    // LDS DMA, three buffers: batch b lands in buffer b % 3 as rows of HD
+    // LDS DMA, NB buffers: batch b lands in buffer b % NB as rows of HD
     // elements whose 16-byte chunk c sits at chunk position c ^ (row & 15)
-    // (conflict-free fragment reads without padding).  Step i issues batch i + 2,
-    // scores batch i from its buffer into registers and stores batch i - 1's
-    // scores first, so the only memory operations issued after batch i + 1's
-    // DMA are those stores and batch i + 2's DMA: vmcnt(LPT) (loads complete in
-    // order) then means batch i + 1 has landed.  The barrier is s_barrier with
-    // compiler memory barriers around it.
+    // (conflict-free fragment reads without padding).  Step i stores batch
+    // i - 1's scores, issues batch i + NB - 1 and scores batch i from its
+    // buffer into registers, so with three buffers the only memory operations
+    // issued after batch i + 1's DMA are those stores and batch i + 2's DMA:
+    // vmcnt(LPT) (loads complete in order) then means batch i + 1 has landed
+    // (with two, vmcnt(0)).  The barrier is s_barrier with compiler memory
+    // barriers around it.  Two waves per block: the odd waves' statistics of
+    // batch i (exchange buffer i & 1) are joined in step i + 1.
     auto run_dma = [&](auto full_tag) __attribute__((always_inline)) {
       constexpr int W = SPAN * BW;  // waves per workgroup
+      constexpr int NB = BW == 1 ? 3 : 2;
       constexpr int BUF = NU * 16 * HD;
       T* const b0 = leaf_dma_buffer<T, BUF, 0>();
       T* const b1 = leaf_dma_buffer<T, BUF, 1>();
-      T* const b2 = leaf_dma_buffer<T, BUF, 2>();
+      T* const b2 = NB == 3 ? leaf_dma_buffer<T, BUF, 2>() : b0;
       const int wave_u = __builtin_amdgcn_readfirstlane(wave);
       // batch `batch` into `buf`: instruction j of wave w fills 64 chunks (4 rows);
       // rows that do not exist load request 0's first head (never scored)
@@ -849,46 +854,67 @@ leaf_split_kernel(LeafArgs a) {
 #pragma unroll
             for (int d = 0; d < DS; ++d) sv[mt] = Op::mma(kreg[mt][d], qf[d], sv[mt]);
           }
-          const float head = head_of(full_tag, sv);
-          const int rq = (u * 16 + col) >> gl;
-          const bool real = rq < nreq && ((u * 16 + col) & (Gp - 1)) < a.G;
-          held[p] = head_sum(real ? head : 0.f, Gp);
+          if constexpr (BW == 1) {
+            const float head = head_of(full_tag, sv);
+            const int rq = (u * 16 + col) >> gl;
+            const bool real = rq < nreq && ((u * 16 + col) & (Gp - 1)) < a.G;
+            held[p] = head_sum(real ? head : 0.f, Gp);
+          } else {
+            const float2 pr = partial_of(full_tag, sv);
+            if (hf) {
+              if (grp == 0) xch[(((batch & 1) * SPAN + c) * NU + p) * 16 + col] = pr;
+            } else {
+              own[p] = pr;
+            }
+          }
         }
       };
       auto store = [&](int batch) __attribute__((always_inline)) {
+        if constexpr (BW == 2) {
+          join_batch(batch);
+        } else {
 #pragma unroll
-        for (int p = 0; p < NU; ++p) {
-          const int u = batch * NU + p;
-          if (u >= nunits) break;
-          const int rq = (u * 16 + col) >> gl;
-          if (grp == 0 && (col & (Gp - 1)) == 0 && rq < nreq && ((mmask[rq] >> c) & 1))
-            a.scores[mslot[rq] + c] = held[p];
+          for (int p = 0; p < NU; ++p) {
+            const int u = batch * NU + p;
+            if (u >= nunits) break;
+            const int rq = (u * 16 + col) >> gl;
+            if (grp == 0 && (col & (Gp - 1)) == 0 && rq < nreq && ((mmask[rq] >> c) & 1))
+              a.scores[mslot[rq] + c] = held[p];
+          }
         }
       };
       auto step = [&](int i, const T* cur, T* nxt) __attribute__((always_inline)) {
         if (i > 0 && rows_valid > 0) store(i - 1);
-        if (i + 2 < nb) issue(i + 2, nxt);
+        if (i + NB - 1 < nb) issue(i + NB - 1, nxt);
         if (rows_valid > 0) score(i, cur);
-        sync(i + 2 < nb);
+        sync(NB == 3 && i + 2 < nb);
       };
       // the first two batches, then the key fragments, all waited for here: the
       // compiler counts only the key loads, so it must see them complete before
       // any scoring (a counted wait there would also drain DMAs in flight)
       issue(0, b0);
-      if (nb > 1) issue(1, b1);
+      if (NB == 3 && nb > 1) issue(1, b1);
       load_keys();
       sync(false);
-      // whole rounds of three steps (the loop is entered and left with only b1's
-      // DMA possibly in flight, so its reads of b0 need no wait), then the last
-      // one or two batches
       int i = 0;
-      for (; i + 2 < nb; i += 3) {
-        step(i, b0, b2);
-        step(i + 1, b1, b0);
-        step(i + 2, b2, b1);
+      if constexpr (NB == 3) {
+        // whole rounds of three steps (the loop is entered and left with only
+        // b1's DMA possibly in flight, so its reads of b0 need no wait), then
+        // the last one or two batches
+        for (; i + 2 < nb; i += 3) {
+          step(i, b0, b2);
+          step(i + 1, b1, b0);
+          step(i + 2, b2, b1);
+        }
+        if (i < nb) step(i, b0, b2);
+        if (i + 1 < nb) step(i + 1, b1, b0);
+      } else {
+        for (; i + 1 < nb; i += 2) {
+          step(i, b0, b1);
+          step(i + 1, b1, b0);
+        }
+        if (i < nb) step(i, b0, b1);
       }
-      if (i < nb) step(i, b0, b2);
-      if (i + 1 < nb) step(i + 1, b1, b0);
       if (rows_valid > 0) store(nb - 1);
     };
     auto run = [&](auto full_tag) __attribute__((always_inline)) {
@@ -920,8 +946,8 @@ static void launch_leaf_split(const LeafArgs& a, int cus, hipStream_t stream) {
   const void* kernel = (const void*)leaf_split_kernel<T, HD, SPAN, NU, NTM, LSE, BW>;
   // two waves per block: the odd waves' statistics, two batches of NU units of 16 rows per block;
   // with LDS DMA the three query buffers are static, the dynamic part the bookkeeping only
-  const size_t lds = leaf_dma<T, HD, BW>() ? (size_t)a.tile * 16
-                     : leaf_split_lds<T, HD>(NU, a.tile) + (BW == 2 ? (size_t)2 * SPAN * NU * 16 * sizeof(float2) : 0);
+  const size_t xch = BW == 2 ? (size_t)2 * SPAN * NU * 16 * sizeof(float2) : 0;
+  const size_t lds = (leaf_dma<T, HD, BW>() ? (size_t)a.tile * 16 : leaf_split_lds<T, HD>(NU, a.tile)) + xch;
   allow_lds(kernel, lds);
   static int per_cu = 0;  // per instance
   if (per_cu == 0) {
