@@ -78,6 +78,17 @@ void allow_lds(const void* kernel, size_t bytes) {
     (void)hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
 }
 
+// A node's stored value: the exact mean rounded to float32, then to the storage
+// type - two roundings, as the reference's float32 mean cast to its dtype
+// (mean_pooling_torch.py:7-14).  The empty asm keeps the compiler from folding
+// double -> float -> half into one rounding, which differs at fp16 midpoints.
+template <typename T>
+__device__ __forceinline__ T store_mean(double mean) {
+  float f = (float)mean;
+  asm volatile("" : "+v"(f));
+  return from_f<T>(f);
+}
+
 template <typename T, int VEC>
 __global__ void __launch_bounds__(256) pool_kernel(const T* __restrict__ src, int64_t src_batch,
                                                    int64_t src_row, int rows, T* __restrict__ dst,
@@ -118,7 +129,7 @@ __global__ void __launch_bounds__(256) pool_kernel(const T* __restrict__ src, in
     }
     const double inv = (double)count;
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) out[c * VEC + e] = from_f<T>((float)(acc[e] / inv));
+    for (int e = 0; e < VEC; ++e) out[c * VEC + e] = store_mean<T>(acc[e] / inv);
   }
 }
 
@@ -197,7 +208,7 @@ __global__ void __launch_bounds__(256) append_kernel(const T* __restrict__ keys,
       for (int e = 0; e < VEC; ++e) acc[e] += (double)v[e];
     }
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) dst[e] = from_f<T>((float)(acc[e] / (double)n));
+    for (int e = 0; e < VEC; ++e) dst[e] = store_mean<T>(acc[e] / (double)n);
   };
   int count = (tokens + C - 1) / C;
   for (int node = changed; node < count; ++node)

@@ -43,6 +43,25 @@ def structured_qkv(seed, batch, length, qh, kh, dim, dtype="fp32", offset_block=
     return [O.round_storage(x, dtype) for x in arrays]
 
 
+def midpoint_blocks(heads=1, starts=(0.1345, 0.3, 0.7, 1.5, 3.1, 0.07, 12.0, 0.02)):
+    """fp16 keys [1, 128, heads, len(starts)] whose 128-row mean (per column) is an
+    fp16 midpoint plus 2^-30: 126 rows of h (even last mantissa bit), one of
+    2h + 64 ulp(h), one of 2^-23.  Rounded to float32 the mean is the midpoint,
+    which rounds (half to even) to h; rounded straight to fp16 it is h + ulp(h).
+    Returns (keys, h per column)."""
+    cols, hs = [], []
+    for x in starts:
+        h = np.float16(x)
+        if int(h.view(np.uint16)) & 1:
+            h = np.nextafter(h, np.float16(np.inf))
+        ulp = 2.0 ** (np.floor(np.log2(float(h))) - 10)
+        cols.append([float(h)] * 126 + [2 * float(h) + 64 * ulp, 2.0 ** -23])
+        hs.append(float(h))
+    col = np.asarray(cols, dtype=np.float16).T.astype(np.float32)  # [128, columns]
+    keys = np.broadcast_to(col[None, :, None, :], (1, 128, heads, len(starts))).copy()
+    return keys, np.asarray(hs, dtype=np.float32)
+
+
 def to_gpu(x, dtype):
     return torch.from_numpy(np.ascontiguousarray(x)).to(TORCH_DTYPES[dtype]).cuda()
 

@@ -39,6 +39,21 @@ def test_mean_pool_bit_exact(P, dtype, size):
     np.testing.assert_array_equal(out, O.mean_pool(k, size, dtype))
 
 
+def test_mean_pool_rounds_through_float32(P):
+    """fp16 means that are a midpoint plus 2^-30 (``parity.midpoint_blocks``): the
+    pooled node is the float32 mean rounded to fp16 (half to even), as the oracle's,
+    for the pooling kernel and for the cache's append kernel completing the block."""
+    from parity import midpoint_blocks
+    keys, h = midpoint_blocks(heads=2)
+    kg = to_gpu(keys, "fp16")
+    out = P.mean_pool(kg, 128).float().cpu().numpy()
+    np.testing.assert_array_equal(out, O.mean_pool(keys, 128, "fp16"))
+    np.testing.assert_array_equal(out[0, 0, 0], h)
+    cache = P.PyramidCache.from_keys(kg[:, :127], block_size=128)
+    cache.append(kg[:, 127:])
+    np.testing.assert_array_equal(cache.levels[0].float().cpu().numpy(), out)
+
+
 @pytest.mark.parametrize("branching", [2, 4, 8])
 def test_build_pyramid_bit_exact(P, branching):
     print(f"build_pyramid b={branching}", flush=True)

@@ -119,6 +119,19 @@ def test_mean_pool_brute_force(n, size):
                                rtol=1e-6, atol=1e-7)
 
 
+def test_mean_pool_rounds_through_float32():
+    """A node is the float32 mean cast to the storage dtype (two roundings,
+    ``mean_pooling_torch.py:7-14``): on means that are an fp16 midpoint plus 2^-30
+    the oracle returns the even neighbour h, as the reference's eager float32
+    mean does, not h + ulp (one rounding)."""
+    from parity import midpoint_blocks
+    keys, h = midpoint_blocks()
+    out = O.mean_pool(keys, 128, "fp16")
+    np.testing.assert_array_equal(out[0, 0, 0], h)
+    eager = torch.from_numpy(keys).half().float().mean(1).half().float().numpy()
+    np.testing.assert_array_equal(out[0, 0], eager[0])
+
+
 def test_bf16_rounding_matches_torch():
     rng = np.random.default_rng(3)
     x = (rng.standard_normal(100_000) * 10 ** rng.uniform(-6, 6, 100_000)).astype(np.float32)
