@@ -461,3 +461,154 @@ def test_bsa_random_shapes(P, case):
         scores, ids, _ = O.bsa_scores(qs, k, c["block"], pos, c["ff"], c["fr"], dt)
         differ, exempt, failures = adjudicate_flat(got, want, scores, ids)
         assert not failures, f"{len(failures)} of {differ} differing rows, e.g. {failures[:3]}"
+
+
+# ---------------------------------------------------------------- pooling
+
+@st.composite
+def pooling_cases(draw):
+    dtype = draw(st.sampled_from(["fp32", "bf16", "fp16"]))
+    return dict(
+        seed=draw(st.integers(0, 10_000)),
+        batch=draw(st.integers(1, 3)),
+        length=draw(st.one_of(st.integers(1, 64), st.integers(64, 3000))),
+        kh=draw(st.integers(1, 4)),
+        dim=draw(st.sampled_from([8, 16, 24, 64, 96, 128, 256])),
+        size=draw(st.sampled_from([2, 3, 4, 16, 64, 100, 128, 512])),
+        branching=draw(st.sampled_from([2, 3, 4, 8])),
+        dtype=dtype,
+        # magnitudes over 10^(+-spread): float64 sums of fp16 keys are exact at any
+        # magnitude (multiples of 2^-24 below 2^16); bf16 and fp32 keys spread over
+        # twelve decades have no order-independent sum, so they stay within 10^+-1
+        spread=draw(st.sampled_from([1.0, 6.0])) if dtype == "fp16" else 1.0,
+    )
+
+
+@settings(max_examples=40, **SETTINGS)
+@given(case=pooling_cases())
+def test_pooling_random_shapes(P, case):
+    """``mean_pool`` and ``build_pyramid`` (``mean_pooling.py:35-52``) bit-exact against
+    the oracle on random shapes, pool sizes, branching factors and keys spread over
+    many binades (exact sums, one rounding to float32, then the dtype)."""
+    c = case
+    print(f"pooling property {c}", flush=True)
+    rng = np.random.default_rng(c["seed"])
+    shape = (c["batch"], c["length"], c["kh"], c["dim"])
+    raw = rng.standard_normal(shape) * 10.0 ** rng.uniform(-c["spread"], c["spread"], shape)
+    limit = {"fp16": 6.0e4, "bf16": 1e30, "fp32": 1e30}[c["dtype"]]
+    keys = O.round_storage(np.clip(raw, -limit, limit).astype(np.float32), c["dtype"])
+    kg = to_gpu(keys, c["dtype"])
+    got = P.mean_pool(kg, c["size"]).float().cpu().numpy()
+    np.testing.assert_array_equal(got, O.mean_pool(keys, c["size"], c["dtype"]))
+    levels = P.build_pyramid(kg, c["size"], branching=c["branching"])
+    want = O.build_pyramid(keys, c["size"], c["branching"], None, c["dtype"])
+    assert len(levels) == len(want)
+    for level, (mine, ref) in enumerate(zip(levels, want)):
+        np.testing.assert_array_equal(mine.float().cpu().numpy(), ref, err_msg=f"level {level}")
+
+
+# ---------------------------------------------------------------- leaf scoring and packed BSA
+
+@st.composite
+def leaf_cases(draw):
+    block = draw(st.sampled_from([16, 32, 64, 128, 256, 512]))
+    ff = draw(st.booleans())
+    fr = draw(st.integers(1, 2))
+    return dict(
+        seed=draw(st.integers(0, 10_000)),
+        batch=draw(st.integers(1, 2)),
+        length=draw(st.one_of(st.integers(1, 2 * block), st.integers(2 * block, 12 * block))),
+        kh=draw(st.integers(1, 2)),
+        group=draw(st.sampled_from([1, 2, 3, 4, 8, 16])),
+        dim=draw(st.sampled_from([16, 32, 48, 64, 96, 128, 256])),
+        block=block,
+        width=draw(st.integers(1, 48)),
+        topk=draw(st.sampled_from([k for k in (2, 4, 8, 16) if k >= int(ff) + fr])),
+        method=draw(st.sampled_from(["pisa", "pisa2", "pisa1"])),
+        ff=ff,
+        fr=fr,
+        dtype=draw(st.sampled_from(["fp32", "bf16", "fp16"])),
+    )
+
+
+@settings(max_examples=40, **SETTINGS)
+@given(case=leaf_cases())
+def test_leaf_scores_random_shapes(P, case):
+    """``leaf_scores`` (``leaf_triton.py:144-232``): random candidates (padding, blocks
+    past the keys, repeats) on random shapes against the oracle: the same slots
+    scored, scores within 2e-5 (float32 sums in another order)."""
+    c = case
+    print(f"leaf property {c}", flush=True)
+    dt, n = c["dtype"], c["length"]
+    q, k = structured_qkv(c["seed"], c["batch"], n, c["group"] * c["kh"], c["kh"], c["dim"], dt,
+                          offset_block=c["block"], value=False)
+    # the oracle scores every candidate on the CPU: bound its work (q . k products)
+    budget = 3e9 / (c["batch"] * c["kh"] * c["width"] * c["block"] * c["dim"] * c["group"])
+    if n > budget:
+        n = max(1, int(budget))
+        q, k = np.ascontiguousarray(q[:, :n]), np.ascontiguousarray(k[:, :n])
+    rng = np.random.default_rng(c["seed"] + 5)
+    blocks = -(-n // c["block"])
+    cand = rng.integers(-1, blocks + 2, size=(c["batch"], n, c["kh"], c["width"])).astype(np.int32)
+    pos = O.query_positions(c["batch"], n, n)
+    out = P.leaf_scores(to_gpu(q, dt), to_gpu(k, dt), torch.from_numpy(cand).cuda(), c["block"],
+                        c["method"], torch.from_numpy(pos).cuda(), c["topk"], c["ff"],
+                        c["fr"]).cpu().numpy()
+    ref = O.leaf_scores(q, k, cand, c["block"], c["method"], pos, c["topk"], c["ff"], c["fr"],
+                        leaf_means=O.mean_pool(k, c["block"], dt))
+    assert np.array_equal(np.isneginf(out), np.isneginf(ref))
+    fin = np.isfinite(ref)
+    np.testing.assert_allclose(out[fin], ref[fin], rtol=2e-5, atol=2e-5)
+
+
+@st.composite
+def packed_bsa_cases(draw):
+    block = draw(st.sampled_from([4, 8, 16, 32, 64, 128]))
+    docs = draw(st.integers(1, 6))
+    ff = draw(st.booleans())
+    fr = draw(st.integers(1, 3))
+    return dict(
+        seed=draw(st.integers(0, 10_000)),
+        lengths=draw(st.lists(st.one_of(st.integers(1, 2 * block), st.integers(2 * block, 30 * block)),
+                              min_size=docs, max_size=docs)),
+        decode=draw(st.booleans()),
+        kh=draw(st.integers(1, 2)),
+        group=draw(st.sampled_from([1, 2, 4, 16])),
+        dim=draw(st.sampled_from([16, 64, 96, 128])),
+        block=block,
+        topk=draw(st.sampled_from([k for k in (2, 4, 8, 16) if k >= int(ff) + fr])),
+        ff=ff,
+        fr=fr,
+        dtype=draw(st.sampled_from(["fp32", "bf16", "fp16"])),
+    )
+
+
+@settings(max_examples=30, **SETTINGS)
+@given(case=packed_bsa_cases())
+def test_packed_bsa_random_documents(P, case):
+    """``bsa_fn`` with ``cu_seqlens`` (``bsa.py:26-52``): each document's ids equal the
+    oracle's on that document alone (prefill, or one decode query per document)."""
+    from parity import adjudicate_flat
+    c = case
+    print(f"packed bsa property {c}", flush=True)
+    dt, block = c["dtype"], c["block"]
+    bounds = _bounds(c["lengths"])
+    docs = list(zip(bounds[:-1], bounds[1:]))
+    q, k = structured_qkv(c["seed"], 1, bounds[-1], c["group"] * c["kh"], c["kh"], c["dim"], dt,
+                          offset_block=block, value=False)
+    if c["decode"]:
+        q = np.ascontiguousarray(q[:, :len(docs)])
+    decode = q.shape[1] != k.shape[1]
+    cu = torch.tensor(bounds, dtype=torch.int32, device="cuda")
+    got = P.bsa_fn(to_gpu(q, dt), to_gpu(k, dt), block, c["topk"], cu_seqlens=cu,
+                   force_first=c["ff"], force_recent=c["fr"]).cpu().numpy()
+    for d, (s, e) in enumerate(docs):
+        rows = slice(d, d + 1) if decode else slice(s, e)
+        qd, kd, mine = q[:, rows], k[:, s:e], got[:, rows]
+        tokens = np.unique(np.linspace(0, qd.shape[1] - 1, min(qd.shape[1], 64)).astype(np.int64))
+        pos = O.query_positions(1, qd.shape[1], e - s)[:, tokens]
+        want = O.bsa_select(qd[:, tokens], kd, block, c["topk"], pos, c["ff"], c["fr"], dt)
+        if not np.array_equal(mine[:, tokens], want):
+            scores, ids, _ = O.bsa_scores(qd[:, tokens], kd, block, pos, c["ff"], c["fr"], dt)
+            differ, exempt, failures = adjudicate_flat(mine[:, tokens], want, scores, ids)
+            assert not failures, f"document {d}: {len(failures)} of {differ} differing rows"
