@@ -207,9 +207,9 @@ __global__ void __launch_bounds__(256) bsa_kernel(BsaArgs a) {
       const T* mr = means + (int64_t)min(block, a.M - 1) * mrow;
 #pragma unroll
       for (int s = 0; s < DS; ++s) {
-        frag f;
-        load_frags(mr + (inside(s) ? 4 * E * s : 0), *reinterpret_cast<frag(*)[1]>(&f));
-        bf[s] = inside(s) ? f : frag{};
+        frag f[1];
+        load_frags(mr + (inside(s) ? 4 * E * s : 0), f);
+        bf[s] = inside(s) ? f[0] : frag{};
       }
     } else {
       load_row_frags<E>(means + (int64_t)min(block, a.M - 1) * mrow, bf);
