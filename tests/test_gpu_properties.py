@@ -612,3 +612,95 @@ def test_packed_bsa_random_documents(P, case):
             scores, ids, _ = O.bsa_scores(qd[:, tokens], kd, block, pos, c["ff"], c["fr"], dt)
             differ, exempt, failures = adjudicate_flat(mine[:, tokens], want, scores, ids)
             assert not failures, f"document {d}: {len(failures)} of {differ} differing rows"
+
+
+# ---------------------------------------------------------------- the attention layer
+
+@st.composite
+def layer_cases(draw):
+    ff = draw(st.booleans())
+    fr = draw(st.integers(1, 2))
+    packed = draw(st.booleans())
+    docs = draw(st.integers(1, 4)) if packed else 1
+    return dict(
+        seed=draw(st.integers(0, 10_000)),
+        batch=1 if packed else draw(st.integers(1, 2)),
+        lengths=draw(st.lists(st.integers(1, 400), min_size=docs, max_size=docs)),
+        packed=packed,
+        hidden=draw(st.sampled_from([32, 64, 96])),
+        kh=draw(st.integers(1, 2)),
+        group=draw(st.sampled_from([1, 2, 4])),
+        dim=draw(st.sampled_from([16, 32, 64])),
+        block=draw(st.sampled_from([16, 32, 64])),
+        method=draw(st.sampled_from(["pisa", "pisa2", "pisa1", "bsa", "full"])),
+        topk=draw(st.sampled_from([k for k in (4, 8) if k >= int(ff) + fr])),
+        ff=ff,
+        fr=fr,
+        branching=draw(st.sampled_from([2, 4])),
+        rope_fraction=draw(st.sampled_from([0.0, 0.5, 1.0])),
+        rope_theta=draw(st.sampled_from([10000.0, 500000.0])),
+        rope_mode=draw(st.sampled_from(["document", "sequence"])),
+        bias=draw(st.booleans()),
+    )
+
+
+@settings(max_examples=30, **SETTINGS)
+@given(case=layer_cases())
+def test_layer_random_configs(P, case):
+    """``PyramidSparseAttention`` (``pyramid_sparse_attention.py:71-222``) in float32 on
+    random configurations, packed or not: its output equals the float64 composition of
+    the oracle's rotary and attention over the ids the layer's own selection picks
+    (projections, rotary positions per document or per sequence, block-sparse or
+    dense causal attention, output projection), within 1e-4."""
+    c = case
+    print(f"layer property {c}", flush=True)
+    torch.manual_seed(c["seed"])
+    qh, kh, dim = c["group"] * c["kh"], c["kh"], c["dim"]
+    cfg = P.PisaLayerConfig(hidden_size=c["hidden"], num_attention_heads=qh, num_key_value_heads=kh,
+                            head_dim=dim, attention_method=c["method"], block_size=c["block"],
+                            topk=c["topk"], force_first=c["ff"], force_recent=c["fr"],
+                            branching=c["branching"], rope_fraction=c["rope_fraction"],
+                            rope_theta=c["rope_theta"], rope_position_mode=c["rope_mode"],
+                            bias=c["bias"])
+    layer = P.PyramidSparseAttention(cfg).cuda()
+    bounds = _bounds(c["lengths"])
+    n = bounds[-1]
+    x = torch.randn(c["batch"], n, c["hidden"], device="cuda")
+    cu = torch.tensor(bounds, dtype=torch.int32, device="cuda") if c["packed"] else None
+    with torch.no_grad():
+        out, _ = layer(x, cu_seqlens=cu)
+        where = P.token_positions(n, x.device, cu if c["rope_mode"] == "document" else None)
+        q = layer.rope(layer.q_proj(x).view(c["batch"], n, qh, dim), where)
+        k = layer.rope(layer.k_proj(x).view(c["batch"], n, kh, dim), where)
+        if c["method"] == "full":
+            ids = None
+        else:
+            routing = {} if c["method"] == "bsa" else dict(
+                routing_schedule=cfg.prefill_routing, leaf_tile=cfg.leaf_tile, branching=c["branching"])
+            ids = P.select_blocks(q, k, method=c["method"], block_size=c["block"], topk=c["topk"],
+                                  cu_seqlens=cu, force_first=c["ff"], force_recent=c["fr"],
+                                  **routing).cpu().numpy()
+    w = {name: p.detach().double().cpu().numpy() for name, p in layer.named_parameters()}
+    xn = x.double().cpu().numpy()
+    theta = layer.rope.theta.cpu().numpy()
+    pos = where.cpu().numpy()
+
+    def project(name, heads):
+        y = xn @ w[f"{name}.weight"].T + (w[f"{name}.bias"] if c["bias"] else 0.0)
+        return y.reshape(c["batch"], n, heads, dim)
+
+    qn = O.rotary(project("q_proj", qh), theta, pos)
+    kn = O.rotary(project("k_proj", kh), theta, pos)
+    vn = project("v_proj", kh)
+    parts = []
+    for s, e in zip(bounds[:-1], bounds[1:]):
+        docs_ids = (np.broadcast_to(np.arange(-(-(e - s) // c["block"])), (c["batch"], e - s, kh,
+                                                                      -(-(e - s) // c["block"])))
+                    if ids is None else ids[:, s:e])
+        o, _ = O.sparse_attention(qn[:, s:e], kn[:, s:e], vn[:, s:e], np.ascontiguousarray(docs_ids),
+                                  c["block"])
+        parts.append(o)
+    mixed = np.concatenate(parts, 1).reshape(c["batch"], n, qh * dim)
+    ref = mixed @ w["o_proj.weight"].T + (w["o_proj.bias"] if c["bias"] else 0.0)
+    err = np.abs(out.double().cpu().numpy() - ref).max()
+    assert err <= 1e-4 * max(1.0, np.abs(ref).max()), f"max-abs error {err}"
