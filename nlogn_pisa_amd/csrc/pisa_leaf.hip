@@ -460,14 +460,16 @@ leaf_tile_kernel(LeafArgs a) {
 // span (with 128-key blocks, waves 2c and 2c + 1 own its two halves): it holds
 // the block's MFMA A fragments (its key rows) in registers for the whole tile,
 // and every wave scores every unit of the tile against its own keys.  The
-// tile's query rows pass through LDS once, NU units (16 rows each) at a time and
-// double buffered, so LDS serves 16 query rows per unit and block instead of the
-// span's whole key set per unit.  Loads of the next NU units are in flight while
-// the current ones are scored; one workgroup barrier per NU units.
+// tile's query rows pass through LDS once, NU units (16 rows each) at a time, so
+// LDS serves 16 query rows per unit and block instead of the span's whole key set
+// per unit.  Loads of the next NU units (at head dim 128, of the next two) are in
+// flight while the current ones are scored; one workgroup barrier per NU units.
 
-// LDS of a split-span workgroup: two buffers of NU units of padded query rows,
-// then per request its query-row offset, first slot and scoreable mask (and,
-// with two waves per block, the odd waves' row statistics, added by the launch).
+// LDS of a split-span workgroup staging through registers: two buffers of NU
+// units of padded query rows, then per request its query-row offset, first slot
+// and scoreable mask (and, with two waves per block, the odd waves' row
+// statistics, added by the launch).  With LDS DMA the query buffers are static
+// LDS and the dynamic part starts at the bookkeeping.
 template <typename T, int HD>
 __host__ __device__ inline size_t leaf_split_lds(int nu, int tile) {
   return (size_t)2 * nu * 16 * (HD + 16 / sizeof(T)) * sizeof(T) + (size_t)tile * 16;
