@@ -900,9 +900,8 @@ leaf_split_kernel(LeafArgs a) {
       sync(false);
       int i = 0;
       if constexpr (NB == 3) {
-        // whole rounds of three steps (the loop is entered and left with only
-        // b1's DMA possibly in flight, so its reads of b0 need no wait), then
-        // the last one or two batches
+        // whole rounds of three steps (buffers fixed per step), then the last one
+        // or two batches
         for (; i + 2 < nb; i += 3) {
           step(i, b0, b2);
           step(i + 1, b1, b0);
