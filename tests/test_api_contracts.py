@@ -251,3 +251,16 @@ def test_packed_key_layout(bounds, decode):
                 assert g * C <= positions[t] or j * C > p      # causal test in block coordinates
             else:
                 assert g == -1
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """``bench.py --gpus N`` with N above 1 exits with status 2 and says why (one GPU
+    per box; no multi-GPU path), before touching torch or the GPU."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    res = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"],
+                         capture_output=True, text=True, timeout=120)
+    assert res.returncode == 2
+    assert "exactly one GPU" in res.stderr and res.stdout == ""
