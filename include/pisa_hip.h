@@ -63,7 +63,7 @@ typedef struct pisa_pyramid_desc {
 
 typedef struct pisa_select_params {
   int32_t method;        /* enum pisa_method */
-  int32_t block_size;    /* C, power of two >= 16 */
+  int32_t block_size;    /* C, power of two in [16, 65536] */
   int32_t branching;     /* b, power of two in [2, 16]; the reference hard-codes 2 */
   int32_t topk;          /* K in {8, 16, 32, 64} */
   int32_t force_first;   /* bool */

@@ -77,8 +77,9 @@ int plan_select(const pisa_qk_desc* qk, const pisa_select_params* p, SelectPlan&
   if (!p) return fail(PISA_ERR_INVALID, "null parameters");
   if (p->method < PISA_METHOD_PISA1 || p->method > PISA_METHOD_LSE)
     return fail(PISA_ERR_INVALID, "method must be pisa1, pisa2 or pisa");
-  if (!pow2(p->block_size) || p->block_size < 16 || p->block_size > 512)
-    return fail(PISA_ERR_UNSUPPORTED, "GPU routing requires a power-of-two block_size in [16, 512]");
+  if (!pow2(p->block_size) || p->block_size < 16 || p->block_size > kMaxSelectBlock)
+    return fail(PISA_ERR_UNSUPPORTED, "GPU routing requires a power-of-two block_size in [16, %d]",
+                kMaxSelectBlock);
   if (!pow2(p->branching) || p->branching < 2 || p->branching > 16)
     return fail(PISA_ERR_UNSUPPORTED, "branching must be a power of two in [2, 16]");
   if (p->topk < 1 || p->topk > 64) return fail(PISA_ERR_UNSUPPORTED, "topk must be in [1, 64]");
@@ -348,8 +349,8 @@ extern "C" int pisa_leaf_scores(const pisa_qk_desc* qk, const pisa_select_params
   if (width < 1 || width > 512) return fail(PISA_ERR_UNSUPPORTED, "candidate width must be in [1, 512]");
   if (p->method == PISA_METHOD_PISA1 && !leaf_means)
     return fail(PISA_ERR_INVALID, "pisa1 leaf scoring needs the leaf means");
-  if (p->block_size < 1 || p->block_size > 512)
-    return fail(PISA_ERR_UNSUPPORTED, "leaf scoring supports block_size <= 512");
+  if (p->block_size < 1 || p->block_size > kMaxSelectBlock)
+    return fail(PISA_ERR_UNSUPPORTED, "leaf scoring supports block_size <= %d", kMaxSelectBlock);
   if (qk->head_dim % 16 || qk->head_dim > 256)
     return fail(PISA_ERR_UNSUPPORTED, "leaf scoring needs head_dim % 16 == 0 and <= 256");
   const int G = qk->query_heads / qk->key_heads;

@@ -9,6 +9,11 @@
 
 namespace pisa {
 
+// Largest key block of the selection (power-of-two sizes from 16): routing reads
+// a block only through positions and its leaf scores in 128-key chunks, so the
+// bound keeps row and slot arithmetic far inside 32 bits.
+constexpr int kMaxSelectBlock = 1 << 16;
+
 // Records a printf-style message as this thread's last error and returns `code`.
 int fail(int code, const char* fmt, ...);
 // Turns a pending launch error into PISA_ERR_LAUNCH.

@@ -1089,7 +1089,8 @@ int launch_leaf(int dtype, const LeafArgs& a, hipStream_t stream) {
   const int ldk = a.D + 16 / es;
   size_t lds = (size_t)((a.C + 15) / 16 * 16) * ldk * es;
   if (a.D % 16 != 0 || a.D > 256) return fail(PISA_ERR_UNSUPPORTED, "leaf scoring needs head_dim % 16 == 0, <= 256");
-  if (a.C > 512) return fail(PISA_ERR_UNSUPPORTED, "leaf scoring supports block_size <= 512");
+  if (a.C > kMaxSelectBlock)
+    return fail(PISA_ERR_UNSUPPORTED, "leaf scoring supports block_size <= %d", kMaxSelectBlock);
   const bool staged = lds <= (size_t)device_lds_limit();
   if (!staged) lds = 0;
   if (a.span > 1 && a.C > 64 &&

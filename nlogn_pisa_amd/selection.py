@@ -20,6 +20,7 @@ from .pooling import build_pyramid_storage
 from .validation import packed_queries, query_positions, validate_qkv
 
 BACKENDS = ("torch", "triton", "auto", "hip")
+MAX_BLOCK = 1 << 16  # largest key block of the GPU selection (kMaxSelectBlock)
 
 
 def routing_geometry(blocks, topk, branching=2):
@@ -174,8 +175,8 @@ def _select_params(method, block_size, branching, topk, force_first, force_recen
 def _check_gpu_shape(q, k, block_size, topk, branching, force_first, force_recent):
     if q.dtype not in (torch.float16, torch.bfloat16, torch.float32):
         raise ValueError("GPU routing supports FP16, BF16 and FP32")
-    if block_size & (block_size - 1) or not 16 <= block_size <= 512 or not 1 <= topk <= 64:
-        raise ValueError("GPU routing requires power-of-two block_size >= 16 (up to 512) and "
+    if block_size & (block_size - 1) or not 16 <= block_size <= MAX_BLOCK or not 1 <= topk <= 64:
+        raise ValueError(f"GPU routing requires power-of-two block_size >= 16 (up to {MAX_BLOCK}) and "
                          "topk in [1, 64]")
     if branching * topk > 512:
         raise ValueError("branching * topk must not exceed 512")

@@ -79,6 +79,7 @@ CASES = [
     # blocks over 128 keys run as their 128-key halves; head dim 96 (forward on the general
     # kernels, backward on zero-padded 128-wide rows); 32 query heads per kv head
     ("bf16-c256", 1, 700, 1500, 8, 2, 64, 256, 4, "bf16", True, None),
+    ("bf16-c1024", 1, 500, 3000, 8, 2, 64, 1024, 3, "bf16", True, None),
     ("fp32-c512-d32", 1, 300, 2100, 4, 2, 32, 512, 3, "fp32", True, None),
     ("bf16-d96", 1, 400, 400, 8, 2, 96, 64, 4, "bf16", True, None),
     ("bf16-g32", 1, 256, 512, 64, 2, 64, 64, 4, "bf16", True, None),

@@ -60,9 +60,9 @@ def P():
 
 @st.composite
 def selection_cases(draw):
-    block = draw(st.sampled_from([16, 32, 64, 128, 256, 512]))
+    block = draw(st.sampled_from([16, 32, 64, 128, 256, 512, 1024]))
     # up to 400 blocks (routing three or four levels deep at b = 2), the last one ragged
-    blocks = draw(st.one_of(st.integers(1, 40), st.integers(41, 400 if block <= 128 else 100)))
+    blocks = draw(st.one_of(st.integers(1, 40), st.integers(41, 400 if block <= 128 else 60)))
     length = max(1, blocks * block - draw(st.integers(0, block - 1)))
     decode = draw(st.booleans())
     tq = 1 if decode else draw(st.sampled_from([None, max(1, length // 3)]))

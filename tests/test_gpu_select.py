@@ -146,6 +146,9 @@ CONFIGS = [
     # 256 and 32 query heads per kv head (query rows in LDS)
     ("c256", 1, 9000, 8, 2, 64, 256, 4, 8, "pisa", True, 1, "bf16", 0.0, None),
     ("c256-pisa2-fp32", 1, 6000, 4, 2, 32, 256, 2, 8, "pisa2", True, 2, "fp32", 0.0, None),
+    # blocks of 1024 and 2048 keys (top_k_pyramid_triton.py:329 sets no upper bound)
+    ("c1024", 1, 20000, 8, 2, 64, 1024, 2, 8, "pisa", True, 1, "bf16", 0.0, None),
+    ("c2048-pisa2-fp16", 1, 30000, 4, 1, 128, 2048, 4, 4, "pisa2", True, 1, "fp16", 0.0, None),
     ("d96", 1, 4096, 8, 2, 96, 64, 4, 8, "pisa2", True, 2, "bf16", 0.01, None),
     ("d96-lse-fp16", 1, 3000, 4, 1, 96, 32, 2, 8, "pisa", True, 1, "fp16", 0.0, None),
     ("d256", 1, 2048, 8, 2, 256, 64, 2, 8, "pisa", True, 1, "bf16", 0.0, None),
