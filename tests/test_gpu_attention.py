@@ -325,3 +325,39 @@ def test_packed_attention_is_one_launch_sequence(P):
                                                block)
             assert torch.equal(out[:, s:e], o), f"document [{s}, {e})"
             assert torch.equal(lse[:, s:e], l), f"document [{s}, {e})"
+
+
+def test_strided_views_equal_contiguous(P):
+    """Inputs as views, as a model hands them over: q, k, v sliced out of one fused QKV
+    projection (token stride (Hq + 2 Hkv) D, used in place), and k, v sliced out of
+    wider rows (head-dim slices, copied).  Selection ids and O equal those of
+    contiguous copies bit for bit, dQ too (it is reproducible), dK/dV within bf16
+    rounding (their float32 sums follow the tile order)."""
+    print("attention strided views", flush=True)
+    batch, n, qh, kh, dim, block = 2, 700, 8, 2, 64, 64
+    torch.manual_seed(9)
+    fused = torch.randn(batch, n, qh + 2 * kh, dim, device="cuda").to(torch.bfloat16)
+    wide = torch.randn(batch, n, 2 * kh, dim + 32, device="cuda").to(torch.bfloat16)
+    layouts = {
+        "fused": (fused[:, :, :qh], fused[:, :, qh:qh + kh], fused[:, :, qh + kh:]),
+        "wide": (fused[:, :, :qh], wide[:, :, :kh, :dim], wide[:, :, kh:, 16:16 + dim]),
+    }
+    dout = torch.randn(batch, n, qh, dim, device="cuda").to(torch.bfloat16)
+    for name, (q, k, v) in layouts.items():
+        print(f"layout {name}", flush=True)
+        assert not (q.is_contiguous() and k.is_contiguous() and v.is_contiguous())
+        ids = P.select_blocks(q, k, "pisa", block, 6, force_recent=1, branching=4)
+        want = P.select_blocks(q.contiguous(), k.contiguous(), "pisa", block, 6, force_recent=1,
+                               branching=4)
+        assert torch.equal(ids, want), name
+        grads = []
+        for inputs in ((q, k, v), (q.contiguous(), k.contiguous(), v.contiguous())):
+            leaves = [x.detach().clone().requires_grad_(True) if x.is_contiguous() else
+                      x.detach().requires_grad_(True) for x in inputs]
+            out = P.sparse_attention(*leaves, ids, block)
+            out.backward(dout)
+            grads.append((out.detach(), *(x.grad for x in leaves)))
+        (o1, dq1, dk1, dv1), (o2, dq2, dk2, dv2) = grads
+        assert torch.equal(o1, o2) and torch.equal(dq1, dq2), name
+        for g1, g2 in ((dk1, dk2), (dv1, dv2)):
+            assert (g1.float() - g2.float()).abs().max().item() <= 2e-2, name
