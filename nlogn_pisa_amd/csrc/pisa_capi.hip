@@ -87,7 +87,7 @@ int plan_select(const pisa_qk_desc* qk, const pisa_select_params* p, SelectPlan&
   if (p->first_width < 1 || p->first_width > 512 || p->branching * p->topk > 512)
     return fail(PISA_ERR_UNSUPPORTED, "network width above 512");
   const int G = qk->query_heads / qk->key_heads;
-  if (G > 64) return fail(PISA_ERR_UNSUPPORTED, "routing supports up to 64 query heads per KV head");
+  if (G > 128) return fail(PISA_ERR_UNSUPPORTED, "routing supports up to 128 query heads per KV head");
   const int D = qk->head_dim;
   if (D % 16 || D > 256)
     return fail(PISA_ERR_UNSUPPORTED, "routing supports head_dim a multiple of 16 up to 256");

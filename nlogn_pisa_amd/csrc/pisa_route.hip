@@ -150,7 +150,7 @@ __device__ float score_node(const RouteArgs& a, const float (&qr)[MAXG][CH], int
 // float rows [G][D] in LDS (any D = 16 ch <= 256, G <= kLdsHeads), lane `sub`
 // of a 16-lane group holds dimensions [sub ch, sub ch + ch) of a support row
 // and, for the support statistics, heads sub, sub + 16, ... .
-constexpr int kLdsHeads = 64;
+constexpr int kLdsHeads = 128;
 template <typename T>
 __device__ float score_node_lds(const RouteArgs& a, const float* qs, int b, int h, int id,
                                 int level, int sub) {

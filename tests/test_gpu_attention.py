@@ -83,6 +83,7 @@ CASES = [
     ("fp32-c512-d32", 1, 300, 2100, 4, 2, 32, 512, 3, "fp32", True, None),
     ("bf16-d96", 1, 400, 400, 8, 2, 96, 64, 4, "bf16", True, None),
     ("bf16-g32", 1, 256, 512, 64, 2, 64, 64, 4, "bf16", True, None),
+    ("bf16-g128", 1, 200, 400, 128, 1, 64, 64, 4, "bf16", True, None),
     # fp32 rows of 128 with 128-key blocks: the forward's tiles exceed the LDS, so the
     # blocks are attended as 64-key halves (pisa_attention_block_limit)
     ("fp32-d128-c128", 1, 300, 300, 4, 2, 128, 128, 3, "fp32", True, None),

@@ -155,6 +155,9 @@ CONFIGS = [
     ("g32", 1, 2048, 64, 2, 64, 64, 4, 8, "pisa", True, 1, "bf16", 0.0, None),
     ("g32-pisa2-d128", 1, 2048, 64, 2, 128, 32, 2, 16, "pisa2", True, 2, "bf16", 0.0, None),
     ("g24-pisa1", 1, 1500, 48, 2, 64, 64, 2, 8, "pisa1", True, 1, "bf16", 0.0, None),
+    # 128 query heads per kv head (one kv head; the route's query rows in LDS, 128 KB at D 256)
+    ("g128", 1, 1200, 128, 1, 64, 64, 2, 8, "pisa", True, 1, "bf16", 0.0, None),
+    ("g128-pisa2-d256", 1, 700, 128, 1, 256, 32, 2, 8, "pisa2", True, 2, "bf16", 0.0, None),
 ]
 
 
