@@ -187,7 +187,8 @@ size_t pisa_bsa_workspace_size(const pisa_qk_desc* qk, int32_t block_size);
  * :13-84; equations bsa_select, bsa_torch.py:61-106, network streaming_topk
  * :28-58).  block_size <= 128, topk <= 64, head_dim a multiple of 16 up to
  * 256 (zero-padded to 64, 128 or 256 in the products, as bsa_triton.py:108 pads
- * to a power of two), at most 32 query heads per kv head; block_size < 2 topk
+ * to a power of two), at most 128 query heads per kv head (above 32 taken in
+ * chunks of 32 whose head sums are added per tile); block_size < 2 topk
  * widens the comparison tile as the Torch path does. */
 int pisa_bsa_select(const pisa_qk_desc* qk, int32_t block_size, int32_t topk, int32_t force_first,
                     int32_t force_recent, const void* q, const void* k, const int64_t* positions,

@@ -147,7 +147,12 @@ __device__ __forceinline__ int pick4(const int (&a)[4], int t) {
 
 // PAD: head dims below HD (a multiple of 16); the dimensions past a.D are zero
 // in both MFMA operands (their chunks load the row's first chunk, then clear).
-template <typename T, int HD, int GP, int NC, bool PAD>
+// MULTI: more than GP heads per kv head, taken in chunks of GP (at most
+// kBsaChunks): pass 1 leaves each chunk's normalisers in LDS, pass 2 reloads a
+// chunk's query rows per tile and adds its head sums into the tile's scores.
+constexpr int kBsaChunks = 4;
+
+template <typename T, int HD, int GP, int NC, bool PAD, bool MULTI>
 __global__ void __launch_bounds__(256) bsa_kernel(BsaArgs a) {
   constexpr int E = sizeof(T) == 4 ? 1 : (HD % 32 == 0 ? 8 : 4);
   typedef MfmaOp<T, E> Op;
@@ -180,23 +185,30 @@ __global__ void __launch_bounds__(256) bsa_kernel(BsaArgs a) {
   // dimension chunk s of this lane group lies inside the head dim
   auto inside = [&](int s) { return !PAD || 4 * E * s + E * grp < D; };
 
-  // scaled query rows, rounded to the storage dtype (bsa_torch.py:80-81)
+  // scaled query rows of head chunk ch, rounded to the storage dtype (bsa_torch.py:80-81)
   frag qf[RT][DS];
+  auto load_q = [&](int ch) {
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    const int tok = R::token(rt, j), hd = R::head(rt, j);
-    const bool live = tok < 4 && hd < a.G;
-    const T* row = static_cast<const T*>(a.q) + (int64_t)b * a.q_batch +
-                   (int64_t)min(t0 + tok, a.T - 1) * a.q_token +
-                   (int64_t)(h * a.G + min(hd, a.G - 1)) * D + E * grp;
+    for (int rt = 0; rt < RT; ++rt) {
+      const int tok = R::token(rt, j), hd = ch * GP + R::head(rt, j);
+      const bool live = tok < 4 && hd < a.G;
+      const T* row = static_cast<const T*>(a.q) + (int64_t)b * a.q_batch +
+                     (int64_t)min(t0 + tok, a.T - 1) * a.q_token +
+                     (int64_t)(h * a.G + min(hd, a.G - 1)) * D + E * grp;
 #pragma unroll
-    for (int s = 0; s < DS; ++s) {
-      float x[E];
-      load_f<E>(row + (inside(s) ? 4 * E * s : 0), x);
+      for (int s = 0; s < DS; ++s) {
+        float x[E];
+        load_f<E>(row + (inside(s) ? 4 * E * s : 0), x);
 #pragma unroll
-      for (int e = 0; e < E; ++e) Op::set(qf[rt][s], e, live && inside(s) ? x[e] * a.scale : 0.f);
+        for (int e = 0; e < E; ++e) Op::set(qf[rt][s], e, live && inside(s) ? x[e] * a.scale : 0.f);
+      }
     }
-  }
+  };
+  const int nchunk = MULTI ? (a.G + GP - 1) / GP : 1;
+  // normalisers of every (chunk, accumulator row) of this wave: [chunk][rt][grp][i]
+  __shared__ float nrm_lds[MULTI ? 4 * kBsaChunks * RT * 16 : 1];
+  float* my_nrm = nrm_lds + (MULTI ? (threadIdx.x >> 6) * kBsaChunks * RT * 16 : 0);
+  if constexpr (!MULTI) load_q(0);
 
   const T* means = static_cast<const T*>(a.means) + (int64_t)b * a.M * a.Hkv * D + (int64_t)h * D +
                    E * grp;
@@ -224,43 +236,48 @@ __global__ void __launch_bounds__(256) bsa_kernel(BsaArgs a) {
   const int step = W >= 16 ? 16 : W;  // block stride between register columns
 
   // ---- pass 1: log-sum-exp of each (token, head) over the complete blocks
-  float mx[RT][4], sm[RT][4];
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) mx[rt][i] = -INFINITY, sm[rt][i] = 0.f;
+  float nrm[RT][4];
   const int ncol1 = (max_cmp + 15) / 16;
-  for (int col = 0; col < ncol1; ++col) {
-    const int block = 16 * col + j;
-    f4 acc[RT];
-    logits(block, acc);
+  for (int ch = 0; ch < nchunk; ++ch) {
+    if constexpr (MULTI) load_q(ch);
+    float mx[RT][4], sm[RT][4];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mx[rt][i] = -INFINITY, sm[rt][i] = 0.f;
+    for (int col = 0; col < ncol1; ++col) {
+      const int block = 16 * col + j;
+      f4 acc[RT];
+      logits(block, acc);
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int tok = GP == 4 ? grp : R::acc_token(rt, grp);
+          if (block < pick4(cmp, tok)) {
+            const float x = acc[rt][i], d = x - mx[rt][i];
+            const float e = __expf(-fabsf(d));
+            const bool up = d > 0.f;
+            sm[rt][i] = up ? fmaf(sm[rt][i], e, 1.f) : sm[rt][i] + e;
+            mx[rt][i] = up ? x : mx[rt][i];
+          }
+        }
+      }
+    }
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
+        const float m = row_max16(mx[rt][i]);
+        const float part = mx[rt][i] == -INFINITY ? 0.f : sm[rt][i] * __expf(mx[rt][i] - m);
+        const float total = row_sum16(part);
         const int tok = GP == 4 ? grp : R::acc_token(rt, grp);
-        if (block < pick4(cmp, tok)) {
-          const float x = acc[rt][i], d = x - mx[rt][i];
-          const float e = __expf(-fabsf(d));
-          const bool up = d > 0.f;
-          sm[rt][i] = up ? fmaf(sm[rt][i], e, 1.f) : sm[rt][i] + e;
-          mx[rt][i] = up ? x : mx[rt][i];
-        }
+        nrm[rt][i] = pick4(cmp, tok) > 0 ? m + __logf(total) : 0.f;
+        if (MULTI && j == 0) my_nrm[(ch * RT + rt) * 16 + 4 * grp + i] = nrm[rt][i];
       }
     }
   }
-  float nrm[RT][4];
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float m = row_max16(mx[rt][i]);
-      const float part = mx[rt][i] == -INFINITY ? 0.f : sm[rt][i] * __expf(mx[rt][i] - m);
-      const float total = row_sum16(part);
-      const int tok = GP == 4 ? grp : R::acc_token(rt, grp);
-      nrm[rt][i] = pick4(cmp, tok) > 0 ? m + __logf(total) : 0.f;
-    }
-  }
+  if constexpr (MULTI) wave_lds_sync();
 
   // ---- pass 2: scores of each tile, streaming top-K
   const int my_cur = pick4(cur, grp);
@@ -272,9 +289,16 @@ __global__ void __launch_bounds__(256) bsa_kernel(BsaArgs a) {
   for (int tl = 0; tl < ntile; ++tl) {
     float sc[NC];
     int id[NC];
+    for (int ch = 0; ch < nchunk; ++ch) {
+      if constexpr (MULTI) {
+        load_q(ch);
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      {
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) nrm[rt][i] = my_nrm[(ch * RT + rt) * 16 + 4 * grp + i];
+      }
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
         const int block = tl * W + step * c + j;
         f4 acc[RT];
         logits(block, acc);
@@ -290,7 +314,7 @@ __global__ void __launch_bounds__(256) bsa_kernel(BsaArgs a) {
                                 (tc - block >= 0 && tc - block < a.force_recent);
             float p = block < tc ? __expf(acc[rt][i] - nrm[rt][i]) : 0.f;
             p = forced ? 1.f : p;
-            q += R::acc_head(rt, grp, i) < a.G ? p : 0.f;
+            q += ch * GP + R::acc_head(rt, grp, i) < a.G ? p : 0.f;
           }
           if constexpr (GP == 4) {
             part[0] = q;
@@ -300,8 +324,9 @@ __global__ void __launch_bounds__(256) bsa_kernel(BsaArgs a) {
             part[rt / 2] += q;
           }
         }
+        float s;
         if constexpr (GP == 4) {
-          sc[c] = part[0];
+          s = part[0];
         } else {
           // reduce-scatter over the four lane groups: group g ends with token g
           const auto r02 = __builtin_amdgcn_permlane32_swap(__float_as_uint(part[0]),
@@ -312,11 +337,16 @@ __global__ void __launch_bounds__(256) bsa_kernel(BsaArgs a) {
           const float hi = __uint_as_float(r13[0]) + __uint_as_float(r13[1]);
           const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(lo), __float_as_uint(hi),
                                                           false, false);
-          sc[c] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+          s = __uint_as_float(r[0]) + __uint_as_float(r[1]);
         }
-        id[c] = block <= my_cur ? block : -1;
-        sc[c] = block <= my_cur ? sc[c] : 0.f;
+        sc[c] = ch == 0 ? s : sc[c] + s;
       }
+    }
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int block = tl * W + step * c + j;
+      id[c] = block <= my_cur ? block : -1;
+      sc[c] = block <= my_cur ? sc[c] : 0.f;
     }
     if constexpr (NC == 1) {
       switch (a.log_w) {
@@ -345,24 +375,25 @@ __global__ void __launch_bounds__(256) bsa_kernel(BsaArgs a) {
   }
 }
 
-template <typename T, int HD, int GP, bool PAD>
+template <typename T, int HD, int GP, bool PAD, bool MULTI>
 static void launch_bsa_w(const BsaArgs& a, dim3 grid, hipStream_t stream) {
   if (a.W <= 16) {
-    PISA_TIMED("bsa", stream, hipLaunchKernelGGL((bsa_kernel<T, HD, GP, 1, PAD>), grid, dim3(256), 0, stream, a));
+    PISA_TIMED("bsa", stream, hipLaunchKernelGGL((bsa_kernel<T, HD, GP, 1, PAD, MULTI>), grid, dim3(256), 0, stream, a));
   } else if (a.W == 32) {
-    PISA_TIMED("bsa", stream, hipLaunchKernelGGL((bsa_kernel<T, HD, GP, 2, PAD>), grid, dim3(256), 0, stream, a));
+    PISA_TIMED("bsa", stream, hipLaunchKernelGGL((bsa_kernel<T, HD, GP, 2, PAD, MULTI>), grid, dim3(256), 0, stream, a));
   } else if (a.W == 64) {
-    PISA_TIMED("bsa", stream, hipLaunchKernelGGL((bsa_kernel<T, HD, GP, 4, PAD>), grid, dim3(256), 0, stream, a));
+    PISA_TIMED("bsa", stream, hipLaunchKernelGGL((bsa_kernel<T, HD, GP, 4, PAD, MULTI>), grid, dim3(256), 0, stream, a));
   } else {
-    PISA_TIMED("bsa", stream, hipLaunchKernelGGL((bsa_kernel<T, HD, GP, 8, PAD>), grid, dim3(256), 0, stream, a));
+    PISA_TIMED("bsa", stream, hipLaunchKernelGGL((bsa_kernel<T, HD, GP, 8, PAD, MULTI>), grid, dim3(256), 0, stream, a));
   }
 }
 
 template <typename T, int HD, bool PAD>
 static void launch_bsa_g(const BsaArgs& a, dim3 grid, hipStream_t stream) {
-  if (a.G <= 4) launch_bsa_w<T, HD, 4, PAD>(a, grid, stream);
-  else if (a.G <= 16) launch_bsa_w<T, HD, 16, PAD>(a, grid, stream);
-  else launch_bsa_w<T, HD, 32, PAD>(a, grid, stream);
+  if (a.G <= 4) launch_bsa_w<T, HD, 4, PAD, false>(a, grid, stream);
+  else if (a.G <= 16) launch_bsa_w<T, HD, 16, PAD, false>(a, grid, stream);
+  else if (a.G <= 32) launch_bsa_w<T, HD, 32, PAD, false>(a, grid, stream);
+  else launch_bsa_w<T, HD, 32, PAD, true>(a, grid, stream);
 }
 
 // Head dims 16, 32, 64 and 128 run exact; other multiples of 16 up to 256 run
@@ -416,7 +447,9 @@ extern "C" int pisa_bsa_select(const pisa_qk_desc* qk, int32_t block_size, int32
   if (block_size > 128 || topk > 64)
     return fail(PISA_ERR_UNSUPPORTED, "GPU BSA routing requires block_size <= 128 and topk <= 64");
   const int G = qk->query_heads / qk->key_heads;
-  if (G > 32) return fail(PISA_ERR_UNSUPPORTED, "BSA routing supports at most 32 query heads per kv head");
+  if (G > 32 * kBsaChunks)
+    return fail(PISA_ERR_UNSUPPORTED, "BSA routing supports at most %d query heads per kv head",
+                32 * kBsaChunks);
   if (qk->batch == 0 || qk->query_tokens == 0) return PISA_OK;
   if (workspace_bytes < pisa_bsa_workspace_size(qk, block_size) || !workspace)
     return fail(PISA_ERR_WORKSPACE, "BSA workspace too small");

@@ -98,6 +98,12 @@ CASES = [
     ("d80-g32", "fp16", 1, 1200, None, 32, 1, 80, 16, 16, True, 2, None),
     ("d256", "bf16", 2, 3000, None, 16, 2, 256, 64, 16, True, 2, None),
     ("d160-fp32-decode", "fp32", 2, 5000, 1, 8, 2, 160, 64, 8, False, 2, None),
+    # more than 32 query heads per kv head: head chunks of 32 summed per tile
+    ("g64", "bf16", 1, 1500, None, 64, 1, 64, 32, 16, True, 1, None),
+    ("g48-fp32", "fp32", 1, 800, None, 96, 2, 32, 16, 8, False, 2, None),
+    ("g100-fp16-d80", "fp16", 1, 1000, None, 100, 1, 80, 64, 8, True, 2, None),
+    ("g128-decode", "bf16", 2, 6000, 1, 128, 1, 128, 64, 8, True, 2, None),
+    ("g128-d256-suffix", "bf16", 1, 3000, 40, 128, 1, 256, 64, 16, True, 2, 2500),
 ]
 
 
@@ -148,6 +154,9 @@ def test_bsa_errors(P):
         P.bsa_fn(q, k, 8, 2, force_first=True, force_recent=3)
     with pytest.raises(ValueError, match="block_size <= 128"):
         P.bsa_fn(q, k, 256, 8)
+    with pytest.raises(P._lib.PisaError, match="at most 128 query heads"):
+        P.bsa_fn(torch.zeros(1, 64, 129, 32, device="cuda", dtype=torch.bfloat16),
+                 torch.zeros(1, 64, 1, 32, device="cuda", dtype=torch.bfloat16), 16, 4)
     with pytest.raises(P._lib.PisaError, match="multiples of 16"):
         P.bsa_fn(torch.zeros(1, 64, 4, 40, device="cuda", dtype=torch.bfloat16),
                  torch.zeros(1, 64, 2, 40, device="cuda", dtype=torch.bfloat16), 16, 4)
