@@ -443,7 +443,7 @@ def bsa_cases(draw):
     )
 
 
-@settings(max_examples=40, **SETTINGS)
+@settings(max_examples=60, **SETTINGS)
 @given(case=bsa_cases())
 def test_bsa_random_shapes(P, case):
     """``bsa_fn`` (``bsa_torch.py:8-106``) on random supported shapes against the
@@ -716,3 +716,51 @@ def test_layer_random_configs(P, case):
     ref = mixed @ w["o_proj.weight"].T + (w["o_proj.bias"] if c["bias"] else 0.0)
     err = np.abs(out.double().cpu().numpy() - ref).max()
     assert err <= 1e-4 * max(1.0, np.abs(ref).max()), f"max-abs error {err}"
+
+
+# ---------------------------------------------------------------- flat BSA selection
+
+@st.composite
+def bsa_cases(draw):
+    """Shapes ``bsa_fn`` takes on the GPU (block_size <= 128, topk <= 64): any block
+    size, a ragged last block, 1-128 query heads per kv head (above 32 in chunks),
+    head dims 16-256 (padded ones included), decode / suffix / full prefill."""
+    block = draw(st.sampled_from([1, 3, 4, 8, 16, 24, 32, 48, 64, 100, 128]))
+    nblocks = draw(st.integers(1, 120))
+    length = max(1, nblocks * block - draw(st.integers(0, block - 1)))
+    blocks = -(-length // block)
+    ff = draw(st.booleans())
+    fr = draw(st.integers(0, 3))
+    batch = draw(st.integers(1, 2))
+    group = draw(st.sampled_from([1, 2, 3, 4, 8, 16, 24, 32, 48, 64, 100, 128]))
+    kh = draw(st.sampled_from([1, 2]))
+    dim = draw(st.sampled_from([16, 32, 48, 64, 80, 96, 128, 160, 256]))
+    mode = draw(st.sampled_from(["decode", "suffix", "full"]))
+    row = batch * group * kh * dim
+    if mode == "full" and length * row > 1 << 23:
+        mode = "suffix"
+    tq = {"decode": 1, "suffix": max(1, min(length // 3, (1 << 23) // row)), "full": None}[mode]
+    return dict(
+        seed=draw(st.integers(0, 10_000)), batch=batch, length=length, block=block,
+        topk=draw(st.sampled_from([k for k in (1, 2, 4, 8, 16, 32, 64) if k >= min(blocks, int(ff) + fr)])),
+        ff=ff, fr=fr, group=group, kh=kh, dim=dim, tq=tq,
+        dtype=draw(st.sampled_from(["fp32", "bf16", "fp16"])),
+        offset=draw(st.sampled_from(["none", "scalar", "per_batch"])),
+    )
+
+
+@settings(max_examples=60, **SETTINGS)
+@given(case=bsa_cases())
+def test_bsa_random_shapes(P, case):
+    from test_gpu_bsa import _check as check_bsa
+    c = case
+    print(f"bsa property {c}", flush=True)
+    q, k = structured_qkv(c["seed"], c["batch"], c["length"], c["group"] * c["kh"], c["kh"],
+                          c["dim"], c["dtype"], offset_block=c["block"], value=False, tq=c["tq"])
+    tq = q.shape[1] if c["tq"] is not None else None
+    off_np, off_gpu = _offsets(c["offset"], c["seed"], c["batch"], tq, c["length"])
+    got = P.bsa_fn(to_gpu(q, c["dtype"]), to_gpu(k, c["dtype"]), c["block"], c["topk"],
+                   query_offset=off_gpu, force_first=c["ff"], force_recent=c["fr"]).cpu().numpy()
+    assert got.shape == (c["batch"], q.shape[1], c["kh"], c["topk"])
+    tokens = np.unique(np.linspace(0, q.shape[1] - 1, min(q.shape[1], 64)).astype(np.int64))
+    check_bsa(q, k, c["dtype"], c["block"], c["topk"], c["ff"], c["fr"], off_np, got, tokens=tokens)
