@@ -89,10 +89,8 @@ def selection_cases(draw):
     )
 
 
-@settings(max_examples=60, **SETTINGS)
-@given(case=selection_cases())
-def test_selection_random_shapes(P, case):
-    c = case
+def _selection_case(P, c):
+    """One drawn selection case against the oracle on up to 96 spread tokens."""
     print(f"select property {c}", flush=True)
     q, k = structured_qkv(c["seed"], c["batch"], c["length"], c["group"] * c["kh"], c["kh"], c["dim"],
                           c["dtype"], offset_block=c["block"], needles=c["needles"], value=False,
@@ -105,6 +103,45 @@ def test_selection_random_shapes(P, case):
     tokens = np.unique(np.linspace(0, q.shape[1] - 1, min(q.shape[1], 96)).astype(np.int64))
     _check_against(q, k, c["dtype"], c["method"], c["block"], c["topk"], c["ff"], c["fr"], off_np,
                    c["branching"], ids, trace, tokens=tokens)
+
+
+@settings(max_examples=60, **SETTINGS)
+@given(case=selection_cases())
+def test_selection_random_shapes(P, case):
+    _selection_case(P, case)
+
+
+@st.composite
+def wide_group_selection_cases(draw):
+    """33-128 query heads per kv head (the routing keeps a kv head's query rows in
+    LDS, eight head slots per lane); q kept under 2^23 elements."""
+    block = draw(st.sampled_from([16, 32, 64, 128, 256]))
+    blocks = draw(st.one_of(st.integers(1, 40), st.integers(41, 120)))
+    length = max(1, blocks * block - draw(st.integers(0, block - 1)))
+    group = draw(st.sampled_from([33, 48, 64, 100, 128]))
+    dim = draw(st.sampled_from([16, 48, 64, 128, 256]))
+    mode = draw(st.sampled_from(["decode", "suffix", "full"]))
+    if mode == "full" and length * group * dim > 1 << 23:
+        mode = "suffix"
+    tq = {"decode": 1, "suffix": max(1, min(length // 3, (1 << 23) // (group * dim))), "full": None}[mode]
+    ff = draw(st.booleans())
+    fr = draw(st.integers(1, 2))
+    return dict(
+        seed=draw(st.integers(0, 10_000)), batch=1, length=length, tq=tq, kh=1, group=group,
+        dim=dim, block=block, branching=draw(st.sampled_from([2, 4, 8])),
+        topk=draw(st.sampled_from([k for k in (2, 4, 8, 16, 32, 64) if k >= int(ff) + fr])),
+        method=draw(st.sampled_from(["pisa", "pisa2", "pisa1"])), ff=ff, fr=fr,
+        dtype=draw(st.sampled_from(["fp32", "bf16", "fp16"])),
+        schedule=draw(st.sampled_from(["auto", "grouped", "fused"])),
+        needles=draw(st.sampled_from([0.0, 0.05])),
+        offset=draw(st.sampled_from(["none", "scalar"])),
+    )
+
+
+@settings(max_examples=24, **SETTINGS)
+@given(case=wide_group_selection_cases())
+def test_selection_wide_groups(P, case):
+    _selection_case(P, case)
 
 
 @st.composite
