@@ -182,10 +182,8 @@ def _random_ids(rng, batch, tq, kh, topk, blocks, duplicates):
     return ids
 
 
-@settings(max_examples=60, **SETTINGS)
-@given(case=attention_cases())
-def test_attention_random_shapes(P, case):
-    c = case
+def _attention_case(P, c):
+    """One drawn attention case (forward, or forward and backward) against the oracle."""
     print(f"attention property {c}", flush=True)
     dt = c["dtype"]
     q, k, v = structured_qkv(c["seed"], c["batch"], c["length"], c["group"] * c["kh"], c["kh"], c["dim"],
@@ -221,6 +219,28 @@ def test_attention_random_shapes(P, case):
     for name, mine, ref in zip(("dq", "dk", "dv"), (qg.grad, kg.grad, vg.grad), grads):
         err = excess_error(mine.float().cpu().numpy(), ref, dt)
         assert err <= grad_tol(dt, ref), f"{name} excess error {err}"
+
+
+@settings(max_examples=60, **SETTINGS)
+@given(case=attention_cases())
+def test_attention_random_shapes(P, case):
+    _attention_case(P, case)
+
+
+@st.composite
+def wide_group_attention_cases(draw):
+    """24-128 query heads per kv head (a tile request carries the whole group),
+    at most 48 query rows so the float64 oracle stays quick."""
+    c = draw(attention_cases())
+    c.update(group=draw(st.sampled_from([24, 32, 48, 64, 100, 128])), kh=1, batch=1,
+             tq=min(c["tq"], 48))
+    return c
+
+
+@settings(max_examples=24, **SETTINGS)
+@given(case=wide_group_attention_cases())
+def test_attention_wide_groups(P, case):
+    _attention_case(P, case)
 
 
 # ---------------------------------------------------------------- packed documents
