@@ -98,3 +98,44 @@ def test_argument_errors_surface_without_a_gpu(lib):
         _lib.PISA_ERR_INVALID
     desc = _lib.AttnDesc()
     assert lib.pisa_attention_workspace_size(ctypes.byref(desc), 0) == 0
+
+
+def _qk(query_heads=8, key_heads=2, head_dim=64, tokens=1024):
+    qk = _lib.QkDesc(batch=1, query_tokens=tokens, query_heads=query_heads, key_tokens=tokens,
+                     key_heads=key_heads, head_dim=head_dim, dtype=_lib.PISA_BF16)
+    qk.q_stride_token, qk.k_stride_token = query_heads * head_dim, key_heads * head_dim
+    qk.q_stride_batch, qk.k_stride_batch = tokens * qk.q_stride_token, tokens * qk.k_stride_token
+    return qk
+
+
+@pytest.mark.parametrize("shape, params, message", [
+    (dict(query_heads=129, key_heads=1), {}, "up to 128 query heads"),
+    (dict(head_dim=40), {}, "multiple of 16 up to 256"),
+    (dict(head_dim=272), {}, "multiple of 16 up to 256"),
+    ({}, dict(block_size=1 << 17), "block_size in \\[16, 65536\\]"),
+    ({}, dict(block_size=48), "power-of-two block_size"),
+    ({}, dict(topk=65), "topk must be in \\[1, 64\\]"),
+])
+def test_selection_refuses_unsupported_shapes_without_a_gpu(lib, shape, params, message):
+    """The shape checks run on the host before anything reaches the device."""
+    p = _lib.SelectParams(method=2, block_size=64, branching=2, topk=8, force_first=1,
+                          force_recent=2, top=1, first_width=16, schedule=0)
+    for key, value in params.items():
+        setattr(p, key, value)
+    status = lib.pisa_select(ctypes.byref(_qk(**shape)), ctypes.byref(p), None, None, None, None,
+                             0, None, None, None, 0, None)
+    assert status == _lib.PISA_ERR_UNSUPPORTED
+    assert re.search(message, lib.pisa_last_error().decode())
+
+
+@pytest.mark.parametrize("shape, block, topk, message", [
+    (dict(query_heads=129, key_heads=1), 64, 8, "at most 128 query heads"),
+    ({}, 256, 8, "block_size <= 128 and topk <= 64"),
+    ({}, 64, 65, "block_size <= 128 and topk <= 64"),
+])
+def test_bsa_refuses_unsupported_shapes_without_a_gpu(lib, shape, block, topk, message):
+    fake = ctypes.c_void_p(256)   # never dereferenced: the checks return first
+    status = lib.pisa_bsa_select(ctypes.byref(_qk(**shape)), block, topk, 1, 2, fake, fake, fake, 0,
+                                 fake, fake, 1 << 20, None)
+    assert status == _lib.PISA_ERR_UNSUPPORTED
+    assert message in lib.pisa_last_error().decode()
