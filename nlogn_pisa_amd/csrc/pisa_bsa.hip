@@ -161,6 +161,8 @@ __global__ void __launch_bounds__(256) bsa_kernel(BsaArgs a) {
   typedef BsaRows<GP> R;
   constexpr int RT = R::RT;
   constexpr int LOGW = NC == 1 ? 4 : (NC == 2 ? 5 : (NC == 4 ? 6 : 7));  // NC = 1: W <= 16
+  // pisa_bsa_select admits at most 32 * kBsaChunks heads per kv head
+  static_assert(!MULTI || GP == 32, "head chunks are 32 heads wide");
 
   const int lane = threadIdx.x & 63, j = lane & 15, grp = lane >> 4;
   const int unit = (gridDim.x - 1 - blockIdx.x) * 4 + (threadIdx.x >> 6);  // latest tokens first
