@@ -185,8 +185,8 @@ size_t pisa_bsa_workspace_size(const pisa_qk_desc* qk, int32_t block_size);
  * [B, Tq, Hkv, topk] ids in the streaming network's rank order, -1 padded.
  * Replaces select_bsa, ops/flash_sparse_attn/bsa/bsa_triton.py:87-114 (kernel
  * :13-84; equations bsa_select, bsa_torch.py:61-106, network streaming_topk
- * :28-58).  block_size <= 128, topk <= 64, head_dim a multiple of 16 up to
- * 256 (zero-padded to 64, 128 or 256 in the products, as bsa_triton.py:108 pads
+ * :28-58).  block_size <= 128, topk <= 64, head_dim up to 256 (a multiple of 8
+ * for 16-bit inputs; zero-padded to 64, 128 or 256 in the products, as bsa_triton.py:108 pads
  * to a power of two), at most 128 query heads per kv head (above 32 taken in
  * chunks of 32 whose head sums are added per tile); block_size < 2 topk
  * widens the comparison tile as the Torch path does. */

@@ -398,9 +398,10 @@ static void launch_bsa_g(const BsaArgs& a, dim3 grid, hipStream_t stream) {
   else launch_bsa_w<T, HD, 32, PAD, true>(a, grid, stream);
 }
 
-// Head dims 16, 32, 64 and 128 run exact; other multiples of 16 up to 256 run
-// in the next of 64, 128 and 256 with zero dimensions (bsa_triton.py:108 pads to
-// a power of two as well).
+// Head dims 16, 32, 64 and 128 run exact; other head dims up to 256 run in the
+// next of 64, 128 and 256 with zero dimensions (bsa_triton.py:108 pads to a
+// power of two as well): 16-bit rows are read in 8-element chunks (head dims a
+// multiple of 8), fp32 rows element by element (any head dim).
 template <typename T>
 static int launch_bsa(const BsaArgs& a, int D, dim3 grid, hipStream_t stream) {
   switch (D) {
@@ -409,8 +410,9 @@ static int launch_bsa(const BsaArgs& a, int D, dim3 grid, hipStream_t stream) {
     case 64: launch_bsa_g<T, 64, false>(a, grid, stream); break;
     case 128: launch_bsa_g<T, 128, false>(a, grid, stream); break;
     default:
-      if (D % 16 != 0 || D > 256)
-        return fail(PISA_ERR_UNSUPPORTED, "BSA routing supports head dims that are multiples of 16, up to 256");
+      if (D > 256 || D % (sizeof(T) == 4 ? 1 : 8) != 0)
+        return fail(PISA_ERR_UNSUPPORTED,
+                    "BSA routing supports head dims up to 256 (multiples of 8 for 16-bit inputs)");
       if (D < 64) launch_bsa_g<T, 64, true>(a, grid, stream);
       else if (D < 128) launch_bsa_g<T, 128, true>(a, grid, stream);
       else launch_bsa_g<T, 256, true>(a, grid, stream);

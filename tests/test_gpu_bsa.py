@@ -98,6 +98,12 @@ CASES = [
     ("d80-g32", "fp16", 1, 1200, None, 32, 1, 80, 16, 16, True, 2, None),
     ("d256", "bf16", 2, 3000, None, 16, 2, 256, 64, 16, True, 2, None),
     ("d160-fp32-decode", "fp32", 2, 5000, 1, 8, 2, 160, 64, 8, False, 2, None),
+    # head dims off the 16 grid: 16-bit multiples of 8, any fp32 head dim
+    ("d40", "bf16", 1, 1500, None, 8, 2, 40, 32, 8, True, 2, None),
+    ("d24-fp16-g64", "fp16", 1, 900, None, 64, 1, 24, 16, 8, True, 1, None),
+    ("d72-suffix", "bf16", 2, 2000, 50, 16, 2, 72, 64, 16, True, 2, 1500),
+    ("d17-fp32", "fp32", 1, 700, None, 4, 2, 17, 16, 8, False, 2, None),
+    ("d200-fp32-decode", "fp32", 2, 4000, 1, 8, 1, 200, 64, 8, True, 2, None),
     # more than 32 query heads per kv head: head chunks of 32 summed per tile
     ("g64", "bf16", 1, 1500, None, 64, 1, 64, 32, 16, True, 1, None),
     ("g48-fp32", "fp32", 1, 800, None, 96, 2, 32, 16, 8, False, 2, None),
@@ -157,6 +163,9 @@ def test_bsa_errors(P):
     with pytest.raises(P._lib.PisaError, match="at most 128 query heads"):
         P.bsa_fn(torch.zeros(1, 64, 129, 32, device="cuda", dtype=torch.bfloat16),
                  torch.zeros(1, 64, 1, 32, device="cuda", dtype=torch.bfloat16), 16, 4)
-    with pytest.raises(P._lib.PisaError, match="multiples of 16"):
-        P.bsa_fn(torch.zeros(1, 64, 4, 40, device="cuda", dtype=torch.bfloat16),
-                 torch.zeros(1, 64, 2, 40, device="cuda", dtype=torch.bfloat16), 16, 4)
+    with pytest.raises(P._lib.PisaError, match="multiples of 8 for 16-bit"):
+        P.bsa_fn(torch.zeros(1, 64, 4, 36, device="cuda", dtype=torch.bfloat16),
+                 torch.zeros(1, 64, 2, 36, device="cuda", dtype=torch.bfloat16), 16, 4)
+    with pytest.raises(P._lib.PisaError, match="up to 256"):
+        P.bsa_fn(torch.zeros(1, 64, 4, 264, device="cuda", dtype=torch.float32),
+                 torch.zeros(1, 64, 2, 264, device="cuda", dtype=torch.float32), 16, 4)

@@ -781,7 +781,8 @@ def test_layer_random_configs(P, case):
 def bsa_cases(draw):
     """Shapes ``bsa_fn`` takes on the GPU (block_size <= 128, topk <= 64): any block
     size, a ragged last block, 1-128 query heads per kv head (above 32 in chunks),
-    head dims 16-256 (padded ones included), decode / suffix / full prefill."""
+    head dims 16-256 (padded ones included; fp32 also off the 8 grid), decode /
+    suffix / full prefill."""
     block = draw(st.sampled_from([1, 3, 4, 8, 16, 24, 32, 48, 64, 100, 128]))
     nblocks = draw(st.integers(1, 120))
     length = max(1, nblocks * block - draw(st.integers(0, block - 1)))
@@ -791,7 +792,9 @@ def bsa_cases(draw):
     batch = draw(st.integers(1, 2))
     group = draw(st.sampled_from([1, 2, 3, 4, 8, 16, 24, 32, 48, 64, 100, 128]))
     kh = draw(st.sampled_from([1, 2]))
-    dim = draw(st.sampled_from([16, 32, 48, 64, 80, 96, 128, 160, 256]))
+    dtype = draw(st.sampled_from(["fp32", "bf16", "fp16"]))
+    dims = [16, 24, 32, 40, 48, 64, 72, 80, 96, 128, 160, 200, 256]
+    dim = draw(st.sampled_from(dims + ([17, 33, 100, 131] if dtype == "fp32" else [])))
     mode = draw(st.sampled_from(["decode", "suffix", "full"]))
     row = batch * group * kh * dim
     if mode == "full" and length * row > 1 << 23:
@@ -800,8 +803,7 @@ def bsa_cases(draw):
     return dict(
         seed=draw(st.integers(0, 10_000)), batch=batch, length=length, block=block,
         topk=draw(st.sampled_from([k for k in (1, 2, 4, 8, 16, 32, 64) if k >= min(blocks, int(ff) + fr)])),
-        ff=ff, fr=fr, group=group, kh=kh, dim=dim, tq=tq,
-        dtype=draw(st.sampled_from(["fp32", "bf16", "fp16"])),
+        ff=ff, fr=fr, group=group, kh=kh, dim=dim, tq=tq, dtype=dtype,
         offset=draw(st.sampled_from(["none", "scalar", "per_batch"])),
     )
 
