@@ -82,6 +82,16 @@ def _attn_desc(q, k, v, indices, block_size, scale, causal, packed=None):
 
 def _forward(q, k, v, indices, positions, block_size, scale, causal, keep_f32=False,
              packed=None):
+    d, dv_ = q.shape[-1], v.shape[-1]
+    if d % 16 or dv_ % 16:
+        # the kernels take head dims on the 16 grid: zero dimensions change no logit
+        # (the scale stays the caller's) and add value columns that are dropped
+        out, lse, out32 = _forward(_pad_dim(q, -(-d // 16) * 16).contiguous(),
+                                   _pad_dim(k, -(-d // 16) * 16).contiguous(),
+                                   _pad_dim(v, -(-dv_ // 16) * 16).contiguous(), indices,
+                                   positions, block_size, scale, causal, keep_f32, packed)
+        return (out[..., :dv_].contiguous(), lse,
+                None if out32 is None else out32[..., :dv_].contiguous())
     desc = _attn_desc(q, k, v, indices, block_size, scale, causal, packed)
     lib = _lib.library()
     out = torch.empty((*q.shape[:3], v.shape[-1]), device=q.device, dtype=q.dtype)

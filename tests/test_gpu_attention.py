@@ -87,6 +87,12 @@ CASES = [
     # fp32 rows of 128 with 128-key blocks: the forward's tiles exceed the LDS, so the
     # blocks are attended as 64-key halves (pisa_attention_block_limit)
     ("fp32-d128-c128", 1, 300, 300, 4, 2, 128, 128, 3, "fp32", True, None),
+    # head dims off the 16 grid: zero-padded to the next multiple of 16 for the forward
+    # (and to 32/64/128 for the backward), the padding's columns dropped
+    ("bf16-d40", 1, 300, 300, 8, 2, 40, 64, 4, "bf16", True, None),
+    ("fp32-d17-decode", 2, 1, 2000, 8, 2, 17, 64, 6, "fp32", True, None),
+    ("fp16-d72-suffix", 1, 50, 800, 8, 2, 72, 32, 5, "fp16", True, 600),
+    ("bf16-d120-g16", 1, 256, 512, 16, 1, 120, 64, 4, "bf16", True, None),
 ]
 
 
