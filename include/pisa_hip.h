@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PISA_ABI_VERSION 2
+#define PISA_ABI_VERSION 3
 #define PISA_MAX_LEVELS 32
 
 enum pisa_status {
@@ -71,6 +71,9 @@ typedef struct pisa_select_params {
   int32_t top;           /* routing geometry (pisa_routing_geometry) */
   int32_t first_width;
   int32_t schedule;      /* enum pisa_schedule */
+  float scale;           /* leaf score scale; 0: head_dim^-1/2, as the reference.  A caller
+                            that zero-pads rows to a supported head dim passes the scale of
+                            the true head dim (no reference counterpart) */
 } pisa_select_params;
 
 typedef struct pisa_attn_desc {

@@ -59,7 +59,7 @@ class SelectParams(ctypes.Structure):
         ("branching", ctypes.c_int32), ("topk", ctypes.c_int32),
         ("force_first", ctypes.c_int32), ("force_recent", ctypes.c_int32),
         ("top", ctypes.c_int32), ("first_width", ctypes.c_int32),
-        ("schedule", ctypes.c_int32),
+        ("schedule", ctypes.c_int32), ("scale", ctypes.c_float),
     ]
 
 

@@ -84,6 +84,7 @@ int plan_select(const pisa_qk_desc* qk, const pisa_select_params* p, SelectPlan&
     return fail(PISA_ERR_UNSUPPORTED, "branching must be a power of two in [2, 16]");
   if (p->topk < 1 || p->topk > 64) return fail(PISA_ERR_UNSUPPORTED, "topk must be in [1, 64]");
   if (p->force_recent < 1) return fail(PISA_ERR_INVALID, "causal pyramid routing requires force_recent >= 1");
+  if (!(p->scale >= 0.f) || p->scale > 3.0e38f) return fail(PISA_ERR_INVALID, "scale must be finite and >= 0");
   if (p->first_width < 1 || p->first_width > 512 || p->branching * p->topk > 512)
     return fail(PISA_ERR_UNSUPPORTED, "network width above 512");
   const int G = qk->query_heads / qk->key_heads;
@@ -142,9 +143,15 @@ void carve_select(const SelectPlan& pl, Carve& c, SelectBuffers& sb) {
                                     : nullptr;
 }
 
+// The leaf scale: the caller's, else head_dim^-1/2 (top_k_pyramid_torch.py applies
+// dim ** -0.5 to the leaf products).
+float leaf_scale(const pisa_qk_desc* qk, const pisa_select_params* p) {
+  return p && p->scale > 0.f ? p->scale : (float)(1.0 / sqrt((double)qk->head_dim));
+}
+
 LeafArgs leaf_args(const pisa_qk_desc* qk, int method, int block_size, int W, int M0, int G,
                    const void* q, const void* src, int64_t src_batch, int64_t src_row, int src_rows,
-                   int C, const Buckets& b, float* scores) {
+                   int C, const Buckets& b, float* scores, float scale) {
   LeafArgs a;
   a.q = q;
   a.q_batch = qk->q_stride_batch;
@@ -165,7 +172,7 @@ LeafArgs leaf_args(const pisa_qk_desc* qk, int method, int block_size, int W, in
   a.span = 1;
   a.spans = M0;
   a.scoreable = nullptr;
-  a.scale = (float)(1.0 / sqrt((double)qk->head_dim));
+  a.scale = scale;
   a.tile_group = b.tile_group;
   a.tile_req = b.tile_req;
   a.tile_off = b.tile_off;
@@ -240,7 +247,7 @@ extern "C" int pisa_select(const pisa_qk_desc* qk, const pisa_select_params* p, 
   a.force_first = p->force_first ? 1 : 0;
   a.force_recent = p->force_recent;
   a.fused = pl.grouped ? 0 : 1;
-  a.scale = (float)(1.0 / sqrt((double)qk->head_dim));
+  a.scale = leaf_scale(qk, p);
   for (int l = 0; l < PISA_MAX_LEVELS; ++l) {
     a.offsets[l] = l < pyramid->levels ? pyramid->offsets[l] : 0;
     a.lengths[l] = l < pyramid->levels ? pyramid->lengths[l] : 0;
@@ -273,7 +280,7 @@ extern "C" int pisa_select(const pisa_qk_desc* qk, const pisa_select_params* p, 
   LeafRequests req{sb.cand, sb.scoreable, pl.W, qk->key_heads, qk->query_tokens, pl.spans, pl.span};
   LeafArgs la = leaf_args(qk, p->method, p->block_size, pl.W, pl.M0, pl.G, q, k,
                           qk->k_stride_batch, qk->k_stride_token, qk->key_tokens, p->block_size,
-                          sb.buckets, sb.scores);
+                          sb.buckets, sb.scores, leaf_scale(qk, p));
   la.span = pl.span;
   la.spans = pl.spans;
   la.scoreable = sb.scoreable;
@@ -389,7 +396,7 @@ extern "C" int pisa_leaf_scores(const pisa_qk_desc* qk, const pisa_select_params
   LeafArgs la = leaf_args(qk, p->method, p->block_size, width, M0, G, q, pisa1 ? leaf_means : k,
                           pisa1 ? leaf_means_stride_batch : qk->k_stride_batch,
                           pisa1 ? row : qk->k_stride_token, pisa1 ? M0 : qk->key_tokens,
-                          pisa1 ? 1 : p->block_size, b, scores);
+                          pisa1 ? 1 : p->block_size, b, scores, leaf_scale(qk, p));
   const int window = leaf_window(qk);
   const int64_t flat = (int64_t)qk->batch * qk->query_tokens;
   for (int64_t u0 = 0; u0 < flat; u0 += window) {

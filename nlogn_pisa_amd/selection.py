@@ -10,6 +10,8 @@ name runs the HIP library on ROCm tensors; CPU tensors are rejected.
 from __future__ import annotations
 
 import ctypes
+import math
+import types
 
 import torch
 
@@ -118,6 +120,23 @@ def _select_packed(q, k, method, block_size, topk, cu_seqlens, query_offset, for
     return out
 
 
+def _pad_dim(x, width):
+    return torch.nn.functional.pad(x, (0, width - x.shape[-1])).contiguous()
+
+
+def _padded_pyramid(pyramid, width):
+    """A caller's pyramid (cache or levels) with rows zero-padded to ``width``."""
+    if pyramid is None:
+        return None
+    if hasattr(pyramid, "storage"):
+        starts = getattr(pyramid, "starts", None)
+        return types.SimpleNamespace(
+            storage=_pad_dim(pyramid.storage, width), level_sizes=list(pyramid.level_sizes),
+            starts=list(starts if starts is not None else pyramid.offsets.tolist()))
+    levels = list(pyramid.levels if hasattr(pyramid, "levels") else pyramid)
+    return [_pad_dim(x, width) for x in levels]
+
+
 def _pyramid_desc(q, k, block_size, branching, top, pyramid):
     """Packed level storage and its descriptor (levels padded to top + 1)."""
     if pyramid is None:
@@ -162,8 +181,9 @@ def _qk_desc(q, k):
 
 
 def _select_params(method, block_size, branching, topk, force_first, force_recent, top,
-                   first_width, schedule):
+                   first_width, schedule, scale=0.0):
     p = _lib.SelectParams()
+    p.scale = scale
     p.method = _lib.METHODS[method]
     p.block_size, p.branching, p.topk = block_size, branching, topk
     p.force_first, p.force_recent = int(bool(force_first)), force_recent
@@ -194,10 +214,18 @@ def _select_unpacked(q, k, method, block_size, topk, query_offset, force_first, 
     top, first_width = geometry or routing_geometry(blocks, topk, branching)
     q = q.contiguous()
     k = kernel_layout(k)
+    scale = 0.0
+    if q.shape[-1] % 16:
+        # the kernels take head dims on the 16 grid: zero dimensions change no product
+        # or block mean, and the leaf keeps the scale of the true head dim
+        scale = 1.0 / math.sqrt(q.shape[-1])
+        width = -(-q.shape[-1] // 16) * 16
+        q, k = _pad_dim(q, width), _pad_dim(k, width)
+        pyramid = _padded_pyramid(pyramid, width)
     storage, pdesc = _pyramid_desc(q, k, block_size, branching, top, pyramid)
     qk = _qk_desc(q, k)
     params = _select_params(method, block_size, branching, topk, force_first, force_recent, top,
-                            first_width, routing_schedule)
+                            first_width, routing_schedule, scale)
     lib = _lib.library()
     batch, tokens, heads = q.shape[0], q.shape[1], k.shape[2]
     out = torch.empty((batch, tokens, heads, topk), device=q.device, dtype=torch.long)

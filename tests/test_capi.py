@@ -36,7 +36,7 @@ def test_exports_every_declared_function(lib):
     assert set(declared) == set(_lib.EXPORTS)
     for name in declared:
         assert hasattr(lib, name), name
-    assert lib.pisa_abi_version() == 2
+    assert lib.pisa_abi_version() == 3
 
 
 def test_ctypes_structs_match_the_c_layout(tmp_path):

@@ -79,3 +79,22 @@ def test_decode_selection_with_cache(P, method):
         want = P.select_blocks(query, kg[:, :n], method=method, block_size=64, topk=8,
                                query_offset=n - 1)
         assert torch.equal(ids, want), f"decode step {step} ({n} keys)"
+
+
+def test_decode_selection_with_cache_off_grid_head_dim(P):
+    """Head dim 40: the cache's pyramid rows are zero-padded with q and k, and the
+    cached selection equals selection over the concatenated keys."""
+    print("decode selection with cache, head dim 40", flush=True)
+    prefill, steps = 700, 12
+    q, k = structured_qkv(17, 1, prefill + steps, 8, 2, 40, "bf16", needles=0.1, value=False,
+                          tq=steps)
+    qg, kg = to_gpu(q, "bf16"), to_gpu(k, "bf16")
+    cache = P.PyramidCache.from_keys(kg[:, :prefill], block_size=64)
+    for step in range(steps):
+        n = prefill + step + 1
+        cache.append(kg[:, n - 1:n])
+        query = qg[:, step:step + 1]
+        ids = P.select_blocks(query, cache.keys, block_size=64, topk=8, query_offset=n - 1,
+                              pyramid=cache)
+        want = P.select_blocks(query, kg[:, :n], block_size=64, topk=8, query_offset=n - 1)
+        assert torch.equal(ids, want), f"decode step {step} ({n} keys)"

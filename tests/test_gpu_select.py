@@ -158,6 +158,12 @@ CONFIGS = [
     # 128 query heads per kv head (one kv head; the route's query rows in LDS, 128 KB at D 256)
     ("g128", 1, 1200, 128, 1, 64, 64, 2, 8, "pisa", True, 1, "bf16", 0.0, None),
     ("g128-pisa2-d256", 1, 700, 128, 1, 256, 32, 2, 8, "pisa2", True, 2, "bf16", 0.0, None),
+    # head dims off the 16 grid: rows zero-padded to the next multiple of 16, the leaf
+    # scaled by the true head dim
+    ("d40", 1, 3000, 8, 2, 40, 64, 4, 8, "pisa", True, 1, "bf16", 0.0, None),
+    ("d72-pisa2-fp16", 1, 2500, 8, 2, 72, 32, 2, 16, "pisa2", True, 2, "fp16", 0.0, None),
+    ("d24-fp32-pisa1", 1, 2000, 4, 1, 24, 64, 4, 8, "pisa1", True, 1, "fp32", 0.0, None),
+    ("d100-decode", 2, 20000, 16, 2, 100, 64, 4, 16, "pisa", True, 1, "bf16", 0.01, 1),
 ]
 
 
