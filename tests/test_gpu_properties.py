@@ -75,7 +75,8 @@ def selection_cases(draw):
         tq=tq,
         kh=draw(st.integers(1, 2)),
         group=draw(st.sampled_from([1, 2, 3, 4, 8, 16, 32])),
-        dim=draw(st.sampled_from([16, 32, 48, 64, 96, 128, 256])),
+        # off the 16 grid too: rows zero-padded by select_blocks
+        dim=draw(st.sampled_from([16, 24, 32, 40, 48, 64, 72, 96, 128, 256])),
         block=block,
         branching=draw(st.sampled_from([2, 4, 8])),
         topk=draw(st.sampled_from([k for k in (2, 4, 8, 16, 32, 64) if k >= int(ff) + fr])),
