@@ -80,26 +80,27 @@ def _layer(P, dtype, method="pisa", seed=0, **kw):
     return layer
 
 
-def test_layer_prefill_matches_oracle(P):
-    print("layer prefill fp32", flush=True)
-    layer = _layer(P, "fp32")
+@pytest.mark.parametrize("hd", [32, 40])   # 40: rows zero-padded by selection and attention
+def test_layer_prefill_matches_oracle(P, hd):
+    print(f"layer prefill fp32 head dim {hd}", flush=True)
+    layer = _layer(P, "fp32", head_dim=hd)
     torch.manual_seed(1)
     x = torch.randn(1, 300, 128, device="cuda")
     out, _ = layer(x)
     c = layer.config
     with torch.no_grad():
         pos = P.token_positions(300, x.device)
-        q = layer.rope(layer.q_proj(x).view(1, 300, 8, 32), pos)
-        k = layer.rope(layer.k_proj(x).view(1, 300, 2, 32), pos)
+        q = layer.rope(layer.q_proj(x).view(1, 300, 8, hd), pos)
+        k = layer.rope(layer.k_proj(x).view(1, 300, 2, hd), pos)
         ids = P.select_blocks(q, k, method=c.attention_method, block_size=c.block_size, topk=c.topk,
                               force_recent=c.force_recent, branching=c.branching)
     w = {n: p.detach().double().cpu().numpy() for n, p in layer.named_parameters()}
     xn = x.double().cpu().numpy()
-    qn = O.rotary((xn @ w["q_proj.weight"].T).reshape(1, 300, 8, 32), layer.rope.theta.cpu().numpy(),
+    qn = O.rotary((xn @ w["q_proj.weight"].T).reshape(1, 300, 8, hd), layer.rope.theta.cpu().numpy(),
                   np.arange(300)[None])
-    kn = O.rotary((xn @ w["k_proj.weight"].T).reshape(1, 300, 2, 32), layer.rope.theta.cpu().numpy(),
+    kn = O.rotary((xn @ w["k_proj.weight"].T).reshape(1, 300, 2, hd), layer.rope.theta.cpu().numpy(),
                   np.arange(300)[None])
-    vn = (xn @ w["v_proj.weight"].T).reshape(1, 300, 2, 32)
+    vn = (xn @ w["v_proj.weight"].T).reshape(1, 300, 2, hd)
     o, _ = O.sparse_attention(qn, kn, vn, ids.cpu().numpy(), c.block_size)
     ref = o.reshape(1, 300, -1) @ w["o_proj.weight"].T
     assert np.abs(out.detach().double().cpu().numpy() - ref).max() <= 1e-4
